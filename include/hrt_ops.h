@@ -1,0 +1,169 @@
+/*
+ * Argument blocks of the operator kernels registered in the hrt runtime (see hrt.h).
+ *
+ * `hrt_dispatch(hrt_kernel_index(name), &args, sizeof(args), 0, 0, 0)` queues kernel `name` with one
+ * of the blocks below.  They play the role of the reference's push-constant structs (MmPush
+ * `csrc/ops_mm.cpp:19-29`, AttnPush/CoopPush `csrc/ops_attn.cpp:25-42`, SoftmaxPush
+ * `csrc/ops_rows.cpp:37-41`, LnPush `csrc/ops_rows.cpp:103-109`, Dq8Push `csrc/ops_quant.cpp:15-19`,
+ * EwPush `csrc/ops_ew.cpp:22-28`) with two deliberate differences: sizes, strides and offsets are 64-bit
+ * (no 2^32 element limit on a 288 GB device), and each kernel picks its own tiling and grid.
+ *
+ * All addresses are device addresses inside live hrt blocks; the runtime checks every operand's byte
+ * extent against its allocator before launching and rejects out-of-range operands.  Strides are in
+ * elements and must be non-negative.  Arithmetic is fp32 for every dtype; bf16 and f16 results are
+ * rounded once, to nearest-even (bf16: NaN -> 0x7FC0), as `vkrt/shaders/types.glsl:18-50`.
+ */
+#ifndef HRT_OPS_H_
+#define HRT_OPS_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes.  0..2 are the float kinds used in kernel names (f32/bf16/f16, the reference's
+ * KIND numbering, vkrt/shaders/types.glsl:1); 3..6 are raw element sizes for same-type copies/fills. */
+enum {
+  HRT_F32 = 0,
+  HRT_BF16 = 1,
+  HRT_F16 = 2,
+  HRT_RAW8 = 3,
+  HRT_RAW16 = 4,
+  HRT_RAW32 = 5,
+  HRT_RAW64 = 6
+};
+
+#define HRT_MAX_DIMS 8
+
+/* "add_f32" — raw-grid smoke kernel, 256 threads per workgroup: c[i] = a[i] + b[i] for i < n.
+ * Same argument block and meaning as the reference's runtime smoke kernel (vkrt/tests/basic.rs:53-76). */
+typedef struct hrt_add_f32_args {
+  uint64_t a, b, c, n;
+} hrt_add_f32_args;
+
+/* "ew_copy" — dst[i] = convert(src[i]) over an ndim-dimensional index space (ndim <= 8, sizes shared,
+ * separate strides).  Float kinds convert among each other; raw kinds require dst_dtype == src_dtype.
+ * Replaces the strided copy/cast `ew_copy` (csrc/ops_ew.cpp:495-506). */
+typedef struct hrt_copy_args {
+  uint64_t dst, src;
+  int32_t ndim, dst_dtype, src_dtype, pad;
+  int64_t sizes[HRT_MAX_DIMS];
+  int64_t dst_strides[HRT_MAX_DIMS];
+  int64_t src_strides[HRT_MAX_DIMS];
+} hrt_copy_args;
+
+/* "ew_fill" — dst[i] = value over a strided index space; value_bits holds the element's bit pattern in
+ * its low bytes (dtype selects the element size).  Replaces `try_fill` (csrc/ops_ew.cpp:382-392). */
+typedef struct hrt_fill_args {
+  uint64_t dst, value_bits;
+  int32_t ndim, dtype, pad0, pad1;
+  int64_t sizes[HRT_MAX_DIMS];
+  int64_t strides[HRT_MAX_DIMS];
+} hrt_fill_args;
+
+/* "mm_{f32,bf16,f16}" (portable FMA kernel) and "mm_mfma_{bf16,f16}" (gfx950 matrix cores):
+ *   c[b, m, n] = alpha * sum_k a[b, m, k] * b[b, k, n] + beta * bias[b, m, n]     (bias only if has_bias)
+ * a, b, bias: any non-negative strides (transposed / sliced views are read in place; bias broadcasts
+ * with stride 0); c: written with strides c_s*.  fp32 accumulation, one rounding at the store.
+ * Same meaning as MmPush (csrc/ops_mm.cpp:19-29) and the epilogue of vkrt/shaders/mm_coop.comp.in:195-208. */
+typedef struct hrt_mm_args {
+  uint64_t a, b, c, bias;
+  int64_t M, N, K, batch;
+  int64_t a_sb, a_sm, a_sk;
+  int64_t b_sb, b_sk, b_sn;
+  int64_t c_sb, c_sm, c_sn;
+  int64_t bias_sb, bias_sm, bias_sn;
+  float alpha, beta;
+  uint32_t has_bias, flags;
+} hrt_mm_args;
+
+/* "mm_dq8_{bf16,f16}" — fused int8 weight-only linear (no reference counterpart; composes
+ * csrc/ops_quant.cpp:34-59 with csrc/ops_mm.cpp:61-175):
+ *   y[m, n] = alpha * sum_k x[m, k] * deq(q)[n, k] + beta * bias[n]
+ *   deq(q)[n, k] = round_dtype(float(q[n, k]) * float(scale[n, k / 64]))      (bit-exact dequant value)
+ * x: [M, K] with strides (x_sm, x_sk); q: int8 [N, K] contiguous; scale: bf16 [N, nblocks] contiguous,
+ * nblocks = ceil(K / 64); bias: [N] (if has_bias); y: [M, N] contiguous, dtype of x. */
+typedef struct hrt_mm_dq8_args {
+  uint64_t x, q, scale, bias, y;
+  int64_t M, N, K, nblocks;
+  int64_t x_sm, x_sk;
+  float alpha, beta;
+  uint32_t has_bias, flags;
+} hrt_mm_dq8_args;
+
+/* Fused scaled-dot-product attention, non-causal, no mask, D <= 128 (vkrt/shaders/attn.comp.in:1-14,
+ * attn_coop.comp.in:1-9).  q: [B, H, Sq, D], k, v: [B, H, Sk, D] views given by (batch, head, seq)
+ * element strides, d contiguous.  Outputs o / o32 / dq / dk / dv are [B, S, H, D]-contiguous (PyTorch
+ * returns them permuted to [B, H, S, D], csrc/ops_attn.cpp:159-162); lse and delta are fp32 [B, H, Sq].
+ *
+ *  "attn_fwd_{dt}":   o = softmax(scale * q k^T) v (rounded to dt), lse = rowwise logsumexp (fp32),
+ *                     o32 = the unrounded fp32 o when o32 != 0.
+ *  "attn_delta_{dt}": delta[b, h, i] = sum_d O[b, i, h, d] * dout[b, h, i, d], with O read from o
+ *                     (fp32 when flags & HRT_ATTN_O_F32, else dt), as attn.comp.in:210-240.
+ *  "attn_dkdv_{dt}":  dk = scale * dS^T q, dv = P^T dout     (P = exp(scale * q k^T - lse),
+ *  "attn_dq_{dt}":    dq = scale * dS k                        dS = P * (dout v^T - delta))
+ * For bf16/f16 the matrix-core kernels round P and dS to dt before the second product, as
+ * attn_coop.comp.in:182-183, 235-236, 283-284; the f32 kernels keep everything fp32. */
+#define HRT_ATTN_O_F32 1u
+typedef struct hrt_attn_args {
+  uint64_t q, k, v;
+  uint64_t o, lse, o32;
+  uint64_t dout, delta;
+  uint64_t dq, dk, dv;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t do_sb, do_sh, do_ss;
+  int32_t B, H, Sq, Sk, D;
+  float scale;
+  uint32_t flags, pad;
+} hrt_attn_args;
+
+/* Row softmax over R of a contiguous [outer, R, inner] tensor (vkrt/shaders/softmax.comp.in:27-50):
+ *  "softmax_fwd_{dt}": y = exp(x - max) / sum(exp(x - max)); with safe != 0 a row whose entries are all
+ *                      -inf gives 0 (_safe_softmax).
+ *  "softmax_bwd_{dt}": dx = y * (g - sum(g * y)). */
+typedef struct hrt_softmax_args {
+  uint64_t x, y, g, dx;
+  int64_t outer, R, inner;
+  uint32_t safe, pad;
+} hrt_softmax_args;
+
+/* layer_norm over the last D elements of contiguous [rows, D] (vkrt/shaders/ln.comp.in:1-84):
+ *  "ln_fwd_{dt}":   mean = sum(x)/D, var = sum((x-mean)^2)/D (two-pass), rstd = 1/sqrt(var+eps),
+ *                   y = (x-mean)*rstd*w + b   (w, b optional = 0); mean, rstd fp32 [rows].
+ *  "ln_bwd_{dt}":   dx = rstd*(gw - mean(gw) - xhat*mean(gw*xhat)), gw = g*w, xhat = (x-mean)*rstd
+ *                   (dx optional); when ws != 0 also writes per-chunk partial sums of g*xhat and g to
+ *                   ws = fp32 [hrt_ln_chunks(rows)][2][D].
+ *  "ln_wgrad_{dt}": dw[d] = sum over chunks of ws[c][0][d], db[d] = sum of ws[c][1][d] (each optional). */
+typedef struct hrt_ln_args {
+  uint64_t x, y, mean, rstd, w, b;
+  uint64_t g, dx, dw, db, ws;
+  int64_t rows, D;
+  float eps;
+  uint32_t pad;
+} hrt_ln_args;
+
+/* Row chunking of the layer_norm weight-gradient partial sums: 4 rows per chunk (one workgroup of four
+ * wavefronts, one row each). */
+static inline int64_t hrt_ln_rows_per_chunk(int64_t rows) { return rows > 0 ? 4 : 1; }
+static inline int64_t hrt_ln_chunks(int64_t rows) {
+  int64_t r = hrt_ln_rows_per_chunk(rows);
+  return (rows + r - 1) / r;
+}
+
+/* "dq8_{f32,bf16,f16}" — weight-only int8 dequant (vkrt/shaders/dq8.comp.in:39-62, closed form
+ * torch_vulkan/__init__.py:203-205): out[r, c] = round_dt(float(q[r, c]) * float(scale[r, c / 64])).
+ * q: int8 [rows, cols] contiguous; scale: bf16 [rows, nblocks] contiguous, nblocks = ceil(cols / 64);
+ * out: [rows, cols] contiguous.  Bit-exact: the fp32 product is exact, the only rounding is the store. */
+typedef struct hrt_dq8_args {
+  uint64_t q, scale, out;
+  int64_t rows, cols, nblocks;
+} hrt_dq8_args;
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HRT_OPS_H_ */

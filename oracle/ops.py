@@ -1,0 +1,232 @@
+"""numpy restatements of the reference's hot-path algorithms (test infrastructure only; see __init__).
+
+Every function takes and returns numpy arrays.  Floating-point arithmetic is float64 (the reference's
+own tests compare against CPU float64); the bit-exact parts (rounding, dequant) reproduce the exact
+float32 bit patterns the reference kernels store.
+"""
+
+import numpy as np
+
+# ---------------------------------------------------------------------------------------------------------
+# Rounding contract — vkrt/shaders/types.glsl:18-50
+# ---------------------------------------------------------------------------------------------------------
+
+
+def round_bf16(x):
+    """float32 -> bf16 bit pattern (uint16): round to nearest even, every NaN -> 0x7FC0.
+    types.glsl:45-50 (f2bf)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, 0x7FC0, r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(bits):
+    """bf16 bit pattern -> float32 (exact).  types.glsl:44 (bf2f)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_f16(x):
+    """float32 -> IEEE half bit pattern (uint16), round to nearest even including subnormals, overflow
+    -> inf, NaN -> quiet NaN with the top payload bits.  types.glsl:18-41 (f2h)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.int64)
+    sign = (u >> 16) & 0x8000
+    e = (u >> 23) & 0xFF
+    m = u & 0x7FFFFF
+    out = np.zeros(u.shape, dtype=np.int64)
+    # inf / NaN
+    special = e == 0xFF
+    out = np.where(special, sign | 0x7C00 | np.where(m != 0, 0x200 | (m >> 13), 0), out)
+    ne = e - 127 + 15
+    over = (~special) & (ne >= 31)
+    out = np.where(over, sign | 0x7C00, out)
+    # subnormal or zero result
+    sub = (~special) & (ne <= 0)
+    tiny = sub & (ne < -10)
+    out = np.where(tiny, sign, out)
+    subn = sub & ~tiny
+    mm = m | 0x800000
+    shift = np.clip(14 - ne, 1, 63)
+    hm = mm >> shift
+    rem = mm & ((np.int64(1) << shift) - 1)
+    half = np.int64(1) << (shift - 1)
+    up = (rem > half) | ((rem == half) & ((hm & 1) != 0))
+    out = np.where(subn, sign | (hm + up.astype(np.int64)), out)
+    # normal result (a carry out of the mantissa propagates into the exponent, as intended)
+    norm = (~special) & (~over) & (~sub)
+    hm = m >> 13
+    rem = m & 0x1FFF
+    h = sign | (ne << 10) | hm
+    up = (rem > 0x1000) | ((rem == 0x1000) & ((hm & 1) != 0))
+    out = np.where(norm, h + up.astype(np.int64), out)
+    return out.astype(np.uint16)
+
+
+def f16_to_f32(bits):
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def _round_to(x32, kind):
+    """Store rounding of a float32 array for kind "f32" / "bf16" / "f16": returns the stored value as
+    float32 (and the raw bits for the 16-bit kinds)."""
+    if kind == "f32":
+        return x32.astype(np.float32), x32.astype(np.float32).view(np.uint32)
+    if kind == "bf16":
+        b = round_bf16(x32)
+        return bf16_to_f32(b), b
+    if kind == "f16":
+        b = round_f16(x32)
+        return f16_to_f32(b), b
+    raise ValueError(kind)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# int8 weight-only dequant — vkrt/shaders/dq8.comp.in:39-62, closed form torch_vulkan/__init__.py:203-205
+# ---------------------------------------------------------------------------------------------------------
+
+
+def dequant_int8(q, scale_bits, kind):
+    """out[r, c] = round_kind(float32(q[r, c]) * float32(scale[r, c // 64])).
+
+    q: int8 [rows, cols]; scale_bits: uint16 bf16 patterns [rows, ceil(cols / 64)].  The float32 product
+    of an 8-bit integer and an 8-bit-significand bf16 is exact, so the only rounding is the store.
+    Returns the stored bit patterns (uint32 for f32, uint16 for bf16/f16)."""
+    q = np.asarray(q, dtype=np.int8)
+    rows, cols = q.shape
+    nb = (cols + 63) // 64
+    s = bf16_to_f32(np.asarray(scale_bits, dtype=np.uint16).reshape(rows, nb))
+    col_block = np.arange(cols) // 64
+    prod = q.astype(np.float32) * s[:, col_block]  # exact in float32
+    return _round_to(prod, kind)[1]
+
+
+# ---------------------------------------------------------------------------------------------------------
+# GEMM — epilogue vkrt/shaders/mm.comp.in:142-153 / mm_coop.comp.in:195-208, bias broadcast ops_mm.cpp:80-99
+# ---------------------------------------------------------------------------------------------------------
+
+
+def gemm(a, b, bias=None, alpha=1.0, beta=0.0):
+    """alpha * (a @ b) + beta * bias in float64; a [.., M, K], b [.., K, N], bias broadcastable to the
+    output (it is ignored when beta == 0, as the reference ignores it)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    acc = np.matmul(a, b)
+    r = alpha * acc
+    if bias is not None and beta != 0.0:
+        r = r + beta * np.broadcast_to(np.asarray(bias, dtype=np.float64), r.shape)
+    return r
+
+
+# ---------------------------------------------------------------------------------------------------------
+# softmax — vkrt/shaders/softmax.comp.in:27-50
+# ---------------------------------------------------------------------------------------------------------
+
+
+def softmax_fwd(x, dim=-1, safe=False):
+    """y = exp(x - max) / sum(exp(x - max)) along dim; safe: rows whose entries are all -inf give 0."""
+    x = np.asarray(x, dtype=np.float64)
+    m = np.max(x, axis=dim, keepdims=True)
+    all_masked = np.isneginf(m)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        e = np.exp(x - m)
+        y = e / np.sum(e, axis=dim, keepdims=True)
+    if safe:
+        y = np.where(all_masked, 0.0, y)
+    return y
+
+
+def softmax_bwd(y, g, dim=-1):
+    """dx = y * (g - sum(g * y)) along dim."""
+    y = np.asarray(y, dtype=np.float64)
+    g = np.asarray(g, dtype=np.float64)
+    return y * (g - np.sum(g * y, axis=dim, keepdims=True))
+
+
+# ---------------------------------------------------------------------------------------------------------
+# layer_norm — vkrt/shaders/ln.comp.in:42-62 (forward), :63-81 (dx), :27-38 (dw, db)
+# ---------------------------------------------------------------------------------------------------------
+
+
+def layer_norm_fwd(x, ndim_norm=1, w=None, b=None, eps=1e-5):
+    """Normalise over the trailing ndim_norm dims.  Two-pass variance.  Returns (y, mean, rstd) with the
+    statistics shaped like x with the normalised dims set to 1."""
+    x = np.asarray(x, dtype=np.float64)
+    axes = tuple(range(x.ndim - ndim_norm, x.ndim))
+    mean = np.mean(x, axis=axes, keepdims=True)
+    var = np.mean((x - mean) ** 2, axis=axes, keepdims=True)
+    rstd = 1.0 / np.sqrt(var + eps)
+    y = (x - mean) * rstd
+    if w is not None:
+        y = y * np.asarray(w, dtype=np.float64)
+    if b is not None:
+        y = y + np.asarray(b, dtype=np.float64)
+    return y, mean, rstd
+
+
+def layer_norm_bwd(g, x, mean, rstd, ndim_norm=1, w=None):
+    """dx = rstd * (gw - mean(gw) - xhat * mean(gw * xhat)), gw = g * w; dw = sum_rows g * xhat;
+    db = sum_rows g.  Returns (dx, dw, db)."""
+    g = np.asarray(g, dtype=np.float64)
+    x = np.asarray(x, dtype=np.float64)
+    axes = tuple(range(x.ndim - ndim_norm, x.ndim))
+    lead = tuple(range(0, x.ndim - ndim_norm))
+    xhat = (x - mean) * rstd
+    gw = g * np.asarray(w, dtype=np.float64) if w is not None else g
+    s1 = np.mean(gw, axis=axes, keepdims=True)
+    s2 = np.mean(gw * xhat, axis=axes, keepdims=True)
+    dx = rstd * (gw - s1 - xhat * s2)
+    dw = np.sum(g * xhat, axis=lead)
+    db = np.sum(g, axis=lead)
+    return dx, dw, db
+
+
+# ---------------------------------------------------------------------------------------------------------
+# fused attention — forward vkrt/shaders/attn.comp.in:256-313 / attn_coop.comp.in:158-211,
+# delta attn.comp.in:210-240 with ops_attn.cpp:240-248, backward attn.comp.in:315-395 / attn_coop.comp.in:213-301
+# ---------------------------------------------------------------------------------------------------------
+
+
+def attention_fwd(q, k, v, scale):
+    """q [B,H,Sq,D], k, v [B,H,Sk,D] -> (out [B,H,Sq,D], lse [B,H,Sq]); online-softmax result written as the
+    closed form softmax(scale q k^T) v, lse = log sum exp(scale q k^T)."""
+    q, k, v = (np.asarray(t, dtype=np.float64) for t in (q, k, v))
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) * scale
+    m = np.max(s, axis=-1, keepdims=True)
+    p = np.exp(s - m)
+    l = np.sum(p, axis=-1, keepdims=True)
+    out = np.matmul(p / l, v)
+    lse = (m + np.log(l))[..., 0]
+    return out, lse
+
+
+def attention_delta(o, dout):
+    """delta[b,h,i] = sum_d O[b,h,i,d] * dO[b,h,i,d] (O is the unrounded forward output)."""
+    return np.sum(np.asarray(o, dtype=np.float64) * np.asarray(dout, dtype=np.float64), axis=-1)
+
+
+def attention_bwd(q, k, v, dout, lse, delta, scale, round_pds=None):
+    """Flash-attention backward from the saved lse and delta:
+        P = exp(scale q k^T - lse), dP = dO v^T, dS = P * (dP - delta),
+        dV = P^T dO, dK = scale dS^T q, dQ = scale dS k.
+    round_pds: optional function applied to P and dS before the second products (the matrix-core
+    kernels feed them to the MFMA in the input dtype, attn_coop.comp.in:235-236, 283-284)."""
+    q, k, v, dout = (np.asarray(t, dtype=np.float64) for t in (q, k, v, dout))
+    lse = np.asarray(lse, dtype=np.float64)[..., None]
+    delta = np.asarray(delta, dtype=np.float64)[..., None]
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) * scale
+    p = np.exp(s - lse)
+    dp = np.matmul(dout, np.swapaxes(v, -1, -2))
+    ds = p * (dp - delta)
+    if round_pds is not None:
+        p, ds = round_pds(p), round_pds(ds)
+    dv = np.matmul(np.swapaxes(p, -1, -2), dout)
+    dk = np.matmul(np.swapaxes(ds, -1, -2), q) * scale
+    dq = np.matmul(ds, k) * scale
+    return dq, dk, dv
+
+
+def rel_l2(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.linalg.norm(got - ref) / (np.linalg.norm(ref) + 1e-300))

@@ -1,0 +1,102 @@
+"""CPU checks of the boundary (no GPU needed): the C-ABI library loads and exports every symbol that
+include/*.h declares, the shim registers the reference's operator surface on PrivateUse1, the kernel
+registry knows every kernel name the shim asks for, and the slab allocator passes its host test."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(REPO, "torch-vulkan_amd")
+LIBHRT = os.path.join(PKG, "torch_vulkan", "libhrt.so")
+
+
+def declared_functions():
+    names = []
+    for h in ("hrt.h",):
+        text = open(os.path.join(REPO, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(hrt_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_libhrt_exports_every_declared_symbol():
+    assert os.path.exists(LIBHRT), "libhrt.so is not built (python torch-vulkan_amd/build.py)"
+    lib = ctypes.CDLL(LIBHRT)
+    names = declared_functions()
+    assert len(names) >= 27, names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_runtime_reports_errors_without_a_device():
+    """Without hrt_init (and without a GPU here) every call fails cleanly with a message."""
+    lib = ctypes.CDLL(LIBHRT)
+    lib.hrt_alloc.restype = ctypes.c_uint64
+    lib.hrt_alloc.argtypes = [ctypes.c_uint64]
+    lib.hrt_last_error.restype = ctypes.c_size_t
+    lib.hrt_last_error.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+    lib.hrt_kernel_index.argtypes = [ctypes.c_char_p]
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; the uninitialised-runtime path is only checked on CPU hosts")
+    assert lib.hrt_alloc(1024) == 0
+    buf = ctypes.create_string_buffer(256)
+    lib.hrt_last_error(buf, 256)
+    assert b"hrt_init" in buf.value
+    # the kernel table is static: names resolve without a device
+    assert lib.hrt_kernel_index(b"dq8_bf16") >= 0
+    assert lib.hrt_kernel_index(b"no_such_kernel") == -1
+
+
+KERNELS = (
+    ["add_f32", "ew_copy", "ew_fill"]
+    + [f"dq8_{k}" for k in ("f32", "bf16", "f16")]
+    + [f"mm_{k}" for k in ("f32", "bf16", "f16")]
+    + [f"mm_mfma_{k}" for k in ("bf16", "f16")]
+    + [f"softmax_{d}_{k}" for d in ("fwd", "bwd") for k in ("f32", "bf16", "f16")]
+    + [f"ln_{d}_{k}" for d in ("fwd", "bwd", "wgrad") for k in ("f32", "bf16", "f16")]
+    + [f"attn_{op}_fma_{k}" for op in ("fwd", "dkdv", "dq") for k in ("f32", "bf16", "f16")]
+    + [f"attn_{op}_mfma_{k}" for op in ("fwd", "dkdv", "dq") for k in ("bf16", "f16")]
+    + [f"attn_delta_{k}" for k in ("f32", "bf16", "f16")]
+    + [f"mm_dq8_{k}" for k in ("bf16", "f16")]
+)
+
+
+@pytest.mark.parametrize("name", KERNELS)
+def test_kernel_registry_has(name):
+    lib = ctypes.CDLL(LIBHRT)
+    lib.hrt_kernel_index.argtypes = [ctypes.c_char_p]
+    assert lib.hrt_kernel_index(name.encode()) >= 0, name
+
+
+def test_shim_registers_the_reference_operator_surface():
+    import torch_vulkan  # noqa: F401  (loads the shim; no device needed)
+
+    ops = [
+        "aten::mm", "aten::bmm", "aten::addmm", "aten::baddbmm",
+        "aten::_scaled_dot_product_fused_attention_overrideable",
+        "aten::_scaled_dot_product_fused_attention_overrideable_backward",
+        "aten::_softmax", "aten::_safe_softmax", "aten::_softmax_backward_data",
+        "aten::native_layer_norm", "aten::native_layer_norm_backward",
+        "aten::empty.memory_format", "aten::empty_strided", "aten::_copy_from", "aten::_copy_from_and_resize",
+        "aten::view", "aten::as_strided", "aten::_reshape_alias", "aten::resize_", "aten::fill_.Scalar", "aten::zero_",
+    ]
+    missing = [o for o in ops if not torch._C._dispatch_has_kernel_for_dispatch_key(o, "PrivateUse1")]
+    assert not missing, missing
+    assert torch._C._get_privateuse1_backend_name() == "vk"
+    assert hasattr(torch, "vk") and torch.vk.device_count() == 1
+
+
+def test_slab_allocator_host(tmp_path):
+    """Compiles tests/cpu/allocator_test.cpp against the runtime's allocator with ASan/UBSan (host code)."""
+    exe = tmp_path / "alloc_test"
+    src = os.path.join(REPO, "tests", "cpu", "allocator_test.cpp")
+    inc = os.path.join(PKG, "csrc", "hrt")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-I", inc, src, "-o", str(exe)],
+                   check=True)
+    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0 and "ALL OK" in r.stdout, r.stdout

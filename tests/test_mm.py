@@ -1,0 +1,182 @@
+"""mm / bmm / addmm / baddbmm on the GPU vs the float64 oracle (reference tests/test_mm.py:1-221) with the
+reference tolerance max|err| <= tol * max(|ref|max, 1) * (1 + 0.01 sqrt(K)), tol = f32 2e-5, bf16 1.2e-2,
+f16 2e-3: odd shapes, transposed and sliced operands read in place, bias broadcast x alpha/beta, batched,
+nn.Linear autograd, matrix-core vs FMA agreement, and the BASELINE shapes (1024^3 + bias, 1024x2048x8192)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from vkutil import f64, randn
+
+pytestmark = pytest.mark.gpu
+
+import torch_vulkan  # noqa: E402
+
+dev = torch.device("vk")
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+TOL = {torch.float32: 2e-5, torch.bfloat16: 1.2e-2, torch.float16: 2e-3}
+
+
+def check(out, ref64, dtype, k):
+    o = f64(out)
+    assert o.shape == ref64.shape
+    scale = float(np.abs(ref64).max()) + 1e-9
+    err = float(np.abs(o - ref64).max())
+    assert err <= TOL[dtype] * max(scale, 1.0) * (1 + k ** 0.5 * 0.01), f"max err {err} scale {scale}"
+
+
+def no_fallback(*names):
+    fb = torch_vulkan.fallback_counts()
+    assert not {n: fb[n] for n in names if n in fb}, fb
+
+
+SHAPES = [(1, 1, 1), (7, 5, 3), (64, 16, 64), (65, 17, 63), (128, 129, 300), (33, 1000, 40), (5, 2048, 7),
+          (256, 256, 256), (300, 72, 520), (1, 4096, 16), (1024, 16, 2048)]
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_mm_shapes(dt, m, k, n):
+    a, b = randn((m, k), dt, 1), randn((k, n), dt, 2)
+    out = torch.mm(a.to(dev), b.to(dev))
+    assert out.dtype == dt and out.shape == (m, n)
+    check(out, oracle.gemm(f64(a), f64(b)), dt, k)
+    assert torch_vulkan.kernel_counts().get("aten::mm") == 1
+    no_fallback("aten::mm")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_mm_transposed_operands_without_copy(dt, ta, tb):
+    m, k, n = 70, 45, 90
+    a = randn((k, m) if ta else (m, k), dt, 3)
+    b = randn((n, k) if tb else (k, n), dt, 4)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b))
+    torch_vulkan.reset_fallback_counts()
+    check(torch.mm(A, B), ref, dt, k)
+    assert "aten::clone" not in torch_vulkan.fallback_counts()
+    assert torch_vulkan.kernel_counts().get("aten::copy_", 0) == 0  # operands read in place
+    no_fallback("aten::mm")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,k,n", [(96, 80, 70), (256, 512, 384), (200, 136, 264)])
+def test_mfma_transposes_and_bias(dt, ta, tb, m, k, n):
+    a = randn((k, m) if ta else (m, k), dt, 3)
+    b = randn((n, k) if tb else (k, n), dt, 4)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b))
+    check(torch.mm(A, B), ref, dt, k)
+    bias = randn((n,), dt, 5)
+    out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=2.0)
+    check(out, oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 2.0), dt, k)
+
+
+def test_mm_on_sliced_views_with_offset():
+    for dt in DTYPES:
+        a, b = randn((20, 30), dt, 5), randn((30, 25), dt, 6)
+        ad, bd = a.to(dev), b.to(dev)
+        out = torch.mm(ad[3:15, 4:20], bd[4:20, 2:22])
+        check(out, oracle.gemm(f64(a[3:15, 4:20]), f64(b[4:20, 2:22])), dt, 16)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_bmm(dt):
+    a, b = randn((5, 37, 29), dt, 1), randn((5, 29, 41), dt, 2)
+    ref = oracle.gemm(f64(a), f64(b))
+    check(torch.bmm(a.to(dev), b.to(dev)), ref, dt, 29)
+    out2 = torch.bmm(a.to(dev), b.to(dev).transpose(1, 2).contiguous().transpose(1, 2))
+    check(out2, ref, dt, 29)
+    no_fallback("aten::bmm")
+
+
+@pytest.mark.parametrize("bias_shape", [(40,), (1, 40), (30, 1), (30, 40), ()])
+@pytest.mark.parametrize("dt", DTYPES)
+def test_addmm_bias_broadcast_alpha_beta(bias_shape, dt):
+    a, b = randn((30, 20), dt, 1), randn((20, 40), dt, 2)
+    bias = randn(bias_shape, dt, 3)
+    for alpha, beta in [(1.0, 1.0), (0.5, 2.0), (2.0, 0.0)]:
+        out = torch.addmm(bias.to(dev), a.to(dev), b.to(dev), alpha=alpha, beta=beta)
+        ref = oracle.gemm(f64(a), f64(b), f64(bias), alpha, beta)
+        check(out, np.broadcast_to(ref, (30, 40)), dt, 20)
+    no_fallback("aten::addmm")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_baddbmm(dt):
+    a, b = randn((3, 10, 8), dt, 1), randn((3, 8, 12), dt, 2)
+    bias = randn((3, 1, 12), dt, 3)
+    out = torch.baddbmm(bias.to(dev), a.to(dev), b.to(dev), alpha=0.5, beta=1.5)
+    check(out, oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 1.5), dt, 8)
+    no_fallback("aten::baddbmm")
+
+
+def test_mixed_dtype_and_empty_k_fall_back_correctly():
+    a, b = randn((4, 5), torch.float32), randn((5, 6), torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        torch.mm(a.to(dev), b.to(dev))
+    z = torch.mm(torch.zeros(3, 0, device=dev), torch.zeros(0, 4, device=dev))
+    assert torch.equal(z.cpu(), torch.zeros(3, 4))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_linear_forward_backward(dt):
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(48, 32).to(dt)
+    x = randn((2, 10, 48), dt, 5)
+    W, bvec = f64(lin.weight), f64(lin.bias)
+    xd = x.to(dev).requires_grad_(True)
+    lin_d = torch.nn.Linear(48, 32).to(dt)
+    lin_d.load_state_dict(lin.state_dict())
+    lin_d.to(dev)
+    y = lin_d(xd)
+    ref = oracle.gemm(f64(x).reshape(20, 48), W.T, bvec, 1.0, 1.0).reshape(2, 10, 32)
+    check(y, ref, dt, 48)
+    g = randn((2, 10, 32), dt, 6)
+    y.backward(g.to(dev))
+    g2 = f64(g).reshape(20, 32)
+    check(xd.grad, oracle.gemm(g2, W).reshape(2, 10, 48), dt, 32)
+    check(lin_d.weight.grad, oracle.gemm(g2.T, f64(x).reshape(20, 48)), dt, 20)
+    assert "aten::mm" not in torch_vulkan.fallback_counts()
+
+
+def test_mfma_agrees_with_fma_kernel():
+    a, b = randn((4, 70, 90), torch.bfloat16, 1), randn((4, 90, 50), torch.bfloat16, 2)
+    out_mfma = torch.bmm(a.to(dev), b.to(dev)).cpu().float()
+    torch_vulkan.set_coop_enabled(False)
+    try:
+        out_fma = torch.bmm(a.to(dev), b.to(dev)).cpu().float()
+    finally:
+        torch_vulkan.set_coop_enabled(True)
+    assert torch.allclose(out_mfma, out_fma, rtol=1.5e-2, atol=3e-2), (out_mfma - out_fma).abs().max()
+
+
+def test_baseline_addmm_1024_cubed_with_bias():
+    a, b, bias = randn((1024, 1024), torch.bfloat16, 1), randn((1024, 1024), torch.bfloat16, 2), randn((1024,), torch.bfloat16, 3)
+    out = torch.addmm(bias.to(dev), a.to(dev), b.to(dev))
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 1.0, 1.0)
+    check(out, ref, torch.bfloat16, 1024)
+    assert oracle.rel_l2(f64(out), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("layout", ["nn", "linear"])
+def test_baseline_gemm_1024x2048x8192(layout):
+    M, K, N = 1024, 2048, 8192
+    a = randn((M, K), torch.bfloat16, 1)
+    if layout == "nn":
+        b = randn((K, N), torch.bfloat16, 2)
+        out = torch.mm(a.to(dev), b.to(dev))
+        ref = oracle.gemm(f64(a), f64(b))
+    else:  # F.linear: x @ W^T with W [N, K] read through its transpose view
+        w = randn((N, K), torch.bfloat16, 2)
+        out = torch.mm(a.to(dev), w.to(dev).t())
+        ref = oracle.gemm(f64(a), f64(w).T)
+    assert oracle.rel_l2(f64(out), ref) <= 1e-2
+    check(out, ref, torch.bfloat16, K)

@@ -1,0 +1,472 @@
+// hrt runtime: the C ABI declared in include/hrt.h, over HIP.
+//
+// One process-wide Runtime owns the device, ONE HIP stream (default priority) and the slab allocator.
+// Kernels and device-to-device copies are queued on that stream and never waited for, so launches
+// batch naturally; the host waits only where data must be visible to it (download, synchronize) or
+// memory goes back to the driver.  Mirrors the reference runtime's contract (vkrt/src/lib.rs:975-1244):
+// 0 / -1 status codes, 0 for failed values, and a last-error string.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../../include/hrt.h"
+#include "registry.h"
+#include "slab_allocator.h"
+
+namespace hrt {
+
+std::vector<KernelEntry>& kernel_table() {
+  static std::vector<KernelEntry> t;
+  return t;
+}
+
+namespace {
+
+std::mutex g_err_mu;
+std::string g_last_error;
+
+void set_error(const std::string& e) {
+  std::lock_guard<std::mutex> l(g_err_mu);
+  g_last_error = e;
+}
+
+std::atomic<uint64_t> g_stats[8];
+std::atomic<uint64_t> g_validation_errors{0};
+
+uint64_t now_ns() {
+  return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
+
+struct HipBacking final : Backing {
+  hipStream_t stream = nullptr;
+  bool map(uint64_t size, uint64_t* base, std::string* err) override {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, size);
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      *err = "hipMalloc(" + std::to_string(size) + " bytes): " + hipGetErrorString(e);
+      return false;
+    }
+    *base = reinterpret_cast<uint64_t>(p);
+    return true;
+  }
+  void unmap(uint64_t base) override { (void)hipFree(reinterpret_cast<void*>(base)); }
+  void drain() override {
+    if (stream) (void)hipStreamSynchronize(stream);
+  }
+};
+
+struct Runtime {
+  std::mutex mu;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string name;
+  uint64_t total_mem = 0;
+  HipBacking backing;
+  std::unique_ptr<SlabAllocator> alloc;
+  bool profile = false;
+  std::map<std::string, std::pair<uint64_t, uint64_t>> prof;  // name -> (ns, count)
+  hipEvent_t prof_ev[2] = {nullptr, nullptr};
+  hipEvent_t slots[16] = {};
+};
+
+Runtime* g_rt = nullptr;
+std::mutex g_init_mu;
+
+bool in_bounds_locked(uint64_t addr, uint64_t bytes, std::string* err) { return g_rt->alloc->resolve(addr, bytes, err); }
+
+int hip_fail(const char* what, hipError_t e) {
+  (void)hipGetLastError();
+  set_error(std::string(what) + ": " + hipGetErrorString(e));
+  return -1;
+}
+
+Runtime* rt_or_error() {
+  if (!g_rt) set_error("hrt_init has not been called");
+  return g_rt;
+}
+
+int init_runtime() {
+  auto rt = std::make_unique<Runtime>();
+  const char* dev_env = std::getenv("HRT_DEVICE");
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0) {
+    (void)hipGetLastError();
+    set_error(std::string("no HIP device available: ") + (e != hipSuccess ? hipGetErrorString(e) : "0 devices"));
+    return -1;
+  }
+  int dev = 0;
+  if (dev_env && dev_env[0]) {
+    char* end = nullptr;
+    long v = std::strtol(dev_env, &end, 10);
+    if (end == dev_env || *end != '\0' || v < 0 || v >= count) {
+      std::string names;
+      for (int i = 0; i < count; ++i) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) == hipSuccess) names += "\n  " + std::to_string(i) + ": " + p.name;
+      }
+      set_error(std::string("HRT_DEVICE='") + dev_env + "' does not name a device; available:" + names);
+      return -1;
+    }
+    dev = (int)v;
+  }
+  if ((e = hipSetDevice(dev)) != hipSuccess) return hip_fail("hipSetDevice", e);
+  hipDeviceProp_t prop;
+  if ((e = hipGetDeviceProperties(&prop, dev)) != hipSuccess) return hip_fail("hipGetDeviceProperties", e);
+  rt->device = dev;
+  rt->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+  rt->total_mem = prop.totalGlobalMem;
+  if ((e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking)) != hipSuccess) return hip_fail("hipStreamCreate", e);
+  rt->backing.stream = rt->stream;
+  rt->alloc = std::make_unique<SlabAllocator>(&rt->backing, rt->total_mem);
+  const char* pe = std::getenv("HRT_PROFILE");
+  rt->profile = pe && pe[0] && pe[0] != '0';
+  if (rt->profile) {
+    for (auto& ev : rt->prof_ev)
+      if ((e = hipEventCreate(&ev)) != hipSuccess) return hip_fail("hipEventCreate", e);
+  }
+  uint64_t t0 = now_ns();
+  (void)kernel_table();  // populated by static registration at load time
+  g_stats[4] += now_ns() - t0;
+  g_rt = rt.release();
+  return 0;
+}
+
+size_t copy_out(const std::string& s, char* buf, size_t cap) {
+  if (buf && cap > 0) {
+    size_t n = std::min(s.size(), cap - 1);
+    std::memcpy(buf, s.data(), n);
+    buf[n] = '\0';
+  }
+  return s.size();
+}
+
+bool checked(Runtime* rt, uint64_t addr, uint64_t n) {
+  std::string err;
+  if (!rt->alloc->resolve(addr, n, &err)) {
+    g_validation_errors++;
+    set_error(err);
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+}  // namespace hrt
+
+using namespace hrt;
+
+extern "C" {
+
+int hrt_init(void) {
+  std::lock_guard<std::mutex> l(g_init_mu);
+  if (g_rt) return 0;
+  return init_runtime();
+}
+
+size_t hrt_last_error(char* buf, size_t cap) {
+  std::lock_guard<std::mutex> l(g_err_mu);
+  return copy_out(g_last_error, buf, cap);
+}
+
+size_t hrt_device_name(char* buf, size_t cap) {
+  Runtime* rt = rt_or_error();
+  return copy_out(rt ? rt->name : std::string(), buf, cap);
+}
+
+uint64_t hrt_max_alloc(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return rt->alloc->max_alloc();
+}
+
+uint64_t hrt_live_bytes(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return rt->alloc->live_bytes();
+}
+
+int32_t hrt_memory_info(uint64_t* out) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  if (!out) {
+    set_error("hrt_memory_info: null output");
+    return -1;
+  }
+  std::lock_guard<std::mutex> l(rt->mu);
+  size_t free_b = 0, total_b = 0;
+  hipError_t e = hipMemGetInfo(&free_b, &total_b);
+  if (e != hipSuccess) return hip_fail("hipMemGetInfo", e);
+  out[0] = (uint64_t)free_b + rt->alloc->reserved_bytes();
+  if (out[0] > total_b) out[0] = total_b;
+  out[1] = (uint64_t)(total_b - free_b);
+  out[2] = (uint64_t)total_b;
+  return 0;
+}
+
+uint64_t hrt_peak_live_bytes(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return rt->alloc->peak_live_bytes();
+}
+
+void hrt_reset_peak_live_bytes(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return;
+  std::lock_guard<std::mutex> l(rt->mu);
+  rt->alloc->reset_peak();
+}
+
+void hrt_set_memory_limit(uint64_t bytes) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return;
+  std::lock_guard<std::mutex> l(rt->mu);
+  rt->alloc->set_limit(bytes);
+}
+
+uint64_t hrt_alloc(uint64_t size) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  std::string err;
+  uint64_t a = rt->alloc->alloc(size, &err);
+  if (!a) set_error(err);
+  return a;
+}
+
+int hrt_free(uint64_t addr) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  std::lock_guard<std::mutex> l(rt->mu);
+  std::string err;
+  if (!rt->alloc->free(addr, &err)) {
+    set_error(err);
+    return -1;
+  }
+  return 0;
+}
+
+int hrt_upload(uint64_t dst, const void* src, uint64_t n) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  if (n == 0) return 0;
+  uint64_t t0 = now_ns();
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (!src) {
+    set_error("hrt_upload: null source");
+    return -1;
+  }
+  if (!checked(rt, dst, n)) return -1;
+  hipError_t e = hipMemcpyAsync(reinterpret_cast<void*>(dst), src, n, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);  // the source may be freed on return
+  g_stats[2] += now_ns() - t0;
+  g_stats[3]++;
+  g_stats[5] += n;
+  if (e != hipSuccess) return hip_fail("upload", e);
+  return 0;
+}
+
+int hrt_download(void* dst, uint64_t src, uint64_t n) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  if (n == 0) return 0;
+  uint64_t t0 = now_ns();
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (!dst) {
+    set_error("hrt_download: null destination");
+    return -1;
+  }
+  if (!checked(rt, src, n)) return -1;
+  hipError_t e = hipMemcpyAsync(dst, reinterpret_cast<const void*>(src), n, hipMemcpyDeviceToHost, rt->stream);
+  uint64_t tw = now_ns();
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+  g_stats[7] += now_ns() - tw;
+  g_stats[2] += now_ns() - t0;
+  g_stats[3]++;
+  g_stats[6] += n;
+  if (e != hipSuccess) return hip_fail("download", e);
+  return 0;
+}
+
+int hrt_copy_d2d(uint64_t dst, uint64_t src, uint64_t n) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  if (n == 0) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (!checked(rt, dst, n) || !checked(rt, src, n)) return -1;
+  hipError_t e =
+      hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), n, hipMemcpyDeviceToDevice, rt->stream);
+  if (e != hipSuccess) return hip_fail("copy_d2d", e);
+  return 0;
+}
+
+int hrt_kernel_index(const char* name) {
+  if (!name) return -1;
+  const auto& t = kernel_table();
+  for (size_t i = 0; i < t.size(); ++i)
+    if (std::strcmp(t[i].name, name) == 0) return (int)i;
+  return -1;
+}
+
+int hrt_dispatch(uint32_t kernel, const void* args, uint32_t len, uint32_t gx, uint32_t gy, uint32_t gz) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  uint64_t t0 = now_ns();
+  const auto& t = kernel_table();
+  if (kernel >= t.size()) {
+    set_error("hrt_dispatch: unknown kernel id " + std::to_string(kernel));
+    return -1;
+  }
+  const KernelEntry& k = t[kernel];
+  if (len != k.args_size || !args) {
+    set_error(std::string("hrt_dispatch(") + k.name + "): argument block is " + std::to_string(len) + " bytes, expected " +
+              std::to_string(k.args_size));
+    return -1;
+  }
+  uint32_t grid[3] = {gx, gy, gz};
+  if (k.raw_grid) {
+    if (gx == 0 || gy == 0 || gz == 0) {
+      set_error(std::string("hrt_dispatch(") + k.name + "): empty grid");
+      return -1;
+    }
+  } else if (gx != 0 || gy != 0 || gz != 0) {
+    set_error(std::string("hrt_dispatch(") + k.name + "): this kernel sizes its own grid; pass gx = gy = gz = 0");
+    return -1;
+  }
+  std::lock_guard<std::mutex> l(rt->mu);
+  LaunchCtx ctx;
+  ctx.stream = rt->stream;
+  ctx.in_bounds = &in_bounds_locked;
+  if (rt->profile) (void)hipEventRecord(rt->prof_ev[0], rt->stream);
+  bool ok = k.launch(args, grid, ctx);
+  if (!ok) {
+    if (ctx.error.rfind("operand", 0) == 0) g_validation_errors++;
+    set_error(std::string(k.name) + ": " + ctx.error);
+    return -1;
+  }
+  if (rt->profile) {
+    (void)hipEventRecord(rt->prof_ev[1], rt->stream);
+    (void)hipEventSynchronize(rt->prof_ev[1]);
+    float ms = 0.f;
+    (void)hipEventElapsedTime(&ms, rt->prof_ev[0], rt->prof_ev[1]);
+    auto& p = rt->prof[k.name];
+    p.first += (uint64_t)(ms * 1e6);
+    p.second += 1;
+  }
+  g_stats[0] += now_ns() - t0;
+  g_stats[1]++;
+  return 0;
+}
+
+int hrt_synchronize(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  std::lock_guard<std::mutex> l(rt->mu);
+  uint64_t t0 = now_ns();
+  hipError_t e = hipStreamSynchronize(rt->stream);
+  g_stats[7] += now_ns() - t0;
+  if (e != hipSuccess) return hip_fail("synchronize", e);
+  return 0;
+}
+
+size_t hrt_empty_cache(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return rt->alloc->empty_cache();
+}
+
+uint64_t hrt_reserved_bytes(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return rt->alloc->reserved_bytes();
+}
+
+size_t hrt_live_blocks(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return rt->alloc->live_blocks();
+}
+
+size_t hrt_slab_count(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return rt->alloc->slab_count();
+}
+
+size_t hrt_validation_errors(void) { return (size_t)g_validation_errors.load(); }
+
+uint64_t hrt_stat(uint32_t i) { return i < 8 ? g_stats[i].load() : 0; }
+
+size_t hrt_profile_dump(char* buf, size_t cap) {
+  std::string out;
+  if (g_rt) {
+    std::lock_guard<std::mutex> l(g_rt->mu);
+    std::vector<std::pair<std::string, std::pair<uint64_t, uint64_t>>> v(g_rt->prof.begin(), g_rt->prof.end());
+    std::sort(v.begin(), v.end(), [](const auto& a, const auto& b) { return a.second.first > b.second.first; });
+    char line[256];
+    for (const auto& kv : v) {
+      snprintf(line, sizeof(line), "%s\t%.3f\t%llu\n", kv.first.c_str(), kv.second.first * 1e-6,
+               (unsigned long long)kv.second.second);
+      out += line;
+    }
+  }
+  return copy_out(out, buf, cap);
+}
+
+uint32_t hrt_coop_caps(void) {
+  Runtime* rt = rt_or_error();
+  return rt ? 3u : 0u;
+}
+
+int hrt_event_record(uint32_t slot) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  if (slot >= 16) {
+    set_error("hrt_event_record: slot must be < 16");
+    return -1;
+  }
+  std::lock_guard<std::mutex> l(rt->mu);
+  hipError_t e = hipSuccess;
+  if (!rt->slots[slot]) e = hipEventCreate(&rt->slots[slot]);
+  if (e == hipSuccess) e = hipEventRecord(rt->slots[slot], rt->stream);
+  if (e != hipSuccess) return hip_fail("hipEventRecord", e);
+  return 0;
+}
+
+float hrt_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1.f;
+  if (start_slot >= 16 || end_slot >= 16 || !rt->slots[start_slot] || !rt->slots[end_slot]) {
+    set_error("hrt_event_elapsed_ms: slot not recorded");
+    return -1.f;
+  }
+  hipError_t e = hipEventSynchronize(rt->slots[end_slot]);
+  float ms = -1.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, rt->slots[start_slot], rt->slots[end_slot]);
+  if (e != hipSuccess) {
+    hip_fail("hipEventElapsedTime", e);
+    return -1.f;
+  }
+  return ms;
+}
+
+}  // extern "C"

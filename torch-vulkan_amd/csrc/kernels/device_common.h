@@ -1,0 +1,129 @@
+// Device-side helpers shared by the gfx950 kernels: element conversions with the reference's rounding
+// contract, 64-lane wavefront reductions, and small vector types.
+//
+// Rounding contract (vkrt/shaders/types.glsl:18-50, identical to torch's CPU `.to()`):
+//   f32 -> bf16: round to nearest even, every NaN -> 0x7FC0;
+//   f32 -> f16 : round to nearest even including subnormals, overflow -> inf (v_cvt_f16_f32 does this in
+//                the default round-to-nearest-even mode with f16 denormals enabled).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../../include/hrt_ops.h"
+
+namespace hk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  union {
+    uint16_t u;
+    _Float16 f;
+  } c;
+  c.u = (uint16_t)h;
+  return (float)c.f;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
+  union {
+    uint16_t u;
+    _Float16 f;
+  } c;
+  c.f = (_Float16)x;
+  return c.u;
+}
+
+// Element type tags used as template parameters.
+struct F32 {
+  using storage = float;
+  static constexpr int code = HRT_F32;
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static float to_f32(float v) { return v; }
+  __device__ __forceinline__ static float from_f32(float v) { return v; }
+};
+struct BF16 {
+  using storage = uint16_t;
+  static constexpr int code = HRT_BF16;
+  __device__ __forceinline__ static float to_f32(uint16_t v) { return bf16_bits_to_f32(v); }
+  __device__ __forceinline__ static uint16_t from_f32(float v) { return (uint16_t)f32_to_bf16_bits(v); }
+};
+struct F16 {
+  using storage = uint16_t;
+  static constexpr int code = HRT_F16;
+  __device__ __forceinline__ static float to_f32(uint16_t v) { return f16_bits_to_f32(v); }
+  __device__ __forceinline__ static uint16_t from_f32(float v) { return (uint16_t)f32_to_f16_bits(v); }
+};
+
+// Pack two floats into one dword of 16-bit elements (low = a).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)T::from_f32(a) | ((uint32_t)T::from_f32(b) << 16);
+}
+template <typename T>
+__device__ __forceinline__ float lo16(uint32_t w) {
+  return T::to_f32((uint16_t)(w & 0xffffu));
+}
+template <typename T>
+__device__ __forceinline__ float hi16(uint32_t w) {
+  return T::to_f32((uint16_t)(w >> 16));
+}
+
+// ---- wavefront (64 lanes) reductions --------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide reductions for blocks of NW waves; `red` is LDS scratch of at least NW floats.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  if (NW == 1) return v;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) r += red[i];
+  return r;
+}
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  if (NW == 1) return v;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+
+__host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace hk

@@ -1,0 +1,135 @@
+// Weight-only int8 dequant (reference: vkrt/shaders/dq8.comp.in:39-62, closed form
+// torch_vulkan/__init__.py:203-205):  out[r, c] = round_dt(float(q[r, c]) * float(scale[r, c / 64])).
+//
+// HBM-bound: 1 byte in + 2 (bf16/f16) or 4 (f32) bytes out per element plus 2 bytes of scale per 64.
+// Fast path: each thread moves 16 int8 with one 128-bit load and writes them with 128-bit stores
+// (a 16-element chunk never crosses a row or a 64-column scale block when cols % 16 == 0); two chunks
+// per thread are loaded before any store to keep more bytes in flight.  Any other shape or alignment
+// takes the per-element path.  Results are bit-exact: the fp32 product of an int8 and a bf16 is exact,
+// so the only rounding is the final RNE store.
+#include "../hrt/registry.h"
+#include "device_common.h"
+
+namespace hk {
+namespace {
+
+constexpr int kChunks = 2;  // 16-element chunks per thread
+
+template <typename T>
+__device__ __forceinline__ void store16(typename T::storage* out, int64_t e, const float* v);
+
+template <>
+__device__ __forceinline__ void store16<BF16>(uint16_t* out, int64_t e, const float* v) {
+  u32x4 w0, w1;
+  w0.x = pack2<BF16>(v[0], v[1]);
+  w0.y = pack2<BF16>(v[2], v[3]);
+  w0.z = pack2<BF16>(v[4], v[5]);
+  w0.w = pack2<BF16>(v[6], v[7]);
+  w1.x = pack2<BF16>(v[8], v[9]);
+  w1.y = pack2<BF16>(v[10], v[11]);
+  w1.z = pack2<BF16>(v[12], v[13]);
+  w1.w = pack2<BF16>(v[14], v[15]);
+  u32x4* o = reinterpret_cast<u32x4*>(out + e);
+  __builtin_nontemporal_store(w0, o);
+  __builtin_nontemporal_store(w1, o + 1);
+}
+template <>
+__device__ __forceinline__ void store16<F16>(uint16_t* out, int64_t e, const float* v) {
+  u32x4 w0, w1;
+  w0.x = pack2<F16>(v[0], v[1]);
+  w0.y = pack2<F16>(v[2], v[3]);
+  w0.z = pack2<F16>(v[4], v[5]);
+  w0.w = pack2<F16>(v[6], v[7]);
+  w1.x = pack2<F16>(v[8], v[9]);
+  w1.y = pack2<F16>(v[10], v[11]);
+  w1.z = pack2<F16>(v[12], v[13]);
+  w1.w = pack2<F16>(v[14], v[15]);
+  u32x4* o = reinterpret_cast<u32x4*>(out + e);
+  __builtin_nontemporal_store(w0, o);
+  __builtin_nontemporal_store(w1, o + 1);
+}
+template <>
+__device__ __forceinline__ void store16<F32>(float* out, int64_t e, const float* v) {
+  f32x4* o = reinterpret_cast<f32x4*>(out + e);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f32x4 w = {v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+    __builtin_nontemporal_store(w, o + i);
+  }
+}
+
+__device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)(int8_t)((w >> (8 * i)) & 0xffu); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void dq8_vec(const int8_t* __restrict__ q, const uint16_t* __restrict__ scale,
+                                               typename T::storage* __restrict__ out, int64_t cols, int64_t nblocks,
+                                               int64_t nchunks) {
+  const int64_t base = (int64_t)blockIdx.x * (256 * kChunks) + threadIdx.x;
+  u32x4 qv[kChunks];
+  float sv[kChunks];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int64_t ch = base + c * 256;
+    if (ch < nchunks) {
+      const int64_t e = ch * 16;
+      qv[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + e));
+      const int64_t r = e / cols, col = e - r * cols;
+      sv[c] = bf16_bits_to_f32(scale[r * nblocks + (col >> 6)]);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int64_t ch = base + c * 256;
+    if (ch < nchunks) {
+      float v[16];
+      const uint32_t w[4] = {qv[c].x, qv[c].y, qv[c].z, qv[c].w};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = sbyte(w[i >> 2], i & 3) * sv[c];
+      store16<T>(out, ch * 16, v);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dq8_scalar(const int8_t* __restrict__ q, const uint16_t* __restrict__ scale,
+                                                  typename T::storage* __restrict__ out, int64_t cols, int64_t nblocks,
+                                                  int64_t total) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t r = e / cols, col = e - r * cols;
+    const float v = (float)q[e] * bf16_bits_to_f32(scale[r * nblocks + (col >> 6)]);
+    out[e] = T::from_f32(v);
+  }
+}
+
+template <typename T>
+bool launch_dq8(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_dq8_args*>(p);
+  if (a.rows < 0 || a.cols < 0) return ctx.fail("negative shape");
+  if (a.nblocks != (a.cols + 63) / 64) return ctx.fail("nblocks must equal ceil(cols / 64)");
+  const int64_t total = a.rows * a.cols;
+  if (total == 0) return true;
+  const uint64_t osz = sizeof(typename T::storage);
+  if (!ctx.check(a.q, (uint64_t)total, "q") || !ctx.check(a.scale, (uint64_t)(a.rows * a.nblocks) * 2, "scale") ||
+      !ctx.check(a.out, (uint64_t)total * osz, "out"))
+    return false;
+  const bool vec = a.cols % 16 == 0 && a.q % 16 == 0 && a.out % 16 == 0;
+  if (vec) {
+    const int64_t nchunks = total / 16;
+    const int64_t grid = cdiv(nchunks, 256 * kChunks);
+    hipLaunchKernelGGL(dq8_vec<T>, dim3((uint32_t)grid), dim3(256), 0, ctx.stream, (const int8_t*)a.q,
+                       (const uint16_t*)a.scale, (typename T::storage*)a.out, a.cols, a.nblocks, nchunks);
+  } else {
+    int64_t grid = cdiv(total, 256);
+    if (grid > 16384) grid = 16384;
+    hipLaunchKernelGGL(dq8_scalar<T>, dim3((uint32_t)grid), dim3(256), 0, ctx.stream, (const int8_t*)a.q,
+                       (const uint16_t*)a.scale, (typename T::storage*)a.out, a.cols, a.nblocks, total);
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "dq8");
+}
+
+HRT_REGISTER("dq8_f32", hrt_dq8_args, launch_dq8<F32>);
+HRT_REGISTER("dq8_bf16", hrt_dq8_args, launch_dq8<BF16>);
+HRT_REGISTER("dq8_f16", hrt_dq8_args, launch_dq8<F16>);
+
+}  // namespace
+}  // namespace hk

@@ -1,0 +1,246 @@
+// Support kernels of the boundary: the runtime smoke kernel, strided copy/cast and fill.
+// The hot-path adapters call `.contiguous()`, `.to(dtype)` and `at::zeros`; without these the data
+// would round-trip through the host (reference: csrc/ops_ew.cpp:382-392, 495-506; csrc/shim.cpp:257-276).
+#include "../hrt/registry.h"
+#include "device_common.h"
+
+namespace hk {
+namespace {
+
+// ---- add_f32: raw-grid smoke kernel (vkrt/tests/basic.rs:53-76) -----------------------------------
+__global__ __launch_bounds__(256) void add_f32_kernel(const float* a, const float* b, float* c, uint64_t n) {
+  uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) c[i] = a[i] + b[i];
+}
+
+bool launch_add_f32(const void* p, const uint32_t grid[3], hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_add_f32_args*>(p);
+  const uint64_t cover = (uint64_t)grid[0] * grid[1] * grid[2] * 256;
+  const uint64_t n = a.n < cover ? a.n : cover;
+  if (!ctx.check(a.a, n * 4, "a") || !ctx.check(a.b, n * 4, "b") || !ctx.check(a.c, n * 4, "c")) return false;
+  if (grid[1] != 1 || grid[2] != 1) return ctx.fail("add_f32 uses a 1-D grid");
+  hipLaunchKernelGGL(add_f32_kernel, dim3(grid[0]), dim3(256), 0, ctx.stream, (const float*)a.a, (const float*)a.b,
+                     (float*)a.c, n);
+  return hrt::launch_ok(hipGetLastError(), ctx, "add_f32");
+}
+HRT_REGISTER_RAW("add_f32", hrt_add_f32_args, launch_add_f32);
+
+// ---- element access by type code --------------------------------------------------------------------
+template <int CODE>
+struct Elem;
+template <>
+struct Elem<HRT_F32> {
+  using S = float;
+  __device__ static float get(const S* p) { return *p; }
+  __device__ static void put(S* p, float v) { *p = v; }
+};
+template <>
+struct Elem<HRT_BF16> {
+  using S = uint16_t;
+  __device__ static float get(const S* p) { return bf16_bits_to_f32(*p); }
+  __device__ static void put(S* p, float v) { *p = (uint16_t)f32_to_bf16_bits(v); }
+};
+template <>
+struct Elem<HRT_F16> {
+  using S = uint16_t;
+  __device__ static float get(const S* p) { return f16_bits_to_f32(*p); }
+  __device__ static void put(S* p, float v) { *p = (uint16_t)f32_to_f16_bits(v); }
+};
+
+template <int CODE>
+struct Raw;
+template <>
+struct Raw<HRT_RAW8> {
+  using S = uint8_t;
+};
+template <>
+struct Raw<HRT_RAW16> {
+  using S = uint16_t;
+};
+template <>
+struct Raw<HRT_RAW32> {
+  using S = uint32_t;
+};
+template <>
+struct Raw<HRT_RAW64> {
+  using S = uint64_t;
+};
+
+struct Shape {
+  int ndim;
+  int64_t sizes[HRT_MAX_DIMS];
+  int64_t s0[HRT_MAX_DIMS];  // dst strides
+  int64_t s1[HRT_MAX_DIMS];  // src strides
+};
+
+__device__ __forceinline__ void offsets(const Shape& sh, int64_t i, int64_t& o0, int64_t& o1) {
+  o0 = 0;
+  o1 = 0;
+  for (int d = sh.ndim - 1; d >= 0; --d) {
+    int64_t sz = sh.sizes[d];
+    int64_t q = i / sz;
+    int64_t r = i - q * sz;
+    o0 += r * sh.s0[d];
+    o1 += r * sh.s1[d];
+    i = q;
+  }
+}
+
+template <int DC, int SC>
+__global__ __launch_bounds__(256) void cast_nd(void* dst, const void* src, Shape sh, int64_t n) {
+  using DS = typename Elem<DC>::S;
+  using SS = typename Elem<SC>::S;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    int64_t od, os;
+    offsets(sh, i, od, os);
+    Elem<DC>::put((DS*)dst + od, Elem<SC>::get((const SS*)src + os));
+  }
+}
+
+// Contiguous 1-D cast, 4 elements per thread per step.
+template <int DC, int SC>
+__global__ __launch_bounds__(256) void cast_1d(void* dst, const void* src, int64_t n) {
+  using DS = typename Elem<DC>::S;
+  using SS = typename Elem<SC>::S;
+  const SS* s = (const SS*)src;
+  DS* d = (DS*)dst;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
+    if (i + 4 <= n) {
+      float v0 = Elem<SC>::get(s + i), v1 = Elem<SC>::get(s + i + 1), v2 = Elem<SC>::get(s + i + 2),
+            v3 = Elem<SC>::get(s + i + 3);
+      Elem<DC>::put(d + i, v0);
+      Elem<DC>::put(d + i + 1, v1);
+      Elem<DC>::put(d + i + 2, v2);
+      Elem<DC>::put(d + i + 3, v3);
+    } else {
+      for (int64_t j = i; j < n; ++j) Elem<DC>::put(d + j, Elem<SC>::get(s + j));
+    }
+  }
+}
+
+template <typename S>
+__global__ __launch_bounds__(256) void raw_nd(void* dst, const void* src, Shape sh, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    int64_t od, os;
+    offsets(sh, i, od, os);
+    ((S*)dst)[od] = ((const S*)src)[os];
+  }
+}
+
+template <typename S>
+__global__ __launch_bounds__(256) void fill_nd(void* dst, uint64_t bits, Shape sh, int64_t n) {
+  const S v = (S)bits;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    int64_t od, os;
+    offsets(sh, i, od, os);
+    ((S*)dst)[od] = v;
+  }
+}
+
+uint64_t elem_size(int code) {
+  switch (code) {
+    case HRT_F32: return 4;
+    case HRT_BF16: return 2;
+    case HRT_F16: return 2;
+    case HRT_RAW8: return 1;
+    case HRT_RAW16: return 2;
+    case HRT_RAW32: return 4;
+    case HRT_RAW64: return 8;
+    default: return 0;
+  }
+}
+
+uint32_t grid_for(int64_t n, int per_thread) {
+  int64_t g = cdiv(n, 256 * (int64_t)per_thread);
+  if (g > 16384) g = 16384;
+  if (g < 1) g = 1;
+  return (uint32_t)g;
+}
+
+template <int DC, int SC>
+void queue_cast(const hrt_copy_args& a, const Shape& sh, int64_t n, bool contig, hipStream_t s) {
+  if (contig)
+    hipLaunchKernelGGL((cast_1d<DC, SC>), dim3(grid_for(n, 4)), dim3(256), 0, s, (void*)a.dst, (const void*)a.src, n);
+  else
+    hipLaunchKernelGGL((cast_nd<DC, SC>), dim3(grid_for(n, 1)), dim3(256), 0, s, (void*)a.dst, (const void*)a.src, sh, n);
+}
+
+bool launch_copy(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_copy_args*>(p);
+  if (a.ndim < 0 || a.ndim > HRT_MAX_DIMS) return ctx.fail("ndim out of range");
+  const uint64_t de = elem_size(a.dst_dtype), se = elem_size(a.src_dtype);
+  if (!de || !se) return ctx.fail("unknown dtype code");
+  const bool dfloat = a.dst_dtype <= HRT_F16, sfloat = a.src_dtype <= HRT_F16;
+  if (!(dfloat && sfloat) && a.dst_dtype != a.src_dtype) return ctx.fail("raw copies need equal dtypes");
+  Shape sh{};
+  sh.ndim = a.ndim;
+  int64_t n = 1;
+  bool contig = true;
+  int64_t expect = 1;
+  for (int d = a.ndim - 1; d >= 0; --d) {
+    if (a.sizes[d] < 0 || a.dst_strides[d] < 0 || a.src_strides[d] < 0) return ctx.fail("negative size or stride");
+    sh.sizes[d] = a.sizes[d];
+    sh.s0[d] = a.dst_strides[d];
+    sh.s1[d] = a.src_strides[d];
+    if (a.sizes[d] != 1 && (a.dst_strides[d] != expect || a.src_strides[d] != expect)) contig = false;
+    expect *= a.sizes[d];
+    n *= a.sizes[d];
+  }
+  if (n == 0) return true;
+  if (!ctx.check(a.dst, hrt::span_bytes(a.ndim, a.sizes, a.dst_strides, de), "dst") ||
+      !ctx.check(a.src, hrt::span_bytes(a.ndim, a.sizes, a.src_strides, se), "src"))
+    return false;
+  hipStream_t s = ctx.stream;
+  if (dfloat && sfloat && a.dst_dtype != a.src_dtype) {
+    switch (a.dst_dtype * 3 + a.src_dtype) {
+      case HRT_F32 * 3 + HRT_BF16: queue_cast<HRT_F32, HRT_BF16>(a, sh, n, contig, s); break;
+      case HRT_F32 * 3 + HRT_F16: queue_cast<HRT_F32, HRT_F16>(a, sh, n, contig, s); break;
+      case HRT_BF16 * 3 + HRT_F32: queue_cast<HRT_BF16, HRT_F32>(a, sh, n, contig, s); break;
+      case HRT_BF16 * 3 + HRT_F16: queue_cast<HRT_BF16, HRT_F16>(a, sh, n, contig, s); break;
+      case HRT_F16 * 3 + HRT_F32: queue_cast<HRT_F16, HRT_F32>(a, sh, n, contig, s); break;
+      case HRT_F16 * 3 + HRT_BF16: queue_cast<HRT_F16, HRT_BF16>(a, sh, n, contig, s); break;
+      default: return ctx.fail("unsupported cast");
+    }
+  } else {
+    dim3 g(grid_for(n, 1));
+    switch (de) {
+      case 1: hipLaunchKernelGGL(raw_nd<uint8_t>, g, dim3(256), 0, s, (void*)a.dst, (const void*)a.src, sh, n); break;
+      case 2: hipLaunchKernelGGL(raw_nd<uint16_t>, g, dim3(256), 0, s, (void*)a.dst, (const void*)a.src, sh, n); break;
+      case 4: hipLaunchKernelGGL(raw_nd<uint32_t>, g, dim3(256), 0, s, (void*)a.dst, (const void*)a.src, sh, n); break;
+      default: hipLaunchKernelGGL(raw_nd<uint64_t>, g, dim3(256), 0, s, (void*)a.dst, (const void*)a.src, sh, n); break;
+    }
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "ew_copy");
+}
+HRT_REGISTER("ew_copy", hrt_copy_args, launch_copy);
+
+bool launch_fill(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_fill_args*>(p);
+  if (a.ndim < 0 || a.ndim > HRT_MAX_DIMS) return ctx.fail("ndim out of range");
+  const uint64_t es = elem_size(a.dtype);
+  if (!es) return ctx.fail("unknown dtype code");
+  Shape sh{};
+  sh.ndim = a.ndim;
+  int64_t n = 1;
+  for (int d = 0; d < a.ndim; ++d) {
+    if (a.sizes[d] < 0 || a.strides[d] < 0) return ctx.fail("negative size or stride");
+    sh.sizes[d] = a.sizes[d];
+    sh.s0[d] = a.strides[d];
+    sh.s1[d] = 0;
+    n *= a.sizes[d];
+  }
+  if (n == 0) return true;
+  if (!ctx.check(a.dst, hrt::span_bytes(a.ndim, a.sizes, a.strides, es), "dst")) return false;
+  dim3 g(grid_for(n, 1));
+  switch (es) {
+    case 1: hipLaunchKernelGGL(fill_nd<uint8_t>, g, dim3(256), 0, ctx.stream, (void*)a.dst, a.value_bits, sh, n); break;
+    case 2: hipLaunchKernelGGL(fill_nd<uint16_t>, g, dim3(256), 0, ctx.stream, (void*)a.dst, a.value_bits, sh, n); break;
+    case 4: hipLaunchKernelGGL(fill_nd<uint32_t>, g, dim3(256), 0, ctx.stream, (void*)a.dst, a.value_bits, sh, n); break;
+    default: hipLaunchKernelGGL(fill_nd<uint64_t>, g, dim3(256), 0, ctx.stream, (void*)a.dst, a.value_bits, sh, n); break;
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "ew_fill");
+}
+HRT_REGISTER("ew_fill", hrt_fill_args, launch_fill);
+
+}  // namespace
+}  // namespace hk

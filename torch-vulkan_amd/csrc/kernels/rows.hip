@@ -1,0 +1,624 @@
+// Row kernels: softmax forward/backward and layer_norm forward/backward/weight-gradient.
+// Reference algorithms: vkrt/shaders/softmax.comp.in:27-50 and vkrt/shaders/ln.comp.in:1-84 (fp32 math,
+// max-subtracted softmax, two-pass variance, fp32 statistics).
+//
+// All of them are HBM-bound (a few flops per byte).  The main path keeps a whole row in registers: one
+// 64-lane wavefront per row, 16-byte vector loads (4 fp32 / 8 bf16 per lane per vector), wavefront
+// shuffle reductions, so every element is read from HBM exactly once and written once; four rows per
+// 256-thread workgroup.  Rows that are too long for registers, misaligned, or softmaxes over a
+// non-innermost dimension take a generic multi-pass path.
+#include <cmath>
+
+#include "../hrt/registry.h"
+#include "device_common.h"
+
+namespace hk {
+namespace {
+
+constexpr int kMaxNV = 8;  // 16-byte vectors per lane on the register path
+
+// Load / store 16 bytes as float values.
+template <typename T>
+struct Vec;
+template <>
+struct Vec<F32> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void load(const float* p, float* v) {
+    f32x4 w = *reinterpret_cast<const f32x4*>(p);
+    v[0] = w.x, v[1] = w.y, v[2] = w.z, v[3] = w.w;
+  }
+  __device__ __forceinline__ static void store(float* p, const float* v) {
+    f32x4 w = {v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p) = w;
+  }
+};
+template <typename T16>
+struct Vec16 {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void load(const uint16_t* p, float* v) {
+    u32x4 w = *reinterpret_cast<const u32x4*>(p);
+    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = lo16<T16>(a[i]);
+      v[2 * i + 1] = hi16<T16>(a[i]);
+    }
+  }
+  __device__ __forceinline__ static void store(uint16_t* p, const float* v) {
+    u32x4 w;
+    w.x = pack2<T16>(v[0], v[1]);
+    w.y = pack2<T16>(v[2], v[3]);
+    w.z = pack2<T16>(v[4], v[5]);
+    w.w = pack2<T16>(v[6], v[7]);
+    *reinterpret_cast<u32x4*>(p) = w;
+  }
+};
+template <>
+struct Vec<BF16> : Vec16<BF16> {};
+template <>
+struct Vec<F16> : Vec16<F16> {};
+
+template <typename T>
+__device__ __forceinline__ float ld(const typename T::storage* p, int64_t i) {
+  return T::to_f32(p[i]);
+}
+
+// ================================ softmax ================================================================
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage* __restrict__ x,
+                                                       typename T::storage* __restrict__ y, int64_t rows, int64_t R,
+                                                       uint32_t safe) {
+  constexpr int V = Vec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // no block barriers in this kernel
+  const typename T::storage* xr = x + row * R;
+  float v[NV][V];
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < R) {
+      Vec<T>::load(xr + col, v[c]);
+#pragma unroll
+      for (int e = 0; e < V; ++e) m = fmaxf(m, v[c][e]);
+    }
+  }
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < R) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        v[c][e] = expf(v[c][e] - m);
+        s += v[c][e];
+      }
+    }
+  }
+  s = wave_sum(s);
+  const bool zero = safe && m == -INFINITY;
+  typename T::storage* yr = y + row * R;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < R) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[c][e] = zero ? 0.f : v[c][e] / s;
+      Vec<T>::store(yr + col, v[c]);
+    }
+  }
+}
+
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void softmax_bwd_reg(const typename T::storage* __restrict__ y,
+                                                       const typename T::storage* __restrict__ g,
+                                                       typename T::storage* __restrict__ dx, int64_t rows, int64_t R) {
+  constexpr int V = Vec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float yv[NV][V], gv[NV][V];
+  float d = 0.f;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < R) {
+      Vec<T>::load(y + row * R + col, yv[c]);
+      Vec<T>::load(g + row * R + col, gv[c]);
+#pragma unroll
+      for (int e = 0; e < V; ++e) d += gv[c][e] * yv[c][e];
+    }
+  }
+  d = wave_sum(d);
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < R) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) yv[c][e] = yv[c][e] * (gv[c][e] - d);
+      Vec<T>::store(dx + row * R + col, yv[c]);
+    }
+  }
+}
+
+// Generic softmax, inner == 1: one workgroup per row, online max/sum pass then a write pass.
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_fwd_row(const typename T::storage* __restrict__ x,
+                                                       typename T::storage* __restrict__ y, int64_t R, uint32_t safe) {
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * R;
+  float m = -INFINITY, s = 0.f;
+  for (int64_t r = threadIdx.x; r < R; r += 256) {
+    const float v = ld<T>(x, base + r);
+    if (v > m) {
+      s = s * expf(m - v) + 1.f;  // m == -inf: expf(-inf) = 0
+      m = v;
+    } else {
+      s += expf(v - m);
+    }
+  }
+  const float mall = block_max<4>(m, red);
+  s = (m == -INFINITY) ? 0.f : s * expf(m - mall);
+  const float sall = block_sum<4>(s, red);
+  const bool zero = safe && mall == -INFINITY;
+  for (int64_t r = threadIdx.x; r < R; r += 256) {
+    const float v = ld<T>(x, base + r);
+    y[base + r] = T::from_f32(zero ? 0.f : expf(v - mall) / sall);
+  }
+}
+
+// Generic softmax over a non-innermost dimension: one thread per (outer, inner) column; consecutive
+// threads read consecutive inner positions, so every pass over R is coalesced.
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_fwd_col(const typename T::storage* __restrict__ x,
+                                                       typename T::storage* __restrict__ y, int64_t outer, int64_t R,
+                                                       int64_t inner, uint32_t safe) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= outer * inner) return;
+  const int64_t o = t / inner, i = t - o * inner;
+  const int64_t base = o * R * inner + i;
+  float m = -INFINITY;
+  for (int64_t r = 0; r < R; ++r) m = fmaxf(m, ld<T>(x, base + r * inner));
+  float s = 0.f;
+  for (int64_t r = 0; r < R; ++r) s += expf(ld<T>(x, base + r * inner) - m);
+  const bool zero = safe && m == -INFINITY;
+  for (int64_t r = 0; r < R; ++r) {
+    const float v = ld<T>(x, base + r * inner);
+    y[base + r * inner] = T::from_f32(zero ? 0.f : expf(v - m) / s);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_bwd_generic(const typename T::storage* __restrict__ y,
+                                                           const typename T::storage* __restrict__ g,
+                                                           typename T::storage* __restrict__ dx, int64_t outer, int64_t R,
+                                                           int64_t inner) {
+  if (inner == 1) {
+    __shared__ float red[4];
+    const int64_t base = (int64_t)blockIdx.x * R;
+    float d = 0.f;
+    for (int64_t r = threadIdx.x; r < R; r += 256) d += ld<T>(g, base + r) * ld<T>(y, base + r);
+    d = block_sum<4>(d, red);
+    for (int64_t r = threadIdx.x; r < R; r += 256) {
+      const float yv = ld<T>(y, base + r);
+      dx[base + r] = T::from_f32(yv * (ld<T>(g, base + r) - d));
+    }
+    return;
+  }
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= outer * inner) return;
+  const int64_t o = t / inner, i = t - o * inner;
+  const int64_t base = o * R * inner + i;
+  float d = 0.f;
+  for (int64_t r = 0; r < R; ++r) d += ld<T>(g, base + r * inner) * ld<T>(y, base + r * inner);
+  for (int64_t r = 0; r < R; ++r) {
+    const float yv = ld<T>(y, base + r * inner);
+    dx[base + r * inner] = T::from_f32(yv * (ld<T>(g, base + r * inner) - d));
+  }
+}
+
+template <typename T>
+int reg_nv(int64_t R, std::initializer_list<uint64_t> ptrs) {
+  constexpr int V = Vec<T>::N;
+  if (R % V != 0 || R > 64 * V * kMaxNV) return 0;
+  for (uint64_t p : ptrs)
+    if (p % 16 != 0) return 0;
+  int nv = 1;
+  while (64 * V * nv < R) nv *= 2;
+  return nv;
+}
+
+template <typename T>
+bool launch_softmax_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_softmax_args*>(p);
+  if (a.outer < 0 || a.R < 0 || a.inner < 0) return ctx.fail("negative shape");
+  const int64_t n = a.outer * a.R * a.inner;
+  if (n == 0) return true;
+  const uint64_t bytes = (uint64_t)n * sizeof(typename T::storage);
+  if (!ctx.check(a.x, bytes, "x") || !ctx.check(a.y, bytes, "y")) return false;
+  using S = typename T::storage;
+  const S* x = (const S*)a.x;
+  S* y = (S*)a.y;
+  if (a.inner == 1) {
+    const int nv = reg_nv<T>(a.R, {a.x, a.y});
+    const dim3 g((uint32_t)cdiv(a.outer, 4));
+    switch (nv) {
+      case 1: hipLaunchKernelGGL((softmax_fwd_reg<T, 1>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      case 2: hipLaunchKernelGGL((softmax_fwd_reg<T, 2>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      case 4: hipLaunchKernelGGL((softmax_fwd_reg<T, 4>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      case 8: hipLaunchKernelGGL((softmax_fwd_reg<T, 8>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      default:
+        hipLaunchKernelGGL(softmax_fwd_row<T>, dim3((uint32_t)a.outer), dim3(256), 0, ctx.stream, x, y, a.R, a.safe);
+    }
+  } else {
+    hipLaunchKernelGGL(softmax_fwd_col<T>, dim3((uint32_t)cdiv(a.outer * a.inner, 256)), dim3(256), 0, ctx.stream, x, y,
+                       a.outer, a.R, a.inner, a.safe);
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "softmax_fwd");
+}
+
+template <typename T>
+bool launch_softmax_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_softmax_args*>(p);
+  if (a.outer < 0 || a.R < 0 || a.inner < 0) return ctx.fail("negative shape");
+  const int64_t n = a.outer * a.R * a.inner;
+  if (n == 0) return true;
+  const uint64_t bytes = (uint64_t)n * sizeof(typename T::storage);
+  if (!ctx.check(a.y, bytes, "y") || !ctx.check(a.g, bytes, "g") || !ctx.check(a.dx, bytes, "dx")) return false;
+  using S = typename T::storage;
+  const S *y = (const S*)a.y, *g = (const S*)a.g;
+  S* dx = (S*)a.dx;
+  const int nv = a.inner == 1 ? reg_nv<T>(a.R, {a.y, a.g, a.dx}) : 0;
+  const dim3 g4((uint32_t)cdiv(a.outer, 4));
+  switch (nv) {
+    case 1: hipLaunchKernelGGL((softmax_bwd_reg<T, 1>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    case 2: hipLaunchKernelGGL((softmax_bwd_reg<T, 2>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    case 4: hipLaunchKernelGGL((softmax_bwd_reg<T, 4>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    case 8: hipLaunchKernelGGL((softmax_bwd_reg<T, 8>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    default: {
+      const dim3 grid(a.inner == 1 ? (uint32_t)a.outer : (uint32_t)cdiv(a.outer * a.inner, 256));
+      hipLaunchKernelGGL(softmax_bwd_generic<T>, grid, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R, a.inner);
+    }
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "softmax_bwd");
+}
+
+// ================================ layer_norm ============================================================
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __restrict__ x,
+                                                  typename T::storage* __restrict__ y, float* __restrict__ mean_out,
+                                                  float* __restrict__ rstd_out, const typename T::storage* __restrict__ w,
+                                                  const typename T::storage* __restrict__ b, int64_t rows, int64_t D,
+                                                  float eps) {
+  constexpr int V = Vec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float v[NV][V];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < D) {
+      Vec<T>::load(x + row * D + col, v[c]);
+#pragma unroll
+      for (int e = 0; e < V; ++e) s += v[c][e];
+    }
+  }
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < D) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const float d = v[c][e] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) / (float)D;
+  const float rstd = 1.f / sqrtf(var + eps);
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < D) {
+      float wv[V], bv[V];
+      if (w) Vec<T>::load(w + col, wv);
+      if (b) Vec<T>::load(b + col, bv);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float o = (v[c][e] - mean) * rstd;
+        if (w) o *= wv[e];
+        if (b) o += bv[e];
+        v[c][e] = o;
+      }
+      Vec<T>::store(y + row * D + col, v[c]);
+    }
+  }
+  if (lane == 0) {
+    mean_out[row] = mean;
+    rstd_out[row] = rstd;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void ln_fwd_row(const typename T::storage* __restrict__ x, typename T::storage* __restrict__ y,
+                                                  float* __restrict__ mean_out, float* __restrict__ rstd_out,
+                                                  const typename T::storage* __restrict__ w,
+                                                  const typename T::storage* __restrict__ b, int64_t D, float eps) {
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * D;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < D; i += 256) s += ld<T>(x, base + i);
+  const float mean = block_sum<4>(s, red) / (float)D;
+  float q = 0.f;
+  for (int64_t i = threadIdx.x; i < D; i += 256) {
+    const float d = ld<T>(x, base + i) - mean;
+    q += d * d;
+  }
+  const float var = block_sum<4>(q, red) / (float)D;
+  const float rstd = 1.f / sqrtf(var + eps);
+  for (int64_t i = threadIdx.x; i < D; i += 256) {
+    float o = (ld<T>(x, base + i) - mean) * rstd;
+    if (w) o *= ld<T>(w, i);
+    if (b) o += ld<T>(b, i);
+    y[base + i] = T::from_f32(o);
+  }
+  if (threadIdx.x == 0) {
+    mean_out[blockIdx.x] = mean;
+    rstd_out[blockIdx.x] = rstd;
+  }
+}
+
+// Backward, register path: workgroup = one chunk of 4 rows, one wavefront per row.  dx per row;
+// the per-column partial sums of g*xhat and g of the 4 rows are combined in LDS and written as one
+// ws row pair per chunk.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __restrict__ x,
+                                                  const typename T::storage* __restrict__ g,
+                                                  const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+                                                  const typename T::storage* __restrict__ w,
+                                                  typename T::storage* __restrict__ dx, float* __restrict__ ws, int64_t rows,
+                                                  int64_t D) {
+  constexpr int V = Vec<T>::N;
+  extern __shared__ float part[];  // [2][D] when ws != nullptr
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  const bool live = row < rows;
+  float xh[NV][V], gv[NV][V];
+  float s1 = 0.f, s2 = 0.f, mean = 0.f, rstd = 0.f;
+  if (live) {
+    mean = mean_in[row];
+    rstd = rstd_in[row];
+  }
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (live && col < D) {
+      float wv[V];
+      Vec<T>::load(x + row * D + col, xh[c]);
+      Vec<T>::load(g + row * D + col, gv[c]);
+      if (w) Vec<T>::load(w + col, wv);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        xh[c][e] = (xh[c][e] - mean) * rstd;
+        const float gw = w ? gv[c][e] * wv[e] : gv[c][e];
+        s1 += gw;
+        s2 += gw * xh[c][e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) xh[c][e] = gv[c][e] = 0.f;
+    }
+  }
+  s1 = wave_sum(s1) / (float)D;
+  s2 = wave_sum(s2) / (float)D;
+  if (dx && live) {
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+      const int64_t col = (int64_t)(c * 64 + lane) * V;
+      if (col < D) {
+        float wv[V], o[V];
+        if (w) Vec<T>::load(w + col, wv);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float gw = w ? gv[c][e] * wv[e] : gv[c][e];
+          o[e] = rstd * (gw - s1 - xh[c][e] * s2);
+        }
+        Vec<T>::store(dx + row * D + col, o);
+      }
+    }
+  }
+  if (!ws) return;  // uniform across the workgroup: no barrier below is skipped by only some waves
+  for (int step = 0; step < 4; ++step) {
+    if (wave == step) {
+#pragma unroll
+      for (int c = 0; c < NV; ++c) {
+        const int64_t col = (int64_t)(c * 64 + lane) * V;
+        if (col < D) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const float pw = gv[c][e] * xh[c][e], pb = gv[c][e];
+            if (step == 0) {
+              part[col + e] = pw;
+              part[D + col + e] = pb;
+            } else {
+              part[col + e] += pw;
+              part[D + col + e] += pb;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  float* out = ws + (int64_t)blockIdx.x * 2 * D;
+  for (int64_t i = threadIdx.x; i < 2 * D; i += 256) out[i] = part[i];
+}
+
+// Backward, generic path: workgroup per chunk of 4 rows; ws accumulated in place (each thread owns its
+// columns, so the read-modify-write has no races).
+template <typename T>
+__global__ __launch_bounds__(256) void ln_bwd_row(const typename T::storage* __restrict__ x, const typename T::storage* __restrict__ g,
+                                                  const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+                                                  const typename T::storage* __restrict__ w, typename T::storage* __restrict__ dx,
+                                                  float* __restrict__ ws, int64_t rows, int64_t D) {
+  __shared__ float red[4];
+  float* pw = ws ? ws + (int64_t)blockIdx.x * 2 * D : nullptr;
+  for (int rr = 0; rr < 4; ++rr) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + rr;
+    if (row >= rows) {
+      if (pw && rr == 0)
+        for (int64_t i = threadIdx.x; i < 2 * D; i += 256) pw[i] = 0.f;
+      continue;
+    }
+    const float mean = mean_in[row], rstd = rstd_in[row];
+    const int64_t base = row * D;
+    float s1 = 0.f, s2 = 0.f;
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+      const float xh = (ld<T>(x, base + i) - mean) * rstd;
+      const float gv = ld<T>(g, base + i);
+      const float gw = w ? gv * ld<T>(w, i) : gv;
+      s1 += gw;
+      s2 += gw * xh;
+    }
+    s1 = block_sum<4>(s1, red) / (float)D;
+    s2 = block_sum<4>(s2, red) / (float)D;
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+      const float xh = (ld<T>(x, base + i) - mean) * rstd;
+      const float gv = ld<T>(g, base + i);
+      const float gw = w ? gv * ld<T>(w, i) : gv;
+      if (dx) dx[base + i] = T::from_f32(rstd * (gw - s1 - xh * s2));
+      if (pw) {
+        if (rr == 0) {
+          pw[i] = gv * xh;
+          pw[D + i] = gv;
+        } else {
+          pw[i] += gv * xh;
+          pw[D + i] += gv;
+        }
+      }
+    }
+  }
+}
+
+// dw[d] = sum_c ws[c][0][d], db[d] = sum_c ws[c][1][d]: 64 columns x 4 chunk groups per workgroup.
+template <typename T>
+__global__ __launch_bounds__(256) void ln_wgrad_reduce(const float* __restrict__ ws, typename T::storage* __restrict__ dw,
+                                                       typename T::storage* __restrict__ db, int64_t chunks, int64_t D) {
+  __shared__ float sw[4][64], sb[4][64];
+  const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + cl;
+  float aw = 0.f, ab = 0.f;
+  if (col < D) {
+    for (int64_t c = grp; c < chunks; c += 4) {
+      aw += ws[c * 2 * D + col];
+      ab += ws[c * 2 * D + D + col];
+    }
+  }
+  sw[grp][cl] = aw;
+  sb[grp][cl] = ab;
+  __syncthreads();
+  if (grp == 0 && col < D) {
+    const float tw = sw[0][cl] + sw[1][cl] + sw[2][cl] + sw[3][cl];
+    const float tb = sb[0][cl] + sb[1][cl] + sb[2][cl] + sb[3][cl];
+    if (dw) dw[col] = T::from_f32(tw);
+    if (db) db[col] = T::from_f32(tb);
+  }
+}
+
+template <typename T>
+bool launch_ln_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_ln_args*>(p);
+  if (a.rows < 0 || a.D <= 0) return ctx.fail("bad shape");
+  if (a.rows == 0) return true;
+  using S = typename T::storage;
+  const uint64_t bytes = (uint64_t)(a.rows * a.D) * sizeof(S);
+  if (!ctx.check(a.x, bytes, "x") || !ctx.check(a.y, bytes, "y") || !ctx.check(a.mean, a.rows * 4, "mean") ||
+      !ctx.check(a.rstd, a.rows * 4, "rstd") || (a.w && !ctx.check(a.w, a.D * sizeof(S), "w")) ||
+      (a.b && !ctx.check(a.b, a.D * sizeof(S), "b")))
+    return false;
+  const S *x = (const S*)a.x, *w = (const S*)a.w, *b = (const S*)a.b;
+  S* y = (S*)a.y;
+  float *mu = (float*)a.mean, *rs = (float*)a.rstd;
+  const int nv = reg_nv<T>(a.D, {a.x, a.y, a.w, a.b});
+  const dim3 g4((uint32_t)cdiv(a.rows, 4));
+  switch (nv) {
+    case 1: hipLaunchKernelGGL((ln_fwd_reg<T, 1>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 2: hipLaunchKernelGGL((ln_fwd_reg<T, 2>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 4: hipLaunchKernelGGL((ln_fwd_reg<T, 4>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 8: hipLaunchKernelGGL((ln_fwd_reg<T, 8>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    default:
+      hipLaunchKernelGGL(ln_fwd_row<T>, dim3((uint32_t)a.rows), dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.D, a.eps);
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "ln_fwd");
+}
+
+template <typename T>
+bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_ln_args*>(p);
+  if (a.rows < 0 || a.D <= 0) return ctx.fail("bad shape");
+  if (a.rows == 0) return true;
+  if (hrt_ln_rows_per_chunk(a.rows) != 4) return ctx.fail("ln chunking mismatch");
+  using S = typename T::storage;
+  const uint64_t bytes = (uint64_t)(a.rows * a.D) * sizeof(S);
+  const int64_t chunks = hrt_ln_chunks(a.rows);
+  if (!ctx.check(a.x, bytes, "x") || !ctx.check(a.g, bytes, "g") || !ctx.check(a.mean, a.rows * 4, "mean") ||
+      !ctx.check(a.rstd, a.rows * 4, "rstd") || (a.w && !ctx.check(a.w, a.D * sizeof(S), "w")) ||
+      (a.dx && !ctx.check(a.dx, bytes, "dx")) || (a.ws && !ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws")))
+    return false;
+  const S *x = (const S*)a.x, *g = (const S*)a.g, *w = (const S*)a.w;
+  S* dx = (S*)a.dx;
+  float* ws = (float*)a.ws;
+  const float *mu = (const float*)a.mean, *rs = (const float*)a.rstd;
+  int nv = reg_nv<T>(a.D, {a.x, a.g, a.w, a.dx});
+  const size_t lds = ws ? (size_t)(2 * a.D) * 4 : 0;
+  if (lds > 64 * 1024) nv = 0;
+  const dim3 grid((uint32_t)chunks);
+  switch (nv) {
+    case 1: hipLaunchKernelGGL((ln_bwd_reg<T, 1>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 2: hipLaunchKernelGGL((ln_bwd_reg<T, 2>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 4: hipLaunchKernelGGL((ln_bwd_reg<T, 4>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 8: hipLaunchKernelGGL((ln_bwd_reg<T, 8>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    default: hipLaunchKernelGGL(ln_bwd_row<T>, grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "ln_bwd");
+}
+
+template <typename T>
+bool launch_ln_wgrad(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_ln_args*>(p);
+  if (a.rows <= 0 || a.D <= 0) return ctx.fail("bad shape");
+  if (!a.dw && !a.db) return true;
+  using S = typename T::storage;
+  const int64_t chunks = hrt_ln_chunks(a.rows);
+  if (!ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws") || (a.dw && !ctx.check(a.dw, a.D * sizeof(S), "dw")) ||
+      (a.db && !ctx.check(a.db, a.D * sizeof(S), "db")))
+    return false;
+  hipLaunchKernelGGL(ln_wgrad_reduce<T>, dim3((uint32_t)cdiv(a.D, 64)), dim3(256), 0, ctx.stream, (const float*)a.ws,
+                     (S*)a.dw, (S*)a.db, chunks, a.D);
+  return hrt::launch_ok(hipGetLastError(), ctx, "ln_wgrad");
+}
+
+HRT_REGISTER("softmax_fwd_f32", hrt_softmax_args, launch_softmax_fwd<F32>);
+HRT_REGISTER("softmax_fwd_bf16", hrt_softmax_args, launch_softmax_fwd<BF16>);
+HRT_REGISTER("softmax_fwd_f16", hrt_softmax_args, launch_softmax_fwd<F16>);
+HRT_REGISTER("softmax_bwd_f32", hrt_softmax_args, launch_softmax_bwd<F32>);
+HRT_REGISTER("softmax_bwd_bf16", hrt_softmax_args, launch_softmax_bwd<BF16>);
+HRT_REGISTER("softmax_bwd_f16", hrt_softmax_args, launch_softmax_bwd<F16>);
+HRT_REGISTER("ln_fwd_f32", hrt_ln_args, launch_ln_fwd<F32>);
+HRT_REGISTER("ln_fwd_bf16", hrt_ln_args, launch_ln_fwd<BF16>);
+HRT_REGISTER("ln_fwd_f16", hrt_ln_args, launch_ln_fwd<F16>);
+HRT_REGISTER("ln_bwd_f32", hrt_ln_args, launch_ln_bwd<F32>);
+HRT_REGISTER("ln_bwd_bf16", hrt_ln_args, launch_ln_bwd<BF16>);
+HRT_REGISTER("ln_bwd_f16", hrt_ln_args, launch_ln_bwd<F16>);
+HRT_REGISTER("ln_wgrad_f32", hrt_ln_args, launch_ln_wgrad<F32>);
+HRT_REGISTER("ln_wgrad_bf16", hrt_ln_args, launch_ln_wgrad<BF16>);
+HRT_REGISTER("ln_wgrad_f16", hrt_ln_args, launch_ln_wgrad<F16>);
+
+}  // namespace
+}  // namespace hk

@@ -1,0 +1,294 @@
+"""MI355X-native "vk" device for PyTorch: the torch_vulkan API over HIP and hand-written gfx950 kernels.
+
+`import torch_vulkan` loads the C++ shim (which registers the PrivateUse1 operators: mm/bmm/addmm/
+baddbmm, fused SDPA forward+backward, softmax (+backward, _safe_softmax), layer_norm (+backward), copies
+and fills), renames PrivateUse1 to "vk" and installs the `torch.vk` module, so training code written for
+the reference `torch_vulkan` package (torch_vulkan/__init__.py:1-270) runs unchanged: tensors move with
+`.to("vk")`, every other op falls back to the CPU, and the counters below report which path ran.
+
+The native libraries are built in-tree by `torch-vulkan_amd/build.py`; there is no pure-Python
+substitute, so a missing build is an ImportError.
+"""
+
+import importlib
+import os
+import sys
+import types
+
+import torch
+
+_THIS_DIR = os.path.dirname(os.path.abspath(__file__))
+
+
+def _load_extension():
+    if _THIS_DIR not in sys.path:
+        sys.path.insert(0, _THIS_DIR)
+    try:
+        return importlib.import_module("torch_vulkan_C")
+    except ImportError as e:  # no silent fallback: the device does not exist without its native code
+        raise ImportError(
+            f"torch_vulkan: the native extension is not built ({e}); run `python torch-vulkan_amd/build.py`"
+        ) from e
+
+
+_C = _load_extension()
+
+
+def is_available() -> bool:
+    return True
+
+
+def device_count() -> int:
+    return 1
+
+
+def current_device() -> int:
+    return 0
+
+
+def set_device(device) -> None:
+    return None
+
+
+def synchronize(device=None) -> None:
+    _C.synchronize()
+
+
+def device_name() -> str:
+    return _C.device_name()
+
+
+def live_bytes() -> int:
+    return _C.live_bytes()
+
+
+def memory_info() -> dict:
+    """Device memory in bytes: budget (what this process can still reach: free + own reservation), usage
+    (all processes) and heap (device total)."""
+    budget, usage, heap = _C.memory_info()
+    return {"budget": budget, "usage": usage, "heap": heap}
+
+
+def peak_live_bytes() -> int:
+    """High-water mark of live device bytes since reset_peak_live_bytes()."""
+    return _C.peak_live_bytes()
+
+
+def reset_peak_live_bytes() -> None:
+    _C.reset_peak_live_bytes()
+
+
+def set_memory_limit(megabytes: int) -> None:
+    """Cap the device memory reserved by this process (MiB, 0 = no cap); exceeding it raises an OOM
+    RuntimeError.  Also settable with VKT_MEM_LIMIT_MB at import time."""
+    _C.set_memory_limit(int(megabytes) << 20)
+
+
+def set_fused_attention(mode: str) -> None:
+    """Policy of the fused F.scaled_dot_product_attention: "auto" (default), "on" or "off".  auto uses it
+    for bf16/f16 and, for f32, when the score matrix would be >= 256 MiB.  Env: VKT_FUSED_ATTN=0/1."""
+    _C.set_fused_attention({"off": 0, "on": 1, "auto": 2}[mode])
+
+
+def kernel_counts() -> dict:
+    return dict(_C.kernel_counts())
+
+
+def validation_errors() -> int:
+    return _C.validation_errors()
+
+
+def empty_cache() -> None:
+    _C.empty_cache()
+
+
+def reserved_bytes() -> int:
+    return _C.reserved_bytes()
+
+
+def live_blocks() -> int:
+    return _C.live_blocks()
+
+
+def slab_count() -> int:
+    return _C.slab_count()
+
+
+def manual_seed(seed: int) -> None:
+    # random numbers are drawn on the CPU and copied, as in the reference
+    return None
+
+
+def manual_seed_all(seed: int) -> None:
+    return None
+
+
+def seed() -> None:
+    return None
+
+
+def _is_in_bad_fork() -> bool:
+    return False
+
+
+def get_amp_supported_dtype():
+    return [torch.bfloat16, torch.float16]
+
+
+class device:  # noqa: N801  same name and use as torch.cuda.device
+    def __init__(self, device=None):
+        self.idx = device
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
+def get_rng_state(device="vk") -> torch.Tensor:
+    return torch.zeros(1, dtype=torch.uint8)
+
+
+def set_rng_state(new_state, device="vk") -> None:
+    return None
+
+
+def stats() -> dict:
+    return dict(_C.stats())
+
+
+def fallback_time_by_op() -> dict:
+    return dict(_C.fallback_time_by_op())
+
+
+def profile() -> str:
+    """Per-kernel GPU time ("name\\tms\\tcount" lines) when HRT_PROFILE=1 was set at start-up."""
+    return _C.profile()
+
+
+def _print_stats_at_exit():
+    st = stats()
+    print("\n[torch_vulkan stats] " + ", ".join(f"{k}={v:.3f}" for k, v in st.items()))
+    top = sorted(fallback_time_by_op().items(), key=lambda kv: -kv[1])[:8]
+    print("[torch_vulkan stats] top fallback time: " + ", ".join(f"{k}={v:.2f}s" for k, v in top))
+    if os.environ.get("HRT_PROFILE"):
+        rows = [r.split("\t") for r in profile().splitlines()]
+        total = sum(float(r[1]) for r in rows) or 1.0
+        print(f"[torch_vulkan profile] GPU time {total:.1f} ms")
+        for name, ms, n in rows[:18]:
+            print(f"[torch_vulkan profile] {name:34s} {float(ms):9.1f} ms {float(ms) / total * 100:5.1f}%  x{n}")
+    print("[torch_vulkan stats] top kernels: " + str(sorted(kernel_counts().items(), key=lambda kv: -kv[1])[:8]))
+
+
+if os.environ.get("VKT_STATS") or os.environ.get("HRT_PROFILE"):
+    import atexit
+
+    atexit.register(_print_stats_at_exit)
+
+
+def coop_caps() -> int:
+    """Matrix-core kernels available (bit0 = f16, bit1 = bf16): 3 on gfx950."""
+    return _C.coop_caps()
+
+
+def set_coop_enabled(on: bool) -> None:
+    """Switch the matrix-core (MFMA) kernels on/off; off routes bf16/f16 to the FMA kernels.
+    Env: VKT_NO_COOP=1."""
+    _C.set_coop_enabled(bool(on))
+
+
+def dequant_int8(q, scale, out_dtype=torch.bfloat16):
+    """Weight-only int8 dequant: out[r, c] = float(q[r, c]) * float(scale[r, c // 64]) rounded to out_dtype.
+
+    q: int8 [rows, cols]; scale: bfloat16 [rows, ceil(cols / 64)] (64-column blocks per row).  On vk
+    tensors this runs the dq8 kernel; CPU tensors get the same closed form in PyTorch, as the reference's
+    function does (torch_vulkan/__init__.py:193-205).
+    """
+    if q.device.type == "vk":
+        q = q if q.is_contiguous() else q.contiguous()
+        scale = scale if scale.is_contiguous() else scale.contiguous()
+        return _C.dequant_int8(q, scale, out_dtype)
+    cols = q.shape[1]
+    s = scale.float().repeat_interleave(64, dim=1)[:, :cols]
+    return (q.float() * s).to(out_dtype)
+
+
+def dequant_int8_linear(x, q, scale, bias=None):
+    """Fused int8 weight-only linear: x @ dequant_int8(q, scale, x.dtype).T (+ bias), x bf16/f16 on vk.
+
+    The dequantized weight never reaches memory; its values are bit-identical to dequant_int8's."""
+    if x.device.type != "vk":
+        raise RuntimeError("dequant_int8_linear: x must be a vk tensor")
+    q = q if q.is_contiguous() else q.contiguous()
+    scale = scale if scale.is_contiguous() else scale.contiguous()
+    return _C.dequant_int8_linear(x, q, scale, bias)
+
+
+def event_record(slot: int) -> None:
+    """Record HIP event `slot` (0..15) on the runtime's stream (the stream every vk kernel runs on)."""
+    _C.event_record(int(slot))
+
+
+def event_elapsed_ms(start_slot: int, end_slot: int) -> float:
+    """Milliseconds between two recorded slots (waits for the later one)."""
+    return _C.event_elapsed_ms(int(start_slot), int(end_slot))
+
+
+def fallback_counts() -> dict:
+    return dict(_C.fallback_counts())
+
+
+def reset_fallback_counts() -> None:
+    _C.reset_counts()
+
+
+def _register():
+    # Keep nn.Parameter identity when modules move to vk (optimizers built before .to() keep working).
+    torch.__future__.set_swap_module_params_on_conversion(True)
+    # "vulkan" is taken by PyTorch's own inference backend, hence "vk".
+    torch.utils.rename_privateuse1_backend("vk")
+    module = types.ModuleType("torch.vk")
+    for name in (
+        "is_available",
+        "device_count",
+        "current_device",
+        "set_device",
+        "synchronize",
+        "empty_cache",
+        "manual_seed",
+        "manual_seed_all",
+        "seed",
+        "_is_in_bad_fork",
+        "get_amp_supported_dtype",
+        "device",
+        "get_rng_state",
+        "set_rng_state",
+        "memory_info",
+        "set_memory_limit",
+        "peak_live_bytes",
+        "reset_peak_live_bytes",
+    ):
+        setattr(module, name, globals()[name])
+    torch._register_device_module("vk", module)
+
+
+_register()
+
+
+def set_coop_range(lo: int = 0, hi: int = 2**64 - 1, kind: int = 0) -> None:
+    """Debug: only matrix-core-eligible GEMM calls numbered [lo, hi) use MFMA (others the FMA kernel);
+    kind 0 = all, 1 = bmm only, 2 = mm only.  For bisecting a bad call."""
+    _C.set_coop_range(int(lo), int(hi), int(kind))
+
+
+def reset_coop_calls() -> None:
+    _C.reset_coop_calls()
+
+
+def coop_calls() -> int:
+    return _C.coop_calls()
+
+
+if os.environ.get("VKT_MEM_LIMIT_MB"):
+    set_memory_limit(int(os.environ["VKT_MEM_LIMIT_MB"]))
