@@ -1,0 +1,381 @@
+// Matrix-core GEMM "mm_mfma_{bf16,f16}" for gfx950:  c = alpha * a @ b + beta * bias, fp32 accumulate.
+//
+// Same contract as the reference's cooperative-matrix kernel (vkrt/shaders/mm_coop.comp.in:96-208):
+// arbitrary strides (transposes and slices read in place), batched, bias broadcast through strides,
+// epilogue alpha*acc + beta*bias with one rounding.  Built for CDNA4 instead of translated:
+//   * v_mfma_f32_16x16x32 on 64-wide wavefronts; each wavefront owns a (BM/WM) x (BN/WN) sub-tile held
+//     in accumulator registers for the whole K loop;
+//   * A and B tiles are staged through LDS with K contiguous (+8 halves of row padding against bank
+//     conflicts), double-buffered, one barrier per K step; the next tile's global loads are issued
+//     before the current tile's MFMAs so HBM/L2 latency overlaps the math;
+//   * global loads are 128-bit along the operand's contiguous axis: a K-contiguous operand goes straight
+//     to its LDS row, an M-/N-contiguous one (W for dX = dY W, B of a row-major X @ B) is loaded as 8x8
+//     blocks and transposed in registers before the 128-bit LDS store — no copies, no strided LDS writes;
+//   * odd shapes / strides / alignments use a per-element gather loader on the same MMA core;
+//   * tiles are numbered N-fastest so the default round-robin placement of workgroups over the 8 XCDs
+//     gives each XCD a band of N-panels that it reads once into its own L2.
+#include "../hrt/registry.h"
+#include "mfma_common.h"
+
+namespace hk {
+
+bool mm_check_operands(const hrt_mm_args& a, uint64_t elem, hrt::LaunchCtx& ctx);
+
+namespace {
+
+enum LoadMode { KVEC = 0, MNVEC = 1, GATHER = 2 };
+
+constexpr int BK = 64;       // K per LDS stage
+constexpr int LDK = BK + 8;  // padded LDS row (halves)
+
+template <int ROWS, int MODE>
+struct TileLoader {
+  // The ROWS x BK tile of an operand whose element (r, k) is at p[r * s_r + k * s_k]; rows >= nrows and
+  // k >= nk read as zero.  load() fills registers, store() writes LDS as [ROWS][LDK] with K contiguous.
+  static constexpr int CHUNKS = ROWS * BK / 8;  // 16-byte chunks per tile
+  static constexpr int PER_THREAD_V = CHUNKS / 256 > 0 ? CHUNKS / 256 : 1;
+  static constexpr int BLOCKS = (ROWS / 8) * (BK / 8);  // 8x8 blocks (MNVEC)
+  static constexpr int PER_THREAD_T = BLOCKS / 256 > 0 ? BLOCKS / 256 : 1;
+  static constexpr int ELEMS = ROWS * BK / 256;  // GATHER
+  static_assert(CHUNKS % 256 == 0 || CHUNKS < 256, "tile/threads mismatch");
+
+  const uint16_t* p;
+  int64_t s_r, s_k, r0, nrows, nk;
+  u32x4 v[MODE == KVEC ? PER_THREAD_V : (MODE == MNVEC ? 8 * PER_THREAD_T : 1)];
+  uint16_t g[MODE == GATHER ? ELEMS : 1];
+
+  __device__ __forceinline__ void load(int64_t k0) {
+    const int t = threadIdx.x;
+    if constexpr (MODE == KVEC) {
+#pragma unroll
+      for (int i = 0; i < PER_THREAD_V; ++i) {
+        const int c = t + i * 256;
+        const int r = c / (BK / 8), kc = c % (BK / 8);
+        const int64_t gr = r0 + r, gk = k0 + kc * 8;
+        if (c < CHUNKS && gr < nrows && gk < nk)
+          v[i] = *reinterpret_cast<const u32x4*>(p + gr * s_r + gk);
+        else
+          v[i] = u32x4{0, 0, 0, 0};
+      }
+    } else if constexpr (MODE == MNVEC) {
+#pragma unroll
+      for (int i = 0; i < PER_THREAD_T; ++i) {
+        const int b = t + i * 256;
+        const int rb = b % (ROWS / 8), kb = b / (ROWS / 8);
+        const int64_t gr = r0 + rb * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int64_t gk = k0 + kb * 8 + j;
+          if (b < BLOCKS && gr < nrows && gk < nk)
+            v[i * 8 + j] = *reinterpret_cast<const u32x4*>(p + gk * s_k + gr);
+          else
+            v[i * 8 + j] = u32x4{0, 0, 0, 0};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < ELEMS; ++i) {
+        const int e = t + i * 256;
+        const int r = e / BK, k = e % BK;
+        const int64_t gr = r0 + r, gk = k0 + k;
+        g[i] = (gr < nrows && gk < nk) ? p[gr * s_r + gk * s_k] : (uint16_t)0;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+    const int t = threadIdx.x;
+    if constexpr (MODE == KVEC) {
+#pragma unroll
+      for (int i = 0; i < PER_THREAD_V; ++i) {
+        const int c = t + i * 256;
+        if (c < CHUNKS) {
+          const int r = c / (BK / 8), kc = c % (BK / 8);
+          *reinterpret_cast<u32x4*>(lds + r * LDK + kc * 8) = v[i];
+        }
+      }
+    } else if constexpr (MODE == MNVEC) {
+#pragma unroll
+      for (int i = 0; i < PER_THREAD_T; ++i) {
+        const int b = t + i * 256;
+        if (b < BLOCKS) {
+          const int rb = b % (ROWS / 8), kb = b / (ROWS / 8);
+          u32x4 o[8];
+          transpose8x8(&v[i * 8], o);
+#pragma unroll
+          for (int m = 0; m < 8; ++m) *reinterpret_cast<u32x4*>(lds + (rb * 8 + m) * LDK + kb * 8) = o[m];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < ELEMS; ++i) {
+        const int e = t + i * 256;
+        lds[(e / BK) * LDK + (e % BK)] = g[i];
+      }
+    }
+  }
+};
+
+// B tile of the fused int8 linear: rows n of the int8 weight q [N, K] (contiguous), dequantized while
+// staging: value = round_T(float(q[n, k]) * float(scale[n, k / 64])) — bit-identical to dq8 — so the
+// matrix cores see exactly the weights dequant_int8 would have produced, without them touching HBM.
+template <int ROWS, typename T>
+struct Dq8Loader {
+  static constexpr int CHUNKS = ROWS * BK / 8;  // 8 int8 per chunk
+  static constexpr int PT = CHUNKS / 256 > 0 ? CHUNKS / 256 : 1;
+  const int8_t* q;
+  const uint16_t* scale;
+  int64_t K, nblocks, r0, nrows;
+  u32x2 v[PT];
+  float sc[PT];
+
+  __device__ __forceinline__ void load(int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int c = threadIdx.x + i * 256;
+      const int r = c / (BK / 8), kc = c % (BK / 8);
+      const int64_t gr = r0 + r, gk = k0 + kc * 8;
+      if (c < CHUNKS && gr < nrows && gk < K) {
+        v[i] = *reinterpret_cast<const u32x2*>(q + gr * K + gk);
+        sc[i] = bf16_bits_to_f32(scale[gr * nblocks + (gk >> 6)]);
+      } else {
+        v[i] = u32x2{0, 0};
+        sc[i] = 0.f;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int c = threadIdx.x + i * 256;
+      if (c < CHUNKS) {
+        const int r = c / (BK / 8), kc = c % (BK / 8);
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (float)(int8_t)(((e < 4 ? v[i].x : v[i].y) >> (8 * (e & 3))) & 0xffu) * sc[i];
+        *reinterpret_cast<u32x4*>(lds + r * LDK + kc * 8) = pack8<T>(f);
+      }
+    }
+  }
+};
+
+// Main loop shared by the GEMM kernels: K in steps of BK through double-buffered LDS; acc[i][j] is the
+// wavefront's (i, j) 16x16 accumulator tile.
+template <typename T, int BM, int BN, int WM, int WN, class LA, class LB>
+__device__ __forceinline__ void gemm_mainloop(LA& la, LB& lb, int64_t K, uint16_t (*lds)[(BM + BN) * LDK],
+                                              f32x4 (&acc)[BM / WM / 16][BN / WN / 16]) {
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t nk = (K + BK - 1) / BK;
+  la.load(0);
+  lb.load(0);
+  la.store(lds[0]);
+  lb.store(lds[0] + BM * LDK);
+  __syncthreads();
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) {
+      la.load((kt + 1) * BK);
+      lb.load((kt + 1) * BK);
+    }
+    const uint16_t* As = lds[kt & 1];
+    const uint16_t* Bs = As + BM * LDK;
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 32) {
+      u32x4 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const u32x4*>(As + (wm * WTM + i * 16 + fr) * LDK + ks + fk);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bfr[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * WTN + j * 16 + fr) * LDK + ks + fk);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mac(af[i], bfr[j], acc[i][j]);
+    }
+    if (more) {
+      uint16_t* nxt = lds[(kt + 1) & 1];
+      la.store(nxt);
+      lb.store(nxt + BM * LDK);
+    }
+    __syncthreads();
+  }
+}
+
+// Epilogue: c = alpha * acc + beta * bias, one rounding; lane holds rows 4*(lane/16)+r, column lane%16
+// of every 16x16 tile.
+template <typename T, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void gemm_epilogue(const f32x4 (&acc)[BM / WM / 16][BN / WN / 16], uint16_t* C, int64_t c_sm,
+                                              int64_t c_sn, const uint16_t* bias, int64_t bias_sm, int64_t bias_sn,
+                                              bool has_bias, float alpha, float beta, int64_t m0, int64_t n0, int64_t M,
+                                              int64_t N) {
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int fr = lane & 15;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t gn = n0 + wn * WTN + j * 16 + fr;
+      if (gn >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t gm = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
+        if (gm >= M) continue;
+        float o = alpha * acc[i][j][r];
+        if (has_bias) o += beta * T::to_f32(bias[gm * bias_sm + gn * bias_sn]);
+        C[gm * c_sm + gn * c_sn] = T::from_f32(o);
+      }
+    }
+  }
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int AMODE, int BMODE>
+__global__ __launch_bounds__(256) void mm_mfma(hrt_mm_args p, int64_t tiles_m, int64_t tiles_n) {
+  static_assert(WM * WN == 4, "four wavefronts");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * LDK];
+  const int64_t tile = blockIdx.x;
+  const int64_t tn = tile % tiles_n, tm = (tile / tiles_n) % tiles_m, bz = tile / (tiles_n * tiles_m);
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+  // A as rows m with K; B as rows n with K.
+  TileLoader<BM, AMODE> la;
+  la.p = reinterpret_cast<const uint16_t*>(p.a) + bz * p.a_sb;
+  la.s_r = p.a_sm, la.s_k = p.a_sk, la.r0 = m0, la.nrows = p.M, la.nk = p.K;
+  TileLoader<BN, BMODE> lb;
+  lb.p = reinterpret_cast<const uint16_t*>(p.b) + bz * p.b_sb;
+  lb.s_r = p.b_sn, lb.s_k = p.b_sk, lb.r0 = n0, lb.nrows = p.N, lb.nk = p.K;
+  f32x4 acc[BM / WM / 16][BN / WN / 16];
+  gemm_mainloop<T, BM, BN, WM, WN>(la, lb, p.K, lds, acc);
+  gemm_epilogue<T, BM, BN, WM, WN>(acc, reinterpret_cast<uint16_t*>(p.c) + bz * p.c_sb, p.c_sm, p.c_sn,
+                                   reinterpret_cast<const uint16_t*>(p.bias) + bz * p.bias_sb, p.bias_sm, p.bias_sn,
+                                   p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N);
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int AMODE>
+__global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t tiles_m, int64_t tiles_n) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * LDK];
+  const int64_t tile = blockIdx.x;
+  const int64_t tn = tile % tiles_n, tm = tile / tiles_n;
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+  TileLoader<BM, AMODE> la;
+  la.p = reinterpret_cast<const uint16_t*>(p.x);
+  la.s_r = p.x_sm, la.s_k = p.x_sk, la.r0 = m0, la.nrows = p.M, la.nk = p.K;
+  Dq8Loader<BN, T> lb;
+  lb.q = reinterpret_cast<const int8_t*>(p.q);
+  lb.scale = reinterpret_cast<const uint16_t*>(p.scale);
+  lb.K = p.K, lb.nblocks = p.nblocks, lb.r0 = n0, lb.nrows = p.N;
+  f32x4 acc[BM / WM / 16][BN / WN / 16];
+  gemm_mainloop<T, BM, BN, WM, WN>(la, lb, p.K, lds, acc);
+  gemm_epilogue<T, BM, BN, WM, WN>(acc, reinterpret_cast<uint16_t*>(p.y), p.N, 1, reinterpret_cast<const uint16_t*>(p.bias), 0,
+                                   1, p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N);
+}
+
+// Which loader an operand can use.  rows = M (A) or N (B); s_r / s_k its strides.
+int pick_mode(uint64_t ptr, int64_t s_b, int64_t s_r, int64_t s_k, int64_t rows, int64_t K, int64_t batch) {
+  const bool aligned = ptr % 16 == 0 && (batch == 1 || s_b % 8 == 0);
+  if (aligned && s_k == 1 && K % 8 == 0 && (rows == 1 || s_r % 8 == 0)) return KVEC;
+  if (aligned && s_r == 1 && rows % 8 == 0 && (K == 1 || s_k % 8 == 0)) return MNVEC;
+  return GATHER;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int AM, int BMd>
+void queue(const hrt_mm_args& a, hipStream_t s) {
+  const int64_t tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
+  hipLaunchKernelGGL((mm_mfma<T, BM, BN, WM, WN, AM, BMd>), dim3((uint32_t)(tm * tn * a.batch)), dim3(256), 0, s, a, tm, tn);
+}
+
+template <typename T, int BM, int BN, int WM, int WN>
+void dispatch_modes(const hrt_mm_args& a, int am, int bm, hipStream_t s) {
+  switch (am * 3 + bm) {
+    case KVEC * 3 + KVEC: queue<T, BM, BN, WM, WN, KVEC, KVEC>(a, s); break;
+    case KVEC * 3 + MNVEC: queue<T, BM, BN, WM, WN, KVEC, MNVEC>(a, s); break;
+    case MNVEC * 3 + KVEC: queue<T, BM, BN, WM, WN, MNVEC, KVEC>(a, s); break;
+    case MNVEC * 3 + MNVEC: queue<T, BM, BN, WM, WN, MNVEC, MNVEC>(a, s); break;
+    default: break;
+  }
+}
+
+template <typename T>
+void dispatch_gather(const hrt_mm_args& a, int am, int bm, hipStream_t s) {
+  switch (am * 3 + bm) {
+    case KVEC * 3 + KVEC: queue<T, 64, 64, 2, 2, KVEC, KVEC>(a, s); break;
+    case KVEC * 3 + MNVEC: queue<T, 64, 64, 2, 2, KVEC, MNVEC>(a, s); break;
+    case KVEC * 3 + GATHER: queue<T, 64, 64, 2, 2, KVEC, GATHER>(a, s); break;
+    case MNVEC * 3 + KVEC: queue<T, 64, 64, 2, 2, MNVEC, KVEC>(a, s); break;
+    case MNVEC * 3 + MNVEC: queue<T, 64, 64, 2, 2, MNVEC, MNVEC>(a, s); break;
+    case MNVEC * 3 + GATHER: queue<T, 64, 64, 2, 2, MNVEC, GATHER>(a, s); break;
+    case GATHER * 3 + KVEC: queue<T, 64, 64, 2, 2, GATHER, KVEC>(a, s); break;
+    case GATHER * 3 + MNVEC: queue<T, 64, 64, 2, 2, GATHER, MNVEC>(a, s); break;
+    default: queue<T, 64, 64, 2, 2, GATHER, GATHER>(a, s); break;
+  }
+}
+
+template <typename T>
+bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_mm_args*>(pp);
+  if (!mm_check_operands(a, 2, ctx)) return false;
+  const int am = pick_mode(a.a, a.a_sb, a.a_sm, a.a_sk, a.M, a.K, a.batch);
+  const int bm = pick_mode(a.b, a.b_sb, a.b_sn, a.b_sk, a.N, a.K, a.batch);
+  const int64_t big = cdiv(a.M, 128) * cdiv(a.N, 256) * a.batch;
+  const int64_t med = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
+  const int64_t small = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
+  if (small > 0x7fffffffLL) return ctx.fail("GEMM grid too large");
+  if (am == GATHER || bm == GATHER) {
+    dispatch_gather<T>(a, am, bm, ctx.stream);
+  } else if (big >= 240) {
+    dispatch_modes<T, 128, 256, 2, 2>(a, am, bm, ctx.stream);
+  } else if (med >= 240) {
+    dispatch_modes<T, 128, 128, 2, 2>(a, am, bm, ctx.stream);
+  } else {
+    dispatch_modes<T, 64, 64, 2, 2>(a, am, bm, ctx.stream);
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "mm_mfma");
+}
+
+template <typename T, int BM, int BN, int AM>
+void queue_dq8(const hrt_mm_dq8_args& a, hipStream_t s) {
+  const int64_t tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
+  hipLaunchKernelGGL((mm_dq8_mfma<T, BM, BN, 2, 2, AM>), dim3((uint32_t)(tm * tn)), dim3(256), 0, s, a, tm, tn);
+}
+
+template <typename T>
+bool launch_mm_dq8(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_mm_dq8_args*>(pp);
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0) return ctx.fail("empty GEMM");
+  if (a.nblocks != (a.K + 63) / 64) return ctx.fail("nblocks must equal ceil(K / 64)");
+  if (a.x_sm < 0 || a.x_sk < 0) return ctx.fail("negative stride");
+  if (a.K % 8 != 0 || a.q % 8 != 0) return ctx.fail("the fused int8 linear needs K % 8 == 0 and an 8-byte aligned q");
+  const int64_t xs[2] = {a.M, a.K}, xt[2] = {a.x_sm, a.x_sk};
+  if (!ctx.check(a.x, hrt::span_bytes(2, xs, xt, 2), "x") || !ctx.check(a.q, (uint64_t)(a.N * a.K), "q") ||
+      !ctx.check(a.scale, (uint64_t)(a.N * a.nblocks) * 2, "scale") || !ctx.check(a.y, (uint64_t)(a.M * a.N) * 2, "y") ||
+      (a.has_bias && !ctx.check(a.bias, (uint64_t)a.N * 2, "bias")))
+    return false;
+  const int am = pick_mode(a.x, 0, a.x_sm, a.x_sk, a.M, a.K, 1);
+  const int64_t big = cdiv(a.M, 128) * cdiv(a.N, 256);
+  if (big >= 240) {
+    if (am == KVEC) queue_dq8<T, 128, 256, KVEC>(a, ctx.stream);
+    else if (am == MNVEC) queue_dq8<T, 128, 256, MNVEC>(a, ctx.stream);
+    else queue_dq8<T, 64, 64, GATHER>(a, ctx.stream);
+  } else {
+    if (am == KVEC) queue_dq8<T, 64, 64, KVEC>(a, ctx.stream);
+    else if (am == MNVEC) queue_dq8<T, 64, 64, MNVEC>(a, ctx.stream);
+    else queue_dq8<T, 64, 64, GATHER>(a, ctx.stream);
+  }
+  return hrt::launch_ok(hipGetLastError(), ctx, "mm_dq8");
+}
+
+HRT_REGISTER("mm_mfma_bf16", hrt_mm_args, launch_mm_mfma<BF16>);
+HRT_REGISTER("mm_mfma_f16", hrt_mm_args, launch_mm_mfma<F16>);
+HRT_REGISTER("mm_dq8_bf16", hrt_mm_dq8_args, launch_mm_dq8<BF16>);
+HRT_REGISTER("mm_dq8_f16", hrt_mm_dq8_args, launch_mm_dq8<F16>);
+
+}  // namespace
+}  // namespace hk

@@ -1,0 +1,52 @@
+// Matrix-core helpers for gfx950 (CDNA4): typed wrappers of v_mfma_f32_16x16x32_{bf16,f16} and the
+// 8x8 transpose of 16-bit elements used to turn M-/N-contiguous tiles into K-contiguous LDS rows.
+//
+// Lane layout of v_mfma_f32_16x16x32 (checked on the device): with l = lane (0..63), g = l / 16,
+//   A operand (16 x 32, M x K): lane l holds A[l % 16][8 g + i], i = 0..7
+//   B operand (32 x 16, K x N): lane l holds B[8 g + i][l % 16]
+//   accumulator (16 x 16):      lane l holds D[4 g + i][l % 16], i = 0..3
+// so both operands want 8 consecutive K values per lane: every tile is staged in LDS with K contiguous
+// and read with one 128-bit ds_read per fragment.
+#pragma once
+
+#include "device_common.h"
+
+namespace hk {
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<BF16> {
+  __device__ __forceinline__ static f32x4 mac(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<F16> {
+  __device__ __forceinline__ static f32x4 mac(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// in[j] holds row j (8 halves, dword d = cols 2d | 2d+1 << 16); out[m] holds column m (rows 0..7).
+__device__ __forceinline__ void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    uint32_t w[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t a = in[2 * r][m >> 1], b = in[2 * r + 1][m >> 1];
+      w[r] = (m & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+    }
+    out[m] = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// Convert 8 fp32 values to 8 packed 16-bit values of type T (round to nearest even).
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const float* v) {
+  return u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
+}
+
+}  // namespace hk
