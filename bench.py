@@ -1,0 +1,391 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X vk hot path (one GPU).
+
+Headline (`value`): bf16 flash-attention forward + backward at B1 H16 S1024 D128 (BASELINE configs 2+3),
+in algorithmic TFLOP/s: 4*B*H*S^2*D forward + 2.5x that backward = 3.006e10 flop per step (the
+convention of the reference's tools/bench_attention.py:39).  A step is the hot path's four kernels
+(forward, delta, dK/dV, dQ) over one batch already resident in HBM, queued through the hrt C ABI exactly
+as the PyTorch shim queues them, replayed as a HIP graph on the runtime's stream and timed with HIP
+events on that stream.  The same JSON line carries the other BASELINE workloads (GEMMs, softmax,
+layer_norm, int8 dequant, the fused int8 linear, attention at S=4096), each as absolute TFLOP/s or GB/s
+and as a fraction of MI355X's published peak, the roofline object of the step's dominant kernel, the
+PyTorch-level step time, and the reference's CPU path (torch CPU aten) timed on this host.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--skip-cpu] [--only-attn]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "torch-vulkan_amd"))
+
+METRIC = "bf16 TFLOP/s flash-attn fwd+bwd (S1024,H16,D128) & GEMM; % of MFMA/HBM peak"
+PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0}  # MI355X published dense matrix peak
+PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
+    return ap.parse_args()
+
+
+def attn_flops(B, H, Sq, Sk, D):
+    fwd = 4.0 * B * H * Sq * Sk * D
+    return fwd, 2.5 * fwd
+
+
+class Bench:
+    def __init__(self, args):
+        import torch
+
+        import torch_vulkan
+        from torch_vulkan import abi
+
+        self.torch, self.tv, self.abi = torch, torch_vulkan, abi
+        self.rt = abi.Runtime()
+        self.dev = torch.device("vk")
+        self.args = args
+
+    # ---- helpers --------------------------------------------------------------------------------------
+    def randn(self, shape, dtype, seed, scale=1.0):
+        g = self.torch.Generator().manual_seed(seed)
+        return (self.torch.randn(shape, generator=g) * scale).to(dtype).to(self.dev)
+
+    def time_graph(self, enqueue, reps, launches=3):
+        """Average GPU time of one enqueue() call: a graph of `reps` calls, replayed `launches` times
+        between two events on the runtime stream (after one untimed replay)."""
+        rt = self.rt
+        gid = rt.graph(lambda: [enqueue(i) for i in range(reps)])
+        try:
+            rt.graph_launch(gid)
+            rt.synchronize()
+            rt.event_record(0)
+            for _ in range(launches):
+                rt.graph_launch(gid)
+            rt.event_record(1)
+            ms = rt.elapsed_ms(0, 1)
+        finally:
+            rt.graph_destroy(gid)
+        return ms / (reps * launches)
+
+    # ---- attention -----------------------------------------------------------------------------------
+    def attn_setup(self, B, H, S, D, dtype="bf16"):
+        torch, abi = self.torch, self.abi
+        dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+        q, k, v, do = (self.randn((B, H, S, D), dt, s) for s in (1, 2, 3, 4))
+        o = torch.empty((B, S, H, D), dtype=dt, device=self.dev)
+        o32 = torch.empty((B, S, H, D), dtype=torch.float32, device=self.dev)
+        lse = torch.empty((B, H, S), dtype=torch.float32, device=self.dev)
+        delta = torch.empty((B, H, S), dtype=torch.float32, device=self.dev)
+        dq, dk, dv = (torch.empty((B, S, H, D), dtype=dt, device=self.dev) for _ in range(3))
+        a = abi.AttnArgs()
+        a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+        a.o, a.lse, a.o32, a.dout, a.delta = o.data_ptr(), lse.data_ptr(), o32.data_ptr(), do.data_ptr(), delta.data_ptr()
+        a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+        a.q_sb, a.q_sh, a.q_ss = q.stride(0), q.stride(1), q.stride(2)
+        a.k_sb, a.k_sh, a.k_ss = k.stride(0), k.stride(1), k.stride(2)
+        a.v_sb, a.v_sh, a.v_ss = v.stride(0), v.stride(1), v.stride(2)
+        a.do_sb, a.do_sh, a.do_ss = do.stride(0), do.stride(1), do.stride(2)
+        a.B, a.H, a.Sq, a.Sk, a.D = B, H, S, S, D
+        a.scale = 1.0 / D ** 0.5
+        ad = abi.AttnArgs.from_buffer_copy(a)
+        ad.o, ad.flags = o32.data_ptr(), abi.ATTN_O_F32
+        keep = (q, k, v, do, o, o32, lse, delta, dq, dk, dv)
+        names = {n: f"attn_{n}_mfma_{dtype}" for n in ("fwd", "dkdv", "dq")}
+        names["delta"] = f"attn_delta_{dtype}"
+
+        def step(_i=0):
+            self.rt.dispatch(names["fwd"], a)
+            self.rt.dispatch(names["delta"], ad)
+            self.rt.dispatch(names["dkdv"], a)
+            self.rt.dispatch(names["dq"], a)
+
+        kernels = {
+            "fwd": lambda _i: self.rt.dispatch(names["fwd"], a),
+            "delta": lambda _i: self.rt.dispatch(names["delta"], ad),
+            "dkdv": lambda _i: self.rt.dispatch(names["dkdv"], a),
+            "dq": lambda _i: self.rt.dispatch(names["dq"], a),
+        }
+        return step, kernels, keep, names
+
+    def attn_headline(self):
+        """K timed steps of fwd+bwd at B1 H16 S1024 D128 bf16, plus per-kernel durations."""
+        rt, args = self.rt, self.args
+        B, H, S, D = 1, 16, 1024, 128
+        step, kernels, keep, names = self.attn_setup(B, H, S, D)
+        fwd_f, bwd_f = attn_flops(B, H, S, S, D)
+        gid = rt.graph(step)
+        for _ in range(args.warmup):
+            rt.graph_launch(gid)
+        rt.synchronize()
+        rt.event_record(0)
+        for _ in range(args.steps):
+            rt.graph_launch(gid)
+        rt.event_record(1)
+        rt.synchronize()
+        ms = rt.elapsed_ms(0, 1) / args.steps
+        rt.graph_destroy(gid)
+        # per-kernel average launch durations (20 back-to-back launches each)
+        per = {n: self.time_graph(kernels[n], 20) for n in ("fwd", "delta", "dkdv", "dq")}
+        unit = 2.0 * B * H * S * S * D  # one S x S x D product
+        algo = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 1 * unit}  # S, dP shared by dK/dV; dQ's S, dP are recompute
+        delta_bytes = B * S * H * D * (4 + 2) + B * H * S * 4
+        kstats = {}
+        for n, t in per.items():
+            e = {"kernel": names[n], "avg_us": round(t * 1e3, 3)}
+            if n in algo:
+                e["algo_tflop"] = algo[n] / 1e12
+                e["tflops"] = round(algo[n] / (t * 1e-3) / 1e12, 2)
+                e["frac_of_bf16_peak"] = round(e["tflops"] / PEAK_TFLOPS["bf16"], 4)
+            else:
+                e["gbs"] = round(delta_bytes / (t * 1e-3) / 1e9, 1)
+            kstats[n] = e
+        dom = max(("fwd", "dkdv", "dq"), key=lambda n: per[n])
+        ach = algo[dom] / (per[dom] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_TFLOPS["bf16"], 4), "traffic": None, "kernel": names[dom],
+                "algo_flop_per_launch": algo[dom], "avg_launch_us": round(per[dom] * 1e3, 3)}
+        del keep
+        return ms, (fwd_f + bwd_f) / (ms * 1e-3) / 1e12, kstats, roof
+
+    def attn_torch_step(self):
+        """The same fwd+bwd through F.scaled_dot_product_attention and autograd (host overhead included)."""
+        torch, rt = self.torch, self.rt
+        import torch.nn.functional as F
+
+        B, H, S, D = 1, 16, 1024, 128
+        q, k, v, do = (self.randn((B, H, S, D), torch.bfloat16, s) for s in (1, 2, 3, 4))
+
+        def one():
+            qq, kk, vv = (t.detach().requires_grad_(True) for t in (q, k, v))
+            F.scaled_dot_product_attention(qq, kk, vv).backward(do)
+
+        for _ in range(3):
+            one()
+        rt.synchronize()
+        n = 20
+        t0 = time.perf_counter()
+        rt.event_record(2)
+        for _ in range(n):
+            one()
+        rt.event_record(3)
+        rt.synchronize()
+        wall = (time.perf_counter() - t0) / n
+        return {"wall_ms": round(wall * 1e3, 3), "gpu_ms": round(rt.elapsed_ms(2, 3) / n, 3)}
+
+    def attn_s4096(self):
+        B, H, S, D = 1, 16, 4096, 128
+        step, kernels, keep, _ = self.attn_setup(B, H, S, D)
+        t = self.time_graph(lambda i: step(), 3)
+        f, b = attn_flops(B, H, S, S, D)
+        per = {n: round(self.time_graph(kernels[n], 5) * 1e3, 2) for n in ("fwd", "dkdv", "dq")}
+        del keep
+        return {"ms": round(t, 4), "tflops": round((f + b) / (t * 1e-3) / 1e12, 2),
+                "frac_of_bf16_peak": round((f + b) / (t * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4), "kernel_us": per}
+
+    # ---- GEMM --------------------------------------------------------------------------------------
+    def gemm(self, M, K, N, layout, bias=False):
+        torch, abi = self.torch, self.abi
+        a = self.randn((M, K), torch.bfloat16, 1)
+        if layout == "nt":  # F.linear: x @ W^T with W [N, K] read through its transposed view
+            w = self.randn((N, K), torch.bfloat16, 2)
+            b_sk, b_sn = w.stride(1), w.stride(0)
+        else:
+            w = self.randn((K, N), torch.bfloat16, 2)
+            b_sk, b_sn = w.stride(0), w.stride(1)
+        c = torch.empty((M, N), dtype=torch.bfloat16, device=self.dev)
+        bv = self.randn((N,), torch.bfloat16, 3)
+        m = abi.MmArgs()
+        m.a, m.b, m.c, m.bias = a.data_ptr(), w.data_ptr(), c.data_ptr(), bv.data_ptr()
+        m.M, m.N, m.K, m.batch = M, N, K, 1
+        m.a_sm, m.a_sk, m.b_sk, m.b_sn = a.stride(0), a.stride(1), b_sk, b_sn
+        m.c_sm, m.c_sn = N, 1
+        m.bias_sn = 1
+        m.alpha, m.beta, m.has_bias = 1.0, 1.0 if bias else 0.0, 1 if bias else 0
+        t = self.time_graph(lambda i: self.rt.dispatch("mm_mfma_bf16", m), 10)
+        fl = 2.0 * M * N * K
+        return {"shape": f"{M}x{K}x{N}", "layout": layout, "bias": bias, "avg_us": round(t * 1e3, 2),
+                "tflops": round(fl / (t * 1e-3) / 1e12, 2), "frac_of_bf16_peak": round(fl / (t * 1e-3) / 1e12 / 2500.0, 4)}
+
+    def dq8_linear(self, M):
+        torch, abi = self.torch, self.abi
+        N, K = 8192, 2048
+        g = torch.Generator().manual_seed(9)
+        q = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(self.dev)
+        s = (torch.rand(N, 1, generator=g) * 0.019 + 0.001).to(torch.bfloat16).expand(N, K // 64).contiguous().to(self.dev)
+        x = self.randn((M, K), torch.bfloat16, 7)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=self.dev)
+        a = abi.MmDq8Args()
+        a.x, a.q, a.scale, a.y = x.data_ptr(), q.data_ptr(), s.data_ptr(), y.data_ptr()
+        a.M, a.N, a.K, a.nblocks, a.x_sm, a.x_sk, a.alpha, a.beta = M, N, K, K // 64, K, 1, 1.0, 0.0
+        t = self.time_graph(lambda i: self.rt.dispatch("mm_dq8_bf16", a), 10)
+        fl = 2.0 * M * N * K
+        return {"M": M, "avg_us": round(t * 1e3, 2), "tflops": round(fl / (t * 1e-3) / 1e12, 2),
+                "frac_of_bf16_peak": round(fl / (t * 1e-3) / 1e12 / 2500.0, 4)}
+
+    # ---- bandwidth kernels: rotate over > 512 MB so the 256 MB MALL cannot serve them ------------
+    def bw(self, name, nbytes, sets, make_args, kernels):
+        args = [make_args(i) for i in range(sets)]
+        t = self.time_graph(lambda i: [self.rt.dispatch(k, args[i % sets][j]) for j, k in enumerate(kernels)], 2 * sets)
+        return {"avg_us": round(t * 1e3, 3), "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
+                "frac_of_hbm_peak": round(nbytes / (t * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": nbytes}
+
+    def softmax(self):
+        torch, abi = self.torch, self.abi
+        R, C = 16384, 1024
+        xs = [self.randn((R, C), torch.float32, 10 + i, 2.0) for i in range(5)]
+        ys = [torch.empty_like(x) for x in xs]
+        gs = [self.randn((R, C), torch.float32, 20 + i) for i in range(5)]
+        dxs = [torch.empty_like(x) for x in xs]
+
+        def fa(i):
+            a = abi.SoftmaxArgs()
+            a.x, a.y, a.outer, a.R, a.inner = xs[i].data_ptr(), ys[i].data_ptr(), R, C, 1
+            return [a]
+
+        def ba(i):
+            a = abi.SoftmaxArgs()
+            a.y, a.g, a.dx, a.outer, a.R, a.inner = ys[i].data_ptr(), gs[i].data_ptr(), dxs[i].data_ptr(), R, C, 1
+            return [a]
+
+        n = R * C * 4
+        return {"fwd": self.bw("softmax_fwd", 2 * n, 5, fa, ["softmax_fwd_f32"]),
+                "bwd": self.bw("softmax_bwd", 3 * n, 4, ba, ["softmax_bwd_f32"])}
+
+    def layer_norm(self):
+        torch, abi = self.torch, self.abi
+        R, D, sets = 1024, 2048, 64
+        bf = torch.bfloat16
+        w, b = self.randn((D,), bf, 2), self.randn((D,), bf, 3)
+        xs = [self.randn((R, D), bf, 100 + i) for i in range(sets)]
+        gs = [self.randn((R, D), bf, 200 + i) for i in range(sets)]
+        ys = [torch.empty_like(x) for x in xs]
+        dxs = [torch.empty_like(x) for x in xs]
+        mu = torch.empty(R, dtype=torch.float32, device=self.dev)
+        rs = torch.empty(R, dtype=torch.float32, device=self.dev)
+        ws = torch.empty((self.abi.ln_chunks(R), 2, D), dtype=torch.float32, device=self.dev)
+        dw, db = torch.empty(D, dtype=bf, device=self.dev), torch.empty(D, dtype=bf, device=self.dev)
+
+        def fa(i):
+            a = abi.LnArgs()
+            a.x, a.y, a.mean, a.rstd, a.w, a.b, a.rows, a.D, a.eps = (xs[i].data_ptr(), ys[i].data_ptr(), mu.data_ptr(),
+                                                                      rs.data_ptr(), w.data_ptr(), b.data_ptr(), R, D, 1e-5)
+            return [a]
+
+        def ba(i):
+            a = abi.LnArgs()
+            a.x, a.g, a.mean, a.rstd, a.w, a.dx, a.ws, a.dw, a.db, a.rows, a.D = (
+                xs[i].data_ptr(), gs[i].data_ptr(), mu.data_ptr(), rs.data_ptr(), w.data_ptr(), dxs[i].data_ptr(),
+                ws.data_ptr(), dw.data_ptr(), db.data_ptr(), R, D)
+            return [a, a]
+
+        fwd_b = 2 * R * D * 2 + 2 * D * 2 + 2 * R * 4
+        bwd_b = 3 * R * D * 2 + D * 2 + 2 * R * 4 + 2 * D * 2
+        return {"fwd": self.bw("ln_fwd", fwd_b, sets, fa, ["ln_fwd_bf16"]),
+                "bwd": self.bw("ln_bwd", bwd_b, sets, ba, ["ln_bwd_bf16", "ln_wgrad_bf16"])}
+
+    def dequant(self):
+        torch, abi = self.torch, self.abi
+        R, C, sets = 8192, 2048, 12
+        qs, ss, outs = [], [], []
+        for i in range(sets):
+            g = torch.Generator().manual_seed(i)
+            qs.append(torch.randint(-127, 128, (R, C), generator=g, dtype=torch.int8).to(self.dev))
+            ss.append((torch.rand(R, 1, generator=g) * 0.019 + 0.001).to(torch.bfloat16).expand(R, C // 64).contiguous().to(self.dev))
+            outs.append(torch.empty((R, C), dtype=torch.bfloat16, device=self.dev))
+
+        def mk(i):
+            a = abi.Dq8Args()
+            a.q, a.scale, a.out, a.rows, a.cols, a.nblocks = qs[i].data_ptr(), ss[i].data_ptr(), outs[i].data_ptr(), R, C, C // 64
+            return [a]
+
+        return self.bw("dq8", R * C + R * (C // 64) * 2 + R * C * 2, sets, mk, ["dq8_bf16"])
+
+    # ---- CPU baseline: the reference's CPU path (torch CPU aten) -------------------------------------
+    def cpu_baseline(self):
+        import torch
+        import torch.nn.functional as F
+
+        B, H, S, D = 1, 16, 1024, 128
+        g = torch.Generator().manual_seed(0)
+        q, k, v, do = (torch.randn((B, H, S, D), generator=g).to(torch.bfloat16) for _ in range(4))
+
+        def one():
+            qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+            F.scaled_dot_product_attention(qq, kk, vv).backward(do)
+
+        one()
+        times = []
+        t_end = time.perf_counter() + self.args.cpu_seconds
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+            t0 = time.perf_counter()
+            one()
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        f, b = attn_flops(B, H, S, S, D)
+        model = ""
+        try:
+            with open("/proc/cpuinfo") as fh:
+                model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), "")
+        except OSError:
+            pass
+        return {"value": round((f + b) / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+                "kind": "reference", "ms_per_step": round(med * 1e3, 2),
+                "sample": f"torch {torch.__version__} CPU aten F.scaled_dot_product_attention fwd+bwd bf16 "
+                          f"[1,16,1024,128] (the reference's CPU path), median of {len(times)} steps, "
+                          f"{torch.get_num_threads()} threads, {model}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every box here has one "
+              "GPU; the sharding design is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    bench = Bench(args)
+    print(f"[bench] device: {bench.tv.device_name()}", file=sys.stderr, flush=True)
+    ms, tflops, kstats, roof = bench.attn_headline()
+    print(f"[bench] attention fwd+bwd step {ms:.4f} ms = {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs, resident in HBM)",
+        "config": {"workload": "flash-attention fwd+bwd, B=1 H=16 S=1024 D=128 bf16, non-causal, scale 1/sqrt(128) "
+                               "(BASELINE configs[1]+[2]); one step = fwd, delta, dK/dV, dQ kernels",
+                   "B": 1, "H": 16, "S": 1024, "D": 128, "parallelism": "single GPU"},
+        "frac_of_bf16_peak": round(tflops / PEAK_TFLOPS["bf16"], 4),
+        "roofline": roof,
+        "attn_kernels": kstats,
+    }
+    if not args.only_attn:
+        line["attn_torch_path"] = bench.attn_torch_step()
+        print(f"[bench] torch path {line['attn_torch_path']}", file=sys.stderr, flush=True)
+        line["attn_s4096"] = bench.attn_s4096()
+        line["gemm"] = [bench.gemm(1024, 2048, 8192, "nt"), bench.gemm(1024, 2048, 8192, "nn"),
+                        bench.gemm(1024, 1024, 1024, "nn", bias=True)]
+        print(f"[bench] gemm {line['gemm']}", file=sys.stderr, flush=True)
+        line["dq8_linear"] = [bench.dq8_linear(1024), bench.dq8_linear(4096)]
+        line["softmax_f32_16384x1024"] = bench.softmax()
+        line["layer_norm_bf16_1024x2048"] = bench.layer_norm()
+        line["dequant_int8_8192x2048_bf16"] = bench.dequant()
+        print("[bench] bandwidth kernels done", file=sys.stderr, flush=True)
+    if not args.skip_cpu:
+        line["cpu_baseline"] = bench.cpu_baseline()
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

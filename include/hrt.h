@@ -131,6 +131,18 @@ uint32_t hrt_coop_caps(void);
 int hrt_event_record(uint32_t slot);
 float hrt_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot);
 
+/* ---- HIP graphs on the runtime's stream (no counterpart in csrc/vkrt.h; the reference batches
+ * recorded commands instead, vkrt/src/lib.rs:542-643) ---------------------------------------------------
+ * Between hrt_graph_begin and hrt_graph_end every hrt_dispatch and hrt_copy_d2d is recorded into a HIP
+ * graph instead of being executed; calls that would wait for the GPU (upload, download, synchronize,
+ * freeing a dedicated block, empty_cache) and allocations that need a new slab fail while recording.
+ * hrt_graph_end returns the graph id (>= 0, -1 on error); hrt_graph_launch queues one replay on the
+ * runtime stream (asynchronous), hrt_graph_destroy releases it. */
+int hrt_graph_begin(void);
+int64_t hrt_graph_end(void);
+int hrt_graph_launch(int64_t graph);
+int hrt_graph_destroy(int64_t graph);
+
 #ifdef __cplusplus
 }
 #endif

@@ -100,3 +100,31 @@ def test_slab_allocator_host(tmp_path):
                    check=True)
     r = subprocess.run([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0 and "ALL OK" in r.stdout, r.stdout
+
+
+def test_python_abi_structs_match_the_c_headers(tmp_path):
+    """torch_vulkan/abi.py mirrors include/hrt_ops.h: same size and field offsets for every argument block."""
+    from torch_vulkan import abi
+
+    structs = {
+        "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs,
+        "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_attn_args": abi.AttnArgs,
+        "hrt_softmax_args": abi.SoftmaxArgs, "hrt_ln_args": abi.LnArgs, "hrt_dq8_args": abi.Dq8Args,
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "hrt_ops.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("  return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True, check=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l.strip()}
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
+    assert abi.ln_chunks(1024) == 256 and abi.ln_chunks(5) == 2

@@ -50,7 +50,12 @@ uint64_t now_ns() {
 
 struct HipBacking final : Backing {
   hipStream_t stream = nullptr;
+  bool capturing = false;
   bool map(uint64_t size, uint64_t* base, std::string* err) override {
+    if (capturing) {
+      *err = "cannot reserve device memory while a graph is being recorded";
+      return false;
+    }
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, size);
     if (e != hipSuccess || p == nullptr) {
@@ -79,6 +84,7 @@ struct Runtime {
   std::map<std::string, std::pair<uint64_t, uint64_t>> prof;  // name -> (ns, count)
   hipEvent_t prof_ev[2] = {nullptr, nullptr};
   hipEvent_t slots[16] = {};
+  std::vector<hipGraphExec_t> graphs;
 };
 
 Runtime* g_rt = nullptr;
@@ -254,6 +260,10 @@ int hrt_free(uint64_t addr) {
   if (!rt) return -1;
   std::lock_guard<std::mutex> l(rt->mu);
   std::string err;
+  if (rt->backing.capturing && !rt->alloc->is_regular_block(addr)) {
+    set_error("hrt_free: a dedicated block cannot be released while a graph is being recorded");
+    return -1;
+  }
   if (!rt->alloc->free(addr, &err)) {
     set_error(err);
     return -1;
@@ -269,6 +279,10 @@ int hrt_upload(uint64_t dst, const void* src, uint64_t n) {
   std::lock_guard<std::mutex> l(rt->mu);
   if (!src) {
     set_error("hrt_upload: null source");
+    return -1;
+  }
+  if (rt->backing.capturing) {
+    set_error("hrt_upload: not allowed while a graph is being recorded");
     return -1;
   }
   if (!checked(rt, dst, n)) return -1;
@@ -289,6 +303,10 @@ int hrt_download(void* dst, uint64_t src, uint64_t n) {
   std::lock_guard<std::mutex> l(rt->mu);
   if (!dst) {
     set_error("hrt_download: null destination");
+    return -1;
+  }
+  if (rt->backing.capturing) {
+    set_error("hrt_download: not allowed while a graph is being recorded");
     return -1;
   }
   if (!checked(rt, src, n)) return -1;
@@ -352,14 +370,15 @@ int hrt_dispatch(uint32_t kernel, const void* args, uint32_t len, uint32_t gx, u
   LaunchCtx ctx;
   ctx.stream = rt->stream;
   ctx.in_bounds = &in_bounds_locked;
-  if (rt->profile) (void)hipEventRecord(rt->prof_ev[0], rt->stream);
+  const bool prof = rt->profile && !rt->backing.capturing;
+  if (prof) (void)hipEventRecord(rt->prof_ev[0], rt->stream);
   bool ok = k.launch(args, grid, ctx);
   if (!ok) {
     if (ctx.error.rfind("operand", 0) == 0) g_validation_errors++;
     set_error(std::string(k.name) + ": " + ctx.error);
     return -1;
   }
-  if (rt->profile) {
+  if (prof) {
     (void)hipEventRecord(rt->prof_ev[1], rt->stream);
     (void)hipEventSynchronize(rt->prof_ev[1]);
     float ms = 0.f;
@@ -377,6 +396,10 @@ int hrt_synchronize(void) {
   Runtime* rt = rt_or_error();
   if (!rt) return -1;
   std::lock_guard<std::mutex> l(rt->mu);
+  if (rt->backing.capturing) {
+    set_error("hrt_synchronize: not allowed while a graph is being recorded");
+    return -1;
+  }
   uint64_t t0 = now_ns();
   hipError_t e = hipStreamSynchronize(rt->stream);
   g_stats[7] += now_ns() - t0;
@@ -388,6 +411,10 @@ size_t hrt_empty_cache(void) {
   Runtime* rt = rt_or_error();
   if (!rt) return 0;
   std::lock_guard<std::mutex> l(rt->mu);
+  if (rt->backing.capturing) {
+    set_error("hrt_empty_cache: not allowed while a graph is being recorded");
+    return 0;
+  }
   return rt->alloc->empty_cache();
 }
 
@@ -467,6 +494,73 @@ float hrt_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot) {
     return -1.f;
   }
   return ms;
+}
+
+int hrt_graph_begin(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (rt->backing.capturing) {
+    set_error("hrt_graph_begin: a graph is already being recorded");
+    return -1;
+  }
+  hipError_t e = hipStreamBeginCapture(rt->stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) return hip_fail("hipStreamBeginCapture", e);
+  rt->backing.capturing = true;
+  rt->alloc->set_frozen(true);
+  return 0;
+}
+
+int64_t hrt_graph_end(void) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (!rt->backing.capturing) {
+    set_error("hrt_graph_end: no graph is being recorded");
+    return -1;
+  }
+  rt->backing.capturing = false;
+  rt->alloc->set_frozen(false);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(rt->stream, &g);
+  if (e != hipSuccess) return hip_fail("hipStreamEndCapture", e);
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail("hipGraphInstantiate", e);
+  rt->graphs.push_back(x);
+  return (int64_t)rt->graphs.size() - 1;
+}
+
+int hrt_graph_launch(int64_t graph) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (graph < 0 || graph >= (int64_t)rt->graphs.size() || !rt->graphs[graph]) {
+    set_error("hrt_graph_launch: unknown graph id");
+    return -1;
+  }
+  if (rt->backing.capturing) {
+    set_error("hrt_graph_launch: not allowed while a graph is being recorded");
+    return -1;
+  }
+  hipError_t e = hipGraphLaunch(rt->graphs[graph], rt->stream);
+  if (e != hipSuccess) return hip_fail("hipGraphLaunch", e);
+  return 0;
+}
+
+int hrt_graph_destroy(int64_t graph) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (graph < 0 || graph >= (int64_t)rt->graphs.size() || !rt->graphs[graph]) {
+    set_error("hrt_graph_destroy: unknown graph id");
+    return -1;
+  }
+  (void)hipStreamSynchronize(rt->stream);
+  (void)hipGraphExecDestroy(rt->graphs[graph]);
+  rt->graphs[graph] = nullptr;
+  return 0;
 }
 
 }  // extern "C"

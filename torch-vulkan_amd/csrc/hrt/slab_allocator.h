@@ -56,6 +56,8 @@ class SlabAllocator {
   size_t live_blocks() const { return blocks_.size(); }
   size_t slab_count() const { return slabs_.size(); }
   uint64_t limit() const { return limit_; }
+  // While frozen, allocations are served from existing free ranges only (no driver calls at all).
+  void set_frozen(bool f) { frozen_ = f; }
 
   uint64_t reserved_bytes() const {
     uint64_t r = 0;
@@ -90,7 +92,13 @@ class SlabAllocator {
     }
     const uint64_t rounded = (size + kAlign - 1) / kAlign * kAlign;
     uint64_t addr = 0;
-    if (rounded >= dedicated_min_) {
+    if (frozen_) {
+      addr = rounded < dedicated_min_ ? carve(rounded) : 0;
+      if (addr == 0) {
+        *err = "no free range of " + std::to_string(rounded) + " bytes and new device memory cannot be reserved now";
+        return 0;
+      }
+    } else if (rounded >= dedicated_min_) {
       uint64_t base = 0;
       if (!new_slab_with_retry(rounded, /*dedicated=*/true, &base, err)) return 0;
       slabs_[base].used = rounded;
@@ -170,6 +178,14 @@ class SlabAllocator {
       ++n;
     }
     return n;
+  }
+
+  // True when addr is a live block carved from a regular (non-dedicated) slab.
+  bool is_regular_block(uint64_t addr) const {
+    auto it = blocks_.find(addr);
+    if (it == blocks_.end()) return false;
+    auto s = slabs_.find(it->second.slab);
+    return s != slabs_.end() && !s->second.dedicated;
   }
 
   // True when [addr, addr + len) lies inside the requested size of one live block.
@@ -292,6 +308,7 @@ class SlabAllocator {
   Backing* backing_;
   uint64_t max_alloc_;
   uint64_t limit_ = 0;
+  bool frozen_ = false;
   uint64_t slab_bytes_ = kSlabBytes;
   uint64_t dedicated_min_ = kDedicatedMin;
   uint64_t live_ = 0, peak_ = 0;

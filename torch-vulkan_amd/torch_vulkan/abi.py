@@ -1,0 +1,171 @@
+"""ctypes binding of the hrt C ABI (include/hrt.h, include/hrt_ops.h).
+
+This is the Python counterpart of what a maintainer of the reference would bind to the runtime's C ABI
+(csrc/vkrt.h:6-32): the same entry points, the argument blocks of the operator kernels as
+ctypes.Structure mirrors of the C structs, and a `dispatch` helper that raises with the runtime's
+last-error message.  bench.py drives the kernels through it; the PyTorch shim (torch_vulkan_C) calls the
+same library from C++.
+"""
+
+import ctypes
+import os
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhrt.so")
+MAX_DIMS = 8
+F32, BF16, F16, RAW8, RAW16, RAW32, RAW64 = range(7)
+ATTN_O_F32 = 1
+
+u64, i64, i32, u32, f32 = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float
+
+
+class AddF32Args(ctypes.Structure):
+    _fields_ = [("a", u64), ("b", u64), ("c", u64), ("n", u64)]
+
+
+class CopyArgs(ctypes.Structure):
+    _fields_ = [("dst", u64), ("src", u64), ("ndim", i32), ("dst_dtype", i32), ("src_dtype", i32), ("pad", i32),
+                ("sizes", i64 * MAX_DIMS), ("dst_strides", i64 * MAX_DIMS), ("src_strides", i64 * MAX_DIMS)]
+
+
+class FillArgs(ctypes.Structure):
+    _fields_ = [("dst", u64), ("value_bits", u64), ("ndim", i32), ("dtype", i32), ("pad0", i32), ("pad1", i32),
+                ("sizes", i64 * MAX_DIMS), ("strides", i64 * MAX_DIMS)]
+
+
+class MmArgs(ctypes.Structure):
+    _fields_ = [("a", u64), ("b", u64), ("c", u64), ("bias", u64), ("M", i64), ("N", i64), ("K", i64), ("batch", i64),
+                ("a_sb", i64), ("a_sm", i64), ("a_sk", i64), ("b_sb", i64), ("b_sk", i64), ("b_sn", i64),
+                ("c_sb", i64), ("c_sm", i64), ("c_sn", i64), ("bias_sb", i64), ("bias_sm", i64), ("bias_sn", i64),
+                ("alpha", f32), ("beta", f32), ("has_bias", u32), ("flags", u32)]
+
+
+class MmDq8Args(ctypes.Structure):
+    _fields_ = [("x", u64), ("q", u64), ("scale", u64), ("bias", u64), ("y", u64), ("M", i64), ("N", i64), ("K", i64),
+                ("nblocks", i64), ("x_sm", i64), ("x_sk", i64), ("alpha", f32), ("beta", f32), ("has_bias", u32),
+                ("flags", u32)]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("q", u64), ("k", u64), ("v", u64), ("o", u64), ("lse", u64), ("o32", u64), ("dout", u64), ("delta", u64),
+                ("dq", u64), ("dk", u64), ("dv", u64),
+                ("q_sb", i64), ("q_sh", i64), ("q_ss", i64), ("k_sb", i64), ("k_sh", i64), ("k_ss", i64),
+                ("v_sb", i64), ("v_sh", i64), ("v_ss", i64), ("do_sb", i64), ("do_sh", i64), ("do_ss", i64),
+                ("B", i32), ("H", i32), ("Sq", i32), ("Sk", i32), ("D", i32), ("scale", f32), ("flags", u32), ("pad", u32)]
+
+
+class SoftmaxArgs(ctypes.Structure):
+    _fields_ = [("x", u64), ("y", u64), ("g", u64), ("dx", u64), ("outer", i64), ("R", i64), ("inner", i64), ("safe", u32),
+                ("pad", u32)]
+
+
+class LnArgs(ctypes.Structure):
+    _fields_ = [("x", u64), ("y", u64), ("mean", u64), ("rstd", u64), ("w", u64), ("b", u64), ("g", u64), ("dx", u64),
+                ("dw", u64), ("db", u64), ("ws", u64), ("rows", i64), ("D", i64), ("eps", f32), ("pad", u32)]
+
+
+class Dq8Args(ctypes.Structure):
+    _fields_ = [("q", u64), ("scale", u64), ("out", u64), ("rows", i64), ("cols", i64), ("nblocks", i64)]
+
+
+def ln_chunks(rows):
+    """hrt_ln_chunks (include/hrt_ops.h): partial-sum rows of the layer_norm weight gradient."""
+    return (rows + 3) // 4
+
+
+class Runtime:
+    """The hrt library with typed entry points; one per process (the runtime is a process singleton)."""
+
+    def __init__(self, path=_LIB_PATH):
+        lib = ctypes.CDLL(path)
+        sz, vp, cp = ctypes.c_size_t, ctypes.c_void_p, ctypes.c_char_p
+        sig = {
+            "hrt_init": (ctypes.c_int, []),
+            "hrt_last_error": (sz, [cp, sz]),
+            "hrt_device_name": (sz, [cp, sz]),
+            "hrt_max_alloc": (u64, []),
+            "hrt_live_bytes": (u64, []),
+            "hrt_memory_info": (i32, [ctypes.POINTER(u64)]),
+            "hrt_peak_live_bytes": (u64, []),
+            "hrt_reset_peak_live_bytes": (None, []),
+            "hrt_set_memory_limit": (None, [u64]),
+            "hrt_alloc": (u64, [u64]),
+            "hrt_free": (ctypes.c_int, [u64]),
+            "hrt_upload": (ctypes.c_int, [u64, vp, u64]),
+            "hrt_download": (ctypes.c_int, [vp, u64, u64]),
+            "hrt_copy_d2d": (ctypes.c_int, [u64, u64, u64]),
+            "hrt_kernel_index": (ctypes.c_int, [cp]),
+            "hrt_dispatch": (ctypes.c_int, [u32, vp, u32, u32, u32, u32]),
+            "hrt_synchronize": (ctypes.c_int, []),
+            "hrt_empty_cache": (sz, []),
+            "hrt_reserved_bytes": (u64, []),
+            "hrt_live_blocks": (sz, []),
+            "hrt_slab_count": (sz, []),
+            "hrt_validation_errors": (sz, []),
+            "hrt_stat": (u64, [u32]),
+            "hrt_profile_dump": (sz, [cp, sz]),
+            "hrt_coop_caps": (u32, []),
+            "hrt_event_record": (ctypes.c_int, [u32]),
+            "hrt_event_elapsed_ms": (f32, [u32, u32]),
+            "hrt_graph_begin": (ctypes.c_int, []),
+            "hrt_graph_end": (i64, []),
+            "hrt_graph_launch": (ctypes.c_int, [i64]),
+            "hrt_graph_destroy": (ctypes.c_int, [i64]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        self.lib = lib
+        self._ids = {}
+        self.check(lib.hrt_init(), "hrt_init")
+
+    def last_error(self):
+        buf = ctypes.create_string_buffer(4096)
+        self.lib.hrt_last_error(buf, len(buf))
+        return buf.value.decode(errors="replace")
+
+    def check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {self.last_error()}")
+
+    def kernel(self, name):
+        k = self._ids.get(name)
+        if k is None:
+            k = self.lib.hrt_kernel_index(name.encode())
+            if k < 0:
+                raise KeyError(f"kernel {name!r} is not registered")
+            self._ids[name] = k
+        return k
+
+    def dispatch(self, name, args):
+        """Queue operator kernel `name` with a Structure argument block (the kernel sizes its own grid)."""
+        self.check(self.lib.hrt_dispatch(self.kernel(name), ctypes.byref(args), ctypes.sizeof(args), 0, 0, 0), name)
+
+    def synchronize(self):
+        self.check(self.lib.hrt_synchronize(), "hrt_synchronize")
+
+    def event_record(self, slot):
+        self.check(self.lib.hrt_event_record(slot), "hrt_event_record")
+
+    def elapsed_ms(self, a, b):
+        ms = self.lib.hrt_event_elapsed_ms(a, b)
+        if ms < 0:
+            raise RuntimeError("hrt_event_elapsed_ms failed: " + self.last_error())
+        return ms
+
+    def graph(self, enqueue):
+        """Record everything `enqueue()` dispatches into a HIP graph; returns its id."""
+        self.check(self.lib.hrt_graph_begin(), "hrt_graph_begin")
+        try:
+            enqueue()
+        finally:
+            gid = self.lib.hrt_graph_end()
+        if gid < 0:
+            raise RuntimeError("hrt_graph_end failed: " + self.last_error())
+        return gid
+
+    def graph_launch(self, gid):
+        self.check(self.lib.hrt_graph_launch(gid), "hrt_graph_launch")
+
+    def graph_destroy(self, gid):
+        self.check(self.lib.hrt_graph_destroy(gid), "hrt_graph_destroy")
