@@ -109,16 +109,17 @@ HRT_REGISTER("attn_delta_f16", hrt_attn_args, launch_delta<F16>);
 constexpr int ST = 64;  // rows per LDS stage
 
 // ---- dK / dV -----------------------------------------------------------------------------------------------
-template <typename T, int DCH>
-__global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb, int vec_i) {
+template <typename T, int DCH, int LM>
+__global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb) {
   constexpr int DP = DCH * 32;
-  constexpr int RLD = DP + 8;  // [q][d] rows
+  constexpr int NCH = DP / 8;
+  constexpr int RLD = DP + 8;  // [q][d] rows (chunks swizzled)
   constexpr int TLD = ST + 8;  // [d][q] rows
   constexpr int STAGE = 2 * ST * RLD + 2 * DP * TLD + 2 * ST * 2;  // Q, dO, Q^T, dO^T (halves), lse2, delta (floats)
-  constexpr int NB = ST / 8 * (DP / 8);
+  constexpr int RB = ST / 8;
+  constexpr int NB = RB * NCH;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
-  const bool vec = vec_i != 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kg = wave & 1, qh = wave >> 1;
   const int rl = lane & 31, hl = lane >> 5;
@@ -128,33 +129,34 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb, 
   const int64_t b = bh / p.H, hh = bh % p.H;
   const int D = p.D, Sq = p.Sq, Sk = p.Sk;
   using S = uint16_t;
-  const S* Q = reinterpret_cast<const S*>(p.q) + b * p.q_sb + hh * p.q_sh;
-  const S* K = reinterpret_cast<const S*>(p.k) + b * p.k_sb + hh * p.k_sh;
-  const S* V = reinterpret_cast<const S*>(p.v) + b * p.v_sb + hh * p.v_sh;
-  const S* dO = reinterpret_cast<const S*>(p.dout) + b * p.do_sb + hh * p.do_sh;
-  const float* lse = reinterpret_cast<const float*>(p.lse) + bh * Sq;
-  const float* delta = reinterpret_cast<const float*>(p.delta) + bh * Sq;
+  const HK_G S* Q = gcptr<S>(p.q) + b * p.q_sb + hh * p.q_sh;
+  const HK_G S* K = gcptr<S>(p.k) + b * p.k_sb + hh * p.k_sh;
+  const HK_G S* V = gcptr<S>(p.v) + b * p.v_sb + hh * p.v_sh;
+  const HK_G S* dO = gcptr<S>(p.dout) + b * p.do_sb + hh * p.do_sh;
+  const HK_G float* lse = gcptr<float>(p.lse) + bh * Sq;
+  const HK_G float* delta = gcptr<float>(p.delta) + bh * Sq;
 
   // this lane's key: K and V as B fragments (16 d each)
   const int64_t key = kb * 64 + kg * 32 + rl;
   u32x4 kf[2 * DCH], vf[2 * DCH];
 #pragma unroll
   for (int ks = 0; ks < 2 * DCH; ++ks) {
-    kf[ks] = key < Sk ? load_row8(K + key * p.k_ss, ks * 16 + 8 * hl, D, vec) : u32x4{0, 0, 0, 0};
-    vf[ks] = key < Sk ? load_row8(V + key * p.v_ss, ks * 16 + 8 * hl, D, vec) : u32x4{0, 0, 0, 0};
+    kf[ks] = key < Sk ? load_row8<LM != LD_GATHER>(K + key * p.k_ss, ks * 16 + 8 * hl, D) : u32x4{0, 0, 0, 0};
+    vf[ks] = key < Sk ? load_row8<LM != LD_GATHER>(V + key * p.v_ss, ks * 16 + 8 * hl, D) : u32x4{0, 0, 0, 0};
   }
 
   Block8 blk;
   float sv = 0.f;
   auto load_stage = [&](int64_t q0) {
+    const bool full = q0 + ST <= Sq;
     const int bi = threadIdx.x;
     if (bi < 2 * NB) {
       const int t = bi < NB ? bi : bi - NB;
-      const int rb = t / (DP / 8), dc = t % (DP / 8);
+      const int rb = t % RB, dc = t / RB;
       if (bi < NB)
-        blk.load(Q, p.q_ss, q0 + rb * 8, Sq, dc * 8, D, vec);
+        blk.template load<LM>(Q, p.q_ss, q0 + rb * 8, Sq, dc * 8, D, full);
       else
-        blk.load(dO, p.do_ss, q0 + rb * 8, Sq, dc * 8, D, vec);
+        blk.template load<LM>(dO, p.do_ss, q0 + rb * 8, Sq, dc * 8, D, full);
     }
     if (threadIdx.x < 2 * ST) {
       const int64_t qq = q0 + (threadIdx.x & (ST - 1));
@@ -168,10 +170,10 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb, 
     const int bi = threadIdx.x;
     if (bi < 2 * NB) {
       const int t = bi < NB ? bi : bi - NB;
-      const int rb = t / (DP / 8), dc = t % (DP / 8);
+      const int rb = t % RB, dc = t / RB;
       uint16_t* rows = st + (bi < NB ? 0 : ST * RLD);
       uint16_t* cols = st + 2 * ST * RLD + (bi < NB ? 0 : DP * TLD);
-      blk.store_rows(rows, RLD, rb * 8, dc * 8);
+      blk.template store_rows<NCH>(rows, RLD, rb * 8, dc * 8);
       blk.store_cols(cols, TLD, rb * 8, dc * 8);
     }
     if (threadIdx.x < 2 * ST) reinterpret_cast<float*>(st + 2 * ST * RLD + 2 * DP * TLD)[threadIdx.x] = sv;
@@ -185,6 +187,7 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb, 
   load_stage(0);
   store_stage(lds);
   __syncthreads();
+  const int row = qh * 32 + rl;  // the query row this lane reads as an A operand
   for (int st = 0; st < nst; ++st) {
     const bool more = st + 1 < nst;
     if (more) load_stage((int64_t)(st + 1) * ST);
@@ -199,17 +202,22 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb, 
     f32x16 s = zero16(), dp = zero16();
 #pragma unroll
     for (int ks = 0; ks < 2 * DCH; ++ks) {
-      const int off = (qh * 32 + rl) * RLD + ks * 16 + 8 * hl;
+      const int off = row * RLD + Block8::swz_col<NCH>(row, ks * 16 + 8 * hl);
       s = Mfma32<T>::mac(*reinterpret_cast<const u32x4*>(Ql + off), kf[ks], s);
       dp = Mfma32<T>::mac(*reinterpret_cast<const u32x4*>(dOl + off), vf[ks], dp);
     }
     // element 4j+r: query qh*32 + 8j + 4h + r of the stage, key = this lane's key
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int ql = qh * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
-      const float pv = exp2f(s[e] * sl2 - lse2[ql]);
-      s[e] = pv;
-      dp[e] = pv * (dp[e] - dlt[ql]);
+    for (int j = 0; j < 4; ++j) {
+      const int q4 = qh * 32 + 8 * j + 4 * hl;
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + q4);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt + q4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[4 * j + r], sl2, -l4[r]));  // lse2 = +inf: padded query
+        s[4 * j + r] = pv;
+        dp[4 * j + r] = pv * (dp[4 * j + r] - d4[r]);
+      }
     }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -239,8 +247,8 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb, 
   }
   __syncthreads();
   if (qh == 1) return;
-  typename T::storage* dK = reinterpret_cast<typename T::storage*>(p.dk);
-  typename T::storage* dV = reinterpret_cast<typename T::storage*>(p.dv);
+  HK_G typename T::storage* dK = gptr<typename T::storage>(p.dk);
+  HK_G typename T::storage* dV = gptr<typename T::storage>(p.dv);
   // accumulator element 4j+r: key kg*32 + 8j + 4h + r of the block, d = n*32 + lane%32
 #pragma unroll
   for (int n = 0; n < DCH; ++n) {
@@ -258,16 +266,17 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb, 
 }
 
 // ---- dQ ------------------------------------------------------------------------------------------------------
-template <typename T, int DCH>
-__global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb, int vec_i) {
+template <typename T, int DCH, int LM>
+__global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb) {
   constexpr int DP = DCH * 32;
+  constexpr int NCH = DP / 8;
   constexpr int RLD = DP + 8;
   constexpr int TLD = ST + 8;
-  constexpr int STAGE = 2 * ST * RLD + DP * TLD;  // K, V rows, K^T
-  constexpr int NB = ST / 8 * (DP / 8);
+  constexpr int STAGE = 2 * ST * RLD + DP * TLD;  // K, V rows (swizzled), K^T
+  constexpr int RB = ST / 8;
+  constexpr int NB = RB * NCH;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
-  const bool vec = vec_i != 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int qg = wave & 1, kh = wave >> 1;
   const int rl = lane & 31, hl = lane >> 5;
@@ -277,44 +286,45 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb, in
   const int64_t b = bh / p.H, hh = bh % p.H;
   const int D = p.D, Sq = p.Sq, Sk = p.Sk;
   using S = uint16_t;
-  const S* Q = reinterpret_cast<const S*>(p.q) + b * p.q_sb + hh * p.q_sh;
-  const S* K = reinterpret_cast<const S*>(p.k) + b * p.k_sb + hh * p.k_sh;
-  const S* V = reinterpret_cast<const S*>(p.v) + b * p.v_sb + hh * p.v_sh;
-  const S* dO = reinterpret_cast<const S*>(p.dout) + b * p.do_sb + hh * p.do_sh;
+  const HK_G S* Q = gcptr<S>(p.q) + b * p.q_sb + hh * p.q_sh;
+  const HK_G S* K = gcptr<S>(p.k) + b * p.k_sb + hh * p.k_sh;
+  const HK_G S* V = gcptr<S>(p.v) + b * p.v_sb + hh * p.v_sh;
+  const HK_G S* dO = gcptr<S>(p.dout) + b * p.do_sb + hh * p.do_sh;
 
   const int64_t q = qb * 64 + qg * 32 + rl;
   const bool qv = q < Sq;
   u32x4 qf[2 * DCH], df[2 * DCH];
 #pragma unroll
   for (int ks = 0; ks < 2 * DCH; ++ks) {
-    qf[ks] = qv ? load_row8(Q + q * p.q_ss, ks * 16 + 8 * hl, D, vec) : u32x4{0, 0, 0, 0};
-    df[ks] = qv ? load_row8(dO + q * p.do_ss, ks * 16 + 8 * hl, D, vec) : u32x4{0, 0, 0, 0};
+    qf[ks] = qv ? load_row8<LM != LD_GATHER>(Q + q * p.q_ss, ks * 16 + 8 * hl, D) : u32x4{0, 0, 0, 0};
+    df[ks] = qv ? load_row8<LM != LD_GATHER>(dO + q * p.do_ss, ks * 16 + 8 * hl, D) : u32x4{0, 0, 0, 0};
   }
-  const float lse2 = qv ? reinterpret_cast<const float*>(p.lse)[bh * Sq + q] * kLog2e : INFINITY;
-  const float dlt = qv ? reinterpret_cast<const float*>(p.delta)[bh * Sq + q] : 0.f;
+  const float nlse2 = qv ? -gcptr<float>(p.lse)[bh * Sq + q] * kLog2e : -INFINITY;
+  const float dlt = qv ? gcptr<float>(p.delta)[bh * Sq + q] : 0.f;
 
   Block8 blk;
   auto load_stage = [&](int64_t k0) {
+    const bool full = k0 + ST <= Sk;
     const int bi = threadIdx.x;
     if (bi < 2 * NB) {
       const int t = bi < NB ? bi : bi - NB;
-      const int rb = t / (DP / 8), dc = t % (DP / 8);
+      const int rb = t % RB, dc = t / RB;
       if (bi < NB)
-        blk.load(K, p.k_ss, k0 + rb * 8, Sk, dc * 8, D, vec);
+        blk.template load<LM>(K, p.k_ss, k0 + rb * 8, Sk, dc * 8, D, full);
       else
-        blk.load(V, p.v_ss, k0 + rb * 8, Sk, dc * 8, D, vec);
+        blk.template load<LM>(V, p.v_ss, k0 + rb * 8, Sk, dc * 8, D, full);
     }
   };
   auto store_stage = [&](uint16_t* st) {
     const int bi = threadIdx.x;
     if (bi < 2 * NB) {
       const int t = bi < NB ? bi : bi - NB;
-      const int rb = t / (DP / 8), dc = t % (DP / 8);
+      const int rb = t % RB, dc = t / RB;
       if (bi < NB) {
-        blk.store_rows(st, RLD, rb * 8, dc * 8);
+        blk.template store_rows<NCH>(st, RLD, rb * 8, dc * 8);
         blk.store_cols(st + 2 * ST * RLD, TLD, rb * 8, dc * 8);
       } else {
-        blk.store_rows(st + ST * RLD, RLD, rb * 8, dc * 8);
+        blk.template store_rows<NCH>(st + ST * RLD, RLD, rb * 8, dc * 8);
       }
     }
   };
@@ -327,6 +337,7 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb, in
   load_stage(0);
   store_stage(lds);
   __syncthreads();
+  const int row = kh * 32 + rl;  // the key row this lane reads as an A operand
   for (int st = 0; st < nst; ++st) {
     const bool more = st + 1 < nst;
     if (more) load_stage((int64_t)(st + 1) * ST);
@@ -336,16 +347,20 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb, in
     f32x16 s = zero16(), dp = zero16();
 #pragma unroll
     for (int ks = 0; ks < 2 * DCH; ++ks) {
-      const int off = (kh * 32 + rl) * RLD + ks * 16 + 8 * hl;
+      const int off = row * RLD + Block8::swz_col<NCH>(row, ks * 16 + 8 * hl);
       s = Mfma32<T>::mac(*reinterpret_cast<const u32x4*>(Kl + off), qf[ks], s);
       dp = Mfma32<T>::mac(*reinterpret_cast<const u32x4*>(Vl + off), df[ks], dp);
     }
     // element 4j+r: key kh*32 + 8j + 4h + r of the stage, query = this lane's query
-    const int key0 = st * ST + kh * 32 + 4 * hl;
+    if (st * ST + ST > Sk) {
+      const int key0 = st * ST + kh * 32 + 4 * hl;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (key0 + 8 * (e >> 2) + (e & 3) >= Sk) s[e] = -INFINITY;
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int key = key0 + 8 * (e >> 2) + (e & 3);
-      const float pv = key < Sk ? exp2f(s[e] * sl2 - lse2) : 0.f;
+      const float pv = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, nlse2));
       dp[e] = pv * (dp[e] - dlt);
     }
 #pragma unroll
@@ -368,7 +383,7 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb, in
   }
   __syncthreads();
   if (kh == 1) return;
-  typename T::storage* dQ = reinterpret_cast<typename T::storage*>(p.dq);
+  HK_G typename T::storage* dQ = gptr<typename T::storage>(p.dq);
   // accumulator element 4j+r: query qg*32 + 8j + 4h + r of the block, d = n*32 + lane%32
 #pragma unroll
   for (int n = 0; n < DCH; ++n) {
@@ -388,14 +403,22 @@ bool launch_dkdv(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int nkb = (a.Sk + 63) / 64;
   const int64_t total = (int64_t)nkb * a.B * a.H;
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
-  const int vec = attn_vec_ok(a, true) ? 1 : 0;
+  const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
   const dim3 g((uint32_t)total);
+#define HK_L(DCH)                                                                                   \
+  if (lm == LD_FULL)                                                                                \
+    hipLaunchKernelGGL((attn_dkdv_mfma<T, DCH, LD_FULL>), g, dim3(256), 0, ctx.stream, a, nkb);        \
+  else if (lm == LD_VEC)                                                                            \
+    hipLaunchKernelGGL((attn_dkdv_mfma<T, DCH, LD_VEC>), g, dim3(256), 0, ctx.stream, a, nkb);         \
+  else                                                                                              \
+    hipLaunchKernelGGL((attn_dkdv_mfma<T, DCH, LD_GATHER>), g, dim3(256), 0, ctx.stream, a, nkb);
   switch ((a.D + 31) / 32) {
-    case 1: hipLaunchKernelGGL((attn_dkdv_mfma<T, 1>), g, dim3(256), 0, ctx.stream, a, nkb, vec); break;
-    case 2: hipLaunchKernelGGL((attn_dkdv_mfma<T, 2>), g, dim3(256), 0, ctx.stream, a, nkb, vec); break;
-    case 3: hipLaunchKernelGGL((attn_dkdv_mfma<T, 3>), g, dim3(256), 0, ctx.stream, a, nkb, vec); break;
-    default: hipLaunchKernelGGL((attn_dkdv_mfma<T, 4>), g, dim3(256), 0, ctx.stream, a, nkb, vec); break;
+    case 1: HK_L(1) break;
+    case 2: HK_L(2) break;
+    case 3: HK_L(3) break;
+    default: HK_L(4) break;
   }
+#undef HK_L
   return hrt::launch_ok(hipGetLastError(), ctx, "attn_dkdv_mfma");
 }
 
@@ -406,14 +429,22 @@ bool launch_dq(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int nqb = (a.Sq + 63) / 64;
   const int64_t total = (int64_t)nqb * a.B * a.H;
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
-  const int vec = attn_vec_ok(a, true) ? 1 : 0;
+  const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
   const dim3 g((uint32_t)total);
+#define HK_L(DCH)                                                                                   \
+  if (lm == LD_FULL)                                                                                \
+    hipLaunchKernelGGL((attn_dq_mfma<T, DCH, LD_FULL>), g, dim3(256), 0, ctx.stream, a, nqb);        \
+  else if (lm == LD_VEC)                                                                            \
+    hipLaunchKernelGGL((attn_dq_mfma<T, DCH, LD_VEC>), g, dim3(256), 0, ctx.stream, a, nqb);         \
+  else                                                                                              \
+    hipLaunchKernelGGL((attn_dq_mfma<T, DCH, LD_GATHER>), g, dim3(256), 0, ctx.stream, a, nqb);
   switch ((a.D + 31) / 32) {
-    case 1: hipLaunchKernelGGL((attn_dq_mfma<T, 1>), g, dim3(256), 0, ctx.stream, a, nqb, vec); break;
-    case 2: hipLaunchKernelGGL((attn_dq_mfma<T, 2>), g, dim3(256), 0, ctx.stream, a, nqb, vec); break;
-    case 3: hipLaunchKernelGGL((attn_dq_mfma<T, 3>), g, dim3(256), 0, ctx.stream, a, nqb, vec); break;
-    default: hipLaunchKernelGGL((attn_dq_mfma<T, 4>), g, dim3(256), 0, ctx.stream, a, nqb, vec); break;
+    case 1: HK_L(1) break;
+    case 2: HK_L(2) break;
+    case 3: HK_L(3) break;
+    default: HK_L(4) break;
   }
+#undef HK_L
   return hrt::launch_ok(hipGetLastError(), ctx, "attn_dq_mfma");
 }
 

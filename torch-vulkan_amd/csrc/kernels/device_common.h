@@ -22,6 +22,20 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Global-memory pointers.  Operand addresses arrive as integers in the argument blocks; casting them to
+// address space 1 makes the compiler emit global_load/global_store instead of flat accesses (flat
+// accesses also count against the LDS wait counter, which would make every LDS wait drain the
+// in-flight global prefetch).
+#define HK_G __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ HK_G T* gptr(uint64_t a) {
+  return reinterpret_cast<HK_G T*>(a);
+}
+template <typename T>
+__device__ __forceinline__ const HK_G T* gcptr(uint64_t a) {
+  return reinterpret_cast<const HK_G T*>(a);
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {

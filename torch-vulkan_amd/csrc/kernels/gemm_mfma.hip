@@ -39,7 +39,7 @@ struct TileLoader {
   static constexpr int ELEMS = ROWS * BK / 256;  // GATHER
   static_assert(CHUNKS % 256 == 0 || CHUNKS < 256, "tile/threads mismatch");
 
-  const uint16_t* p;
+  const HK_G uint16_t* p;
   int64_t s_r, s_k, r0, nrows, nk;
   u32x4 v[MODE == KVEC ? PER_THREAD_V : (MODE == MNVEC ? 8 * PER_THREAD_T : 1)];
   uint16_t g[MODE == GATHER ? ELEMS : 1];
@@ -53,7 +53,7 @@ struct TileLoader {
         const int r = c / (BK / 8), kc = c % (BK / 8);
         const int64_t gr = r0 + r, gk = k0 + kc * 8;
         if (c < CHUNKS && gr < nrows && gk < nk)
-          v[i] = *reinterpret_cast<const u32x4*>(p + gr * s_r + gk);
+          v[i] = *reinterpret_cast<const HK_G u32x4*>(p + gr * s_r + gk);
         else
           v[i] = u32x4{0, 0, 0, 0};
       }
@@ -67,7 +67,7 @@ struct TileLoader {
         for (int j = 0; j < 8; ++j) {
           const int64_t gk = k0 + kb * 8 + j;
           if (b < BLOCKS && gr < nrows && gk < nk)
-            v[i * 8 + j] = *reinterpret_cast<const u32x4*>(p + gk * s_k + gr);
+            v[i * 8 + j] = *reinterpret_cast<const HK_G u32x4*>(p + gk * s_k + gr);
           else
             v[i * 8 + j] = u32x4{0, 0, 0, 0};
         }
@@ -123,8 +123,8 @@ template <int ROWS, typename T>
 struct Dq8Loader {
   static constexpr int CHUNKS = ROWS * BK / 8;  // 8 int8 per chunk
   static constexpr int PT = CHUNKS / 256 > 0 ? CHUNKS / 256 : 1;
-  const int8_t* q;
-  const uint16_t* scale;
+  const HK_G int8_t* q;
+  const HK_G uint16_t* scale;
   int64_t K, nblocks, r0, nrows;
   u32x2 v[PT];
   float sc[PT];
@@ -136,7 +136,7 @@ struct Dq8Loader {
       const int r = c / (BK / 8), kc = c % (BK / 8);
       const int64_t gr = r0 + r, gk = k0 + kc * 8;
       if (c < CHUNKS && gr < nrows && gk < K) {
-        v[i] = *reinterpret_cast<const u32x2*>(q + gr * K + gk);
+        v[i] = *reinterpret_cast<const HK_G u32x2*>(q + gr * K + gk);
         sc[i] = bf16_bits_to_f32(scale[gr * nblocks + (gk >> 6)]);
       } else {
         v[i] = u32x2{0, 0};
@@ -211,8 +211,8 @@ __device__ __forceinline__ void gemm_mainloop(LA& la, LB& lb, int64_t K, uint16_
 // Epilogue: c = alpha * acc + beta * bias, one rounding; lane holds rows 4*(lane/16)+r, column lane%16
 // of every 16x16 tile.
 template <typename T, int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void gemm_epilogue(const f32x4 (&acc)[BM / WM / 16][BN / WN / 16], uint16_t* C, int64_t c_sm,
-                                              int64_t c_sn, const uint16_t* bias, int64_t bias_sm, int64_t bias_sn,
+__device__ __forceinline__ void gemm_epilogue(const f32x4 (&acc)[BM / WM / 16][BN / WN / 16], HK_G uint16_t* C, int64_t c_sm,
+                                              int64_t c_sn, const HK_G uint16_t* bias, int64_t bias_sm, int64_t bias_sn,
                                               bool has_bias, float alpha, float beta, int64_t m0, int64_t n0, int64_t M,
                                               int64_t N) {
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -247,15 +247,15 @@ __global__ __launch_bounds__(256) void mm_mfma(hrt_mm_args p, int64_t tiles_m, i
   const int64_t m0 = tm * BM, n0 = tn * BN;
   // A as rows m with K; B as rows n with K.
   TileLoader<BM, AMODE> la;
-  la.p = reinterpret_cast<const uint16_t*>(p.a) + bz * p.a_sb;
+  la.p = gcptr<uint16_t>(p.a) + bz * p.a_sb;
   la.s_r = p.a_sm, la.s_k = p.a_sk, la.r0 = m0, la.nrows = p.M, la.nk = p.K;
   TileLoader<BN, BMODE> lb;
-  lb.p = reinterpret_cast<const uint16_t*>(p.b) + bz * p.b_sb;
+  lb.p = gcptr<uint16_t>(p.b) + bz * p.b_sb;
   lb.s_r = p.b_sn, lb.s_k = p.b_sk, lb.r0 = n0, lb.nrows = p.N, lb.nk = p.K;
   f32x4 acc[BM / WM / 16][BN / WN / 16];
   gemm_mainloop<T, BM, BN, WM, WN>(la, lb, p.K, lds, acc);
-  gemm_epilogue<T, BM, BN, WM, WN>(acc, reinterpret_cast<uint16_t*>(p.c) + bz * p.c_sb, p.c_sm, p.c_sn,
-                                   reinterpret_cast<const uint16_t*>(p.bias) + bz * p.bias_sb, p.bias_sm, p.bias_sn,
+  gemm_epilogue<T, BM, BN, WM, WN>(acc, gptr<uint16_t>(p.c) + bz * p.c_sb, p.c_sm, p.c_sn,
+                                   gcptr<uint16_t>(p.bias) + bz * p.bias_sb, p.bias_sm, p.bias_sn,
                                    p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N);
 }
 
@@ -266,15 +266,15 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
   const int64_t tn = tile % tiles_n, tm = tile / tiles_n;
   const int64_t m0 = tm * BM, n0 = tn * BN;
   TileLoader<BM, AMODE> la;
-  la.p = reinterpret_cast<const uint16_t*>(p.x);
+  la.p = gcptr<uint16_t>(p.x);
   la.s_r = p.x_sm, la.s_k = p.x_sk, la.r0 = m0, la.nrows = p.M, la.nk = p.K;
   Dq8Loader<BN, T> lb;
-  lb.q = reinterpret_cast<const int8_t*>(p.q);
-  lb.scale = reinterpret_cast<const uint16_t*>(p.scale);
+  lb.q = gcptr<int8_t>(p.q);
+  lb.scale = gcptr<uint16_t>(p.scale);
   lb.K = p.K, lb.nblocks = p.nblocks, lb.r0 = n0, lb.nrows = p.N;
   f32x4 acc[BM / WM / 16][BN / WN / 16];
   gemm_mainloop<T, BM, BN, WM, WN>(la, lb, p.K, lds, acc);
-  gemm_epilogue<T, BM, BN, WM, WN>(acc, reinterpret_cast<uint16_t*>(p.y), p.N, 1, reinterpret_cast<const uint16_t*>(p.bias), 0,
+  gemm_epilogue<T, BM, BN, WM, WN>(acc, gptr<uint16_t>(p.y), p.N, 1, gcptr<uint16_t>(p.bias), 0,
                                    1, p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N);
 }
 

@@ -43,6 +43,22 @@ __device__ __forceinline__ void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
   }
 }
 
+// Two fp32 -> packed 16-bit of type T with the hardware conversion (round to nearest even; used for
+// matrix-core operands and GEMM/attention outputs, where only finite values occur in practice).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ uint32_t cvt2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t cvt2<BF16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+template <>
+__device__ __forceinline__ uint32_t cvt2<F16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+}
+
 // Convert 8 fp32 values to 8 packed 16-bit values of type T (round to nearest even).
 template <typename T>
 __device__ __forceinline__ u32x4 pack8(const float* v) {
