@@ -116,6 +116,24 @@ def test_large_logits_are_kept_fp32():
     assert oracle.rel_l2(f64(got), ro) < 6e-3
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [64, 128])
+def test_row_max_rising_across_key_stages(dtype, D):
+    """Logits that grow along the key axis by ~11 log2 units per 128 keys: every key stage raises the
+    running row max past the forward kernels' rescale threshold, so the O / l rescale runs at each stage
+    (out and lse checked; the backward recomputes P from lse and has no running max)."""
+    B, H, S, Sq = 1, 2, 512, 96
+    t = torch.arange(S, dtype=torch.float64) * (4.0 / S)
+    noise = uniform((B, H, S, D), torch.float64, 50)
+    k = (t[:, None] * torch.ones(D, dtype=torch.float64) + noise).to(dtype).contiguous()
+    q = (torch.ones(B, H, Sq, D, dtype=torch.float64) * (8.0 / np.sqrt(D))).to(dtype)
+    v = uniform((B, H, S, D), dtype, 51)
+    ro, rl = oracle.attention_fwd(f64(q), f64(k), f64(v), 1 / np.sqrt(D))
+    out, lse, *_ = torch.ops.aten._scaled_dot_product_fused_attention_overrideable(q.to(dev), k.to(dev), v.to(dev), None)
+    assert oracle.rel_l2(f64(out), ro) < REL[dtype]
+    assert np.allclose(f64(lse), rl, rtol=1e-5, atol=1e-5)
+
+
 def test_unsupported_shapes_use_the_math_path():
     B, H, S = 1, 2, 24
     q, k, v = (uniform((B, H, S, 160), torch.float32, s) for s in (21, 22, 23))

@@ -405,7 +405,7 @@ bool launch_dkdv(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
   const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
   const dim3 g((uint32_t)total);
-#define HK_L(DCH)                                                                                   \
+#define HK_LAUNCH(DCH)                                                                                   \
   if (lm == LD_FULL)                                                                                \
     hipLaunchKernelGGL((attn_dkdv_mfma<T, DCH, LD_FULL>), g, dim3(256), 0, ctx.stream, a, nkb);        \
   else if (lm == LD_VEC)                                                                            \
@@ -413,12 +413,12 @@ bool launch_dkdv(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   else                                                                                              \
     hipLaunchKernelGGL((attn_dkdv_mfma<T, DCH, LD_GATHER>), g, dim3(256), 0, ctx.stream, a, nkb);
   switch ((a.D + 31) / 32) {
-    case 1: HK_L(1) break;
-    case 2: HK_L(2) break;
-    case 3: HK_L(3) break;
-    default: HK_L(4) break;
+    case 1: HK_LAUNCH(1) break;
+    case 2: HK_LAUNCH(2) break;
+    case 3: HK_LAUNCH(3) break;
+    default: HK_LAUNCH(4) break;
   }
-#undef HK_L
+#undef HK_LAUNCH
   return hrt::launch_ok(hipGetLastError(), ctx, "attn_dkdv_mfma");
 }
 
@@ -431,7 +431,7 @@ bool launch_dq(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
   const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
   const dim3 g((uint32_t)total);
-#define HK_L(DCH)                                                                                   \
+#define HK_LAUNCH(DCH)                                                                                   \
   if (lm == LD_FULL)                                                                                \
     hipLaunchKernelGGL((attn_dq_mfma<T, DCH, LD_FULL>), g, dim3(256), 0, ctx.stream, a, nqb);        \
   else if (lm == LD_VEC)                                                                            \
@@ -439,12 +439,12 @@ bool launch_dq(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   else                                                                                              \
     hipLaunchKernelGGL((attn_dq_mfma<T, DCH, LD_GATHER>), g, dim3(256), 0, ctx.stream, a, nqb);
   switch ((a.D + 31) / 32) {
-    case 1: HK_L(1) break;
-    case 2: HK_L(2) break;
-    case 3: HK_L(3) break;
-    default: HK_L(4) break;
+    case 1: HK_LAUNCH(1) break;
+    case 2: HK_LAUNCH(2) break;
+    case 3: HK_LAUNCH(3) break;
+    default: HK_LAUNCH(4) break;
   }
-#undef HK_L
+#undef HK_LAUNCH
   return hrt::launch_ok(hipGetLastError(), ctx, "attn_dq_mfma");
 }
 

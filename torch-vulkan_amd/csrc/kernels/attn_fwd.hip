@@ -217,6 +217,215 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma(hrt_attn_args p, int nqb) {
     }
 }
 
+// ---- fast path: D = 64 or 128, 16-byte aligned rows ---------------------------------------------------------
+//
+// Differences from the general kernel above:
+//   * K and V stages go global -> LDS directly (global_load_lds_dwordx4): no staging registers and no
+//     register transposes; V stays row-major and the V^T operand is read with ds_read_b64_tr_b16;
+//   * 8 wavefronts, two per SIMD, so that one's softmax overlaps the other's MFMAs: wavefront w handles
+//     query group w & 1 (32 rows) against keys 32 (w >> 1) .. +31 of every 128-key stage, with ~150 live
+//     registers (the accumulators stay in one register file);
+//   * the running max is only raised when a row max exceeds it by more than 2^8 (P values then stay
+//     <= 256, far inside the bf16 / f16 / fp32 range), so the O rescale almost never runs;
+//   * the four key quarters of a query group are merged at the end through LDS: wavefront (g, k) finishes
+//     d block k of group g.
+constexpr float kLazy = 8.f;  // log2 of the largest unnormalised P value
+
+template <typename T, int DCH>
+__global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
+  constexpr int NW = 8;               // wavefronts
+  constexpr int NCH = DCH * 4;        // 16-byte chunks per row
+  constexpr int ROWB = NCH * 16;      // bytes per LDS tile row
+  constexpr int TILE = KST * ROWB;    // bytes per K or V stage
+  constexpr int PIECE = 3 * 16 * 64;  // floats: the three partial blocks merged into one (group, d block)
+  constexpr int PPT = TILE / (PIECE * 4);
+  static_assert(PPT >= 1 && PPT * 4 >= 2 * DCH && PPT * PIECE * 4 + 2 * NW * 64 * 4 <= TILE, "merge layout");
+  // Four separate LDS objects (not one array), so that the compiler can tell the reads of one buffer from
+  // the in-flight copies into the other and does not wait for those copies before every LDS read.
+  __shared__ __attribute__((aligned(1024))) uint8_t k0_raw[TILE], k1_raw[TILE], v0_raw[TILE], v1_raw[TILE];
+  HK_L uint8_t* const K0 = (HK_L uint8_t*)k0_raw;
+  HK_L uint8_t* const K1 = (HK_L uint8_t*)k1_raw;
+  HK_L uint8_t* const V0 = (HK_L uint8_t*)v0_raw;
+  HK_L uint8_t* const V1 = (HK_L uint8_t*)v1_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = wave & 1, kq = wave >> 1;
+  const int ql = lane & 31, hl = lane >> 5;
+  const int64_t total = (int64_t)nqb * p.B * p.H;
+  int64_t bh, qb;
+  xcd_map(blockIdx.x, total, nqb, bh, qb);
+  const int64_t b = bh / p.H, hh = bh % p.H;
+  const int Sq = p.Sq, Sk = p.Sk;
+  const uint32_t kss = (uint32_t)(p.k_ss * 2), vss = (uint32_t)(p.v_ss * 2);
+  const HK_G uint8_t* Kb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.k) + b * p.k_sb + hh * p.k_sh);
+  const HK_G uint8_t* Vb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.v) + b * p.v_sb + hh * p.v_sh);
+  const int nst = (Sk + KST - 1) / KST;
+
+  const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane), vlo = dma_lane_offsets<NCH>(vss, lane);
+  dma_tile<NCH, KST, NW>(Kb, kss, Sk, K0, wave, lane, klo);
+  dma_tile<NCH, KST, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
+
+  // Q^T operand fragments of this lane's query
+  const HK_G uint16_t* Q = gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh;
+  const int64_t q = qb * 64 + g * 32 + ql;
+  u32x4 qf[2 * DCH];
+#pragma unroll
+  for (int ks = 0; ks < 2 * DCH; ++ks)
+    qf[ks] = q < Sq ? *reinterpret_cast<const HK_G u32x4*>(Q + q * p.q_ss + ks * 16 + 8 * hl) : u32x4{0, 0, 0, 0};
+
+  // per-lane byte offsets of the A-operand fragments inside a tile
+  int koff[2 * DCH], voff[DCH][2];
+#pragma unroll
+  for (int ks = 0; ks < 2 * DCH; ++ks) koff[ks] = tile_off<NCH>(kq * 32 + ql, 2 * ks + hl);
+#pragma unroll
+  for (int n = 0; n < DCH; ++n)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = kq * 32 + 8 * t + 4 * hl + ((lane & 15) >> 2);
+      const int c = 4 * n + 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+      voff[n][t] = tile_off<NCH>(row, c) + (lane & 1) * 8;
+    }
+
+  f32x16 o[DCH];
+#pragma unroll
+  for (int n = 0; n < DCH; ++n) o[n] = zero16();
+  float m = -INFINITY, l = 0.f;  // m in log2 units of the scaled logits
+  const float sl2 = p.scale * kLog2e;
+
+  auto stage = [&](auto bc, int st) {
+    constexpr int BUF = decltype(bc)::value;
+    const int64_t key0 = (int64_t)st * KST;
+    if (st + 1 < nst) {  // next stage into the other buffer (its last readers passed the previous barrier)
+      const int valid = (int)(Sk - key0 - KST);
+      dma_tile<NCH, KST, NW>(Kb + (key0 + KST) * kss, kss, valid, BUF ? K0 : K1, wave, lane, klo);
+      dma_tile<NCH, KST, NW>(Vb + (key0 + KST) * vss, vss, valid, BUF ? V0 : V1, wave, lane, vlo);
+    }
+    const HK_L uint8_t* Kt = BUF ? K1 : K0;
+    const HK_L uint8_t* Vt = BUF ? V1 : V0;
+    f32x16 s = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 2 * DCH; ++ks) s = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]), qf[ks], s);
+    // element 4j+r: key kq*32 + 8j + 4h + r of the stage
+    if (key0 + KST > Sk) {  // ragged last stage: keys >= Sk do not exist (their rows were clamped)
+      const int64_t kbase = key0 + kq * 32 + 4 * hl;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (kbase + 8 * (e >> 2) + (e & 3) >= Sk) s[e] = -INFINITY;
+    }
+    float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int e = 2; e < 16; ++e) mx = fmaxf(mx, s[e]);
+    const float cand = halfswap_max(mx) * sl2;  // scale > 0: max commutes with the scaling
+    const bool up = cand > m + kLazy;           // m = -inf: any finite row max
+    if (__any(up)) {
+      const float mn = up ? cand : m;
+      const float alpha = up ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // m = -inf: 0, and o, l are 0
+      l *= alpha;
+#pragma unroll
+      for (int n = 0; n < DCH; ++n)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[n][e] *= alpha;
+      m = mn;
+    }
+    const float nm = m == -INFINITY ? 0.f : -m;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, nm));  // exp2(-inf) = 0 for masked keys
+      s[e] = pv;
+      l += pv;
+    }
+    const u32x4 pb0 = pack_slots<T>(s, 0, 1), pb1 = pack_slots<T>(s, 2, 3);
+#pragma unroll
+    for (int n = 0; n < DCH; ++n)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const u32x2 lo = lds_tr4(Vt + voff[n][0] + kc * 16 * ROWB);
+        const u32x2 hi = lds_tr4(Vt + voff[n][1] + kc * 16 * ROWB);
+        o[n] = Mfma32<T>::mac(u32x4{lo.x, lo.y, hi.x, hi.y}, kc ? pb1 : pb0, o[n]);
+      }
+    __syncthreads();  // waits for this wave's copies of the next stage, then for every wave
+  };
+  __syncthreads();
+  for (int st = 0; st < nst; st += 2) {
+    stage(std::integral_constant<int, 0>(), st);
+    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1);
+  }
+
+  // ---- merge the four key quarters of each query group.  Piece (g, n) = d block n of group g, finished by
+  // wavefront (g, k = n); its three incoming partial blocks live in tile (g*DCH + n) / PPT as
+  // [source slot 0..2][16][64 lanes]; m and l of every wavefront follow the pieces of tile 0.
+  auto tile_f = [&](int t) -> float* {
+    return reinterpret_cast<float*>(t == 0 ? k0_raw : t == 1 ? k1_raw : t == 2 ? v0_raw : v1_raw);
+  };
+  float* xml = tile_f(0) + PPT * PIECE;  // [wave][m, l][64 lanes]
+  xml[(wave * 2 + 0) * 64 + lane] = m;
+  xml[(wave * 2 + 1) * 64 + lane] = halfswap_sum(l);
+#pragma unroll
+  for (int n = 0; n < DCH; ++n) {
+    if (n == kq) continue;
+    const int pc = g * DCH + n;
+    float* dst = tile_f(pc / PPT) + (pc % PPT) * PIECE + ((kq - n - 1) & 3) * 16 * 64 + lane;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dst[e * 64] = o[n][e];
+  }
+  __syncthreads();
+
+  auto finish = [&](auto nc) {
+    constexpr int N = decltype(nc)::value;
+    float mw[4], aw[4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      mw[k] = xml[((2 * k + g) * 2 + 0) * 64 + lane];
+      mt = fmaxf(mt, mw[k]);
+    }
+    float L = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      aw[k] = mw[k] == -INFINITY ? 0.f : exp2f(mw[k] - mt);
+      L += aw[k] * xml[((2 * k + g) * 2 + 1) * 64 + lane];
+    }
+    if (q >= Sq) return;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    if (N == 0 && hl == 0) gptr<float>(p.lse)[bh * Sq + q] = L > 0.f ? (mt + log2f(L)) * kLn2 : -INFINITY;
+    const int pc = g * DCH + N;
+    const float* src = tile_f(pc / PPT) + (pc % PPT) * PIECE + lane;
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = o[N][e] * aw[N];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (k == N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = fmaf(aw[k], src[(((k - N - 1) & 3) * 16 + e) * 64], acc[e]);
+    }
+    HK_G typename T::storage* out = gptr<typename T::storage>(p.o) + ((b * Sq + q) * p.H + hh) * p.D;
+    HK_G float* o32 = p.o32 ? gptr<float>(p.o32) + ((b * Sq + q) * p.H + hh) * p.D : nullptr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = N * 32 + 8 * j + 4 * hl;
+      const float v0 = acc[4 * j] * inv, v1 = acc[4 * j + 1] * inv, v2 = acc[4 * j + 2] * inv, v3 = acc[4 * j + 3] * inv;
+      *reinterpret_cast<HK_G u32x2*>(out + d) = u32x2{pack2<T>(v0, v1), pack2<T>(v2, v3)};
+      if (o32) *reinterpret_cast<HK_G f32x4*>(o32 + d) = f32x4{v0, v1, v2, v3};
+    }
+  };
+  switch (kq) {
+    case 0: finish(std::integral_constant<int, 0>()); break;
+    case 1: finish(std::integral_constant<int, 1>()); break;
+    case 2: if constexpr (DCH > 2) finish(std::integral_constant<int, 2 % DCH>()); break;
+    default: if constexpr (DCH > 3) finish(std::integral_constant<int, 3 % DCH>()); break;
+  }
+}
+
+// The direct-to-LDS path needs D = 64 or 128, 16-byte aligned rows, and per-stage row offsets that fit
+// the 32-bit lane offsets of the copies.
+bool fwd_dma_ok(const hrt_attn_args& a) {
+  if (!(a.D == 64 || a.D == 128) || !attn_vec_ok(a, false)) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  return a.k_ss * 2 * (KST + 1) < lim && a.v_ss * 2 * (KST + 1) < lim;
+}
+
 template <typename T>
 bool launch_fwd(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_attn_args*>(pp);
@@ -224,8 +433,15 @@ bool launch_fwd(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int nqb = (a.Sq + 63) / 64;
   const int64_t total = (int64_t)nqb * a.B * a.H;
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
-  const int lm = !attn_vec_ok(a, false) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
   const dim3 g((uint32_t)total);
+  if (fwd_dma_ok(a)) {
+    if (a.D == 128)
+      hipLaunchKernelGGL((attn_fwd_dma<T, 4>), g, dim3(512), 0, ctx.stream, a, nqb);
+    else
+      hipLaunchKernelGGL((attn_fwd_dma<T, 2>), g, dim3(512), 0, ctx.stream, a, nqb);
+    return hrt::launch_ok(hipGetLastError(), ctx, "attn_fwd_dma");
+  }
+  const int lm = !attn_vec_ok(a, false) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
 #define HK_FWD(DCH)                                                                                      \
   if (lm == LD_FULL)                                                                                     \
     hipLaunchKernelGGL((attn_fwd_mfma<T, DCH, LD_FULL>), g, dim3(256), 0, ctx.stream, a, nqb);          \
