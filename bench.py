@@ -99,23 +99,21 @@ class Bench:
         a.do_sb, a.do_sh, a.do_ss = do.stride(0), do.stride(1), do.stride(2)
         a.B, a.H, a.Sq, a.Sk, a.D = B, H, S, S, D
         a.scale = 1.0 / D ** 0.5
+        # dQ computes delta = rowsum(O32 * dO) first (the shim's order: fwd, dQ + delta, dK/dV)
         ad = abi.AttnArgs.from_buffer_copy(a)
-        ad.o, ad.flags = o32.data_ptr(), abi.ATTN_O_F32
+        ad.o, ad.flags = o32.data_ptr(), abi.ATTN_O_F32 | abi.ATTN_DQ_DELTA
         keep = (q, k, v, do, o, o32, lse, delta, dq, dk, dv)
         names = {n: f"attn_{n}_mfma_{dtype}" for n in ("fwd", "dkdv", "dq")}
-        names["delta"] = f"attn_delta_{dtype}"
 
         def step(_i=0):
             self.rt.dispatch(names["fwd"], a)
-            self.rt.dispatch(names["delta"], ad)
+            self.rt.dispatch(names["dq"], ad)
             self.rt.dispatch(names["dkdv"], a)
-            self.rt.dispatch(names["dq"], a)
 
         kernels = {
             "fwd": lambda _i: self.rt.dispatch(names["fwd"], a),
-            "delta": lambda _i: self.rt.dispatch(names["delta"], ad),
+            "dq": lambda _i: self.rt.dispatch(names["dq"], ad),
             "dkdv": lambda _i: self.rt.dispatch(names["dkdv"], a),
-            "dq": lambda _i: self.rt.dispatch(names["dq"], a),
         }
         return step, kernels, keep, names
 
@@ -137,19 +135,15 @@ class Bench:
         ms = rt.elapsed_ms(0, 1) / args.steps
         rt.graph_destroy(gid)
         # per-kernel average launch durations (20 back-to-back launches each)
-        per = {n: self.time_graph(kernels[n], 20) for n in ("fwd", "delta", "dkdv", "dq")}
+        per = {n: self.time_graph(kernels[n], 20) for n in ("fwd", "dq", "dkdv")}
         unit = 2.0 * B * H * S * S * D  # one S x S x D product
-        algo = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 1 * unit}  # S, dP shared by dK/dV; dQ's S, dP are recompute
-        delta_bytes = B * S * H * D * (4 + 2) + B * H * S * 4
+        # S, dP are shared by dK/dV; dQ's S and dP are recomputation, and its delta pass is memory work
+        algo = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 1 * unit}
         kstats = {}
         for n, t in per.items():
-            e = {"kernel": names[n], "avg_us": round(t * 1e3, 3)}
-            if n in algo:
-                e["algo_tflop"] = algo[n] / 1e12
-                e["tflops"] = round(algo[n] / (t * 1e-3) / 1e12, 2)
-                e["frac_of_bf16_peak"] = round(e["tflops"] / PEAK_TFLOPS["bf16"], 4)
-            else:
-                e["gbs"] = round(delta_bytes / (t * 1e-3) / 1e9, 1)
+            e = {"kernel": names[n], "avg_us": round(t * 1e3, 3), "algo_tflop": algo[n] / 1e12}
+            e["tflops"] = round(algo[n] / (t * 1e-3) / 1e12, 2)
+            e["frac_of_bf16_peak"] = round(e["tflops"] / PEAK_TFLOPS["bf16"], 4)
             kstats[n] = e
         dom = max(("fwd", "dkdv", "dq"), key=lambda n: per[n])
         ach = algo[dom] / (per[dom] * 1e-3) / 1e12

@@ -106,6 +106,11 @@ typedef struct hrt_mm_dq8_args {
  * For bf16/f16 the matrix-core kernels round P and dS to dt before the second product, as
  * attn_coop.comp.in:182-183, 235-236, 283-284; the f32 kernels keep everything fp32. */
 #define HRT_ATTN_O_F32 1u
+/* "attn_dq_{bf16,f16}" with this flag first computes delta (as "attn_delta_{dt}", from o per
+ * HRT_ATTN_O_F32) into `delta`, then dQ from it; "attn_dkdv_{dt}" can then run on that delta.  No
+ * counterpart in the reference, which always launches the delta pass on its own (csrc/ops_attn.cpp:240-248):
+ * it saves a launch and a second read of dO. */
+#define HRT_ATTN_DQ_DELTA 2u
 typedef struct hrt_attn_args {
   uint64_t q, k, v;
   uint64_t o, lse, o32;

@@ -74,7 +74,7 @@ def test_fused_matches_oracle(shape, dtype):
         e = oracle.rel_l2(f64(got), ref)
         assert e < REL[dtype], f"{name} {shape} {dtype}: rel-L2 {e}"
     kc = torch_vulkan.kernel_counts()
-    assert kc.get(OVR, 0) >= 1 and kc.get(OVR + "_backward", 0) >= 3, kc
+    assert kc.get(OVR, 0) >= 1 and kc.get(OVR + "_backward", 0) >= 2, kc
     fb = torch_vulkan.fallback_counts()
     assert not any("softmax" in n or "bmm" in n for n in fb), fb
 

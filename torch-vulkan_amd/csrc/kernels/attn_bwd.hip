@@ -396,6 +396,404 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb) {
   }
 }
 
+// ---- dQ fast path: D = 64 or 128, 16-byte aligned rows ------------------------------------------------------
+//
+// The forward kernel's structure applied to dQ: K and V stages (128 keys) go global -> LDS directly and
+// double-buffered; 8 wavefronts, wave (g = w & 1, k = w >> 1) handles query group g (32 rows of the 64-row
+// block, this lane's query held as Q^T / dO^T B fragments in registers) against keys 32 k .. +31 of every
+// stage.  Per stage: S^T = K Q^T, dP^T = V dO^T (A operands: K / V rows from LDS), P^T = exp2(S^T sl2 -
+// lse log2e), dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16 and dS^T
+// packed (rounded to the input dtype, attn_coop.comp.in:283-284) straight from the accumulators.  The four
+// key quarters are summed through LDS at the end and dQ is written as coalesced 32-element row pieces.
+// With WITH_DELTA the kernel first computes delta = rowsum(O dO) for its rows (one quarter of d per key
+// quarter, summed through LDS, vkrt/shaders/attn.comp.in:210-240) and stores it for the dK/dV kernel.
+constexpr int KST2 = 128;  // keys per LDS stage
+
+template <typename T, int DCH, bool OF32, bool WITH_DELTA>
+__global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
+  constexpr int NW = 8;
+  constexpr int NCH = DCH * 4;
+  constexpr int ROWB = NCH * 16;
+  constexpr int TILE = KST2 * ROWB;
+  constexpr int PIECE = 3 * 16 * 64;
+  constexpr int PPT = TILE / (PIECE * 4);
+  constexpr int KSQ = DCH / 2;  // 16-wide d chunks per quarter of d
+  static_assert(PPT >= 1 && PPT * 4 >= 2 * DCH && 32 * 36 <= PIECE, "merge layout");
+  __shared__ __attribute__((aligned(1024))) uint8_t k0_raw[TILE], k1_raw[TILE], v0_raw[TILE], v1_raw[TILE];
+  __shared__ float xdel[4][64];
+  HK_L uint8_t* const K0 = (HK_L uint8_t*)k0_raw;
+  HK_L uint8_t* const K1 = (HK_L uint8_t*)k1_raw;
+  HK_L uint8_t* const V0 = (HK_L uint8_t*)v0_raw;
+  HK_L uint8_t* const V1 = (HK_L uint8_t*)v1_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = wave & 1, kq = wave >> 1;
+  const int ql = lane & 31, hl = lane >> 5;
+  uint32_t bh32, qb32;
+  xcd_map32(blockIdx.x, (uint32_t)nqb * p.B * p.H, nqb, bh32, qb32);
+  const int64_t bh = bh32, qb = qb32, b = bh32 / (uint32_t)p.H, hh = bh32 % (uint32_t)p.H;
+  const int Sq = p.Sq, Sk = p.Sk;
+  const uint32_t kss = (uint32_t)(p.k_ss * 2), vss = (uint32_t)(p.v_ss * 2);
+  const HK_G uint8_t* Kb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.k) + b * p.k_sb + hh * p.k_sh);
+  const HK_G uint8_t* Vb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.v) + b * p.v_sb + hh * p.v_sh);
+  const int nst = (Sk + KST2 - 1) / KST2;
+
+  const int j0 = wave * (KST2 * NCH / 64 / NW);
+  const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane, j0), vlo = dma_lane_offsets<NCH>(vss, lane, j0);
+  dma_tile<NCH, KST2, NW>(Kb, kss, Sk, K0, wave, lane, klo);
+  dma_tile<NCH, KST2, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
+
+  const int64_t q = qb * 64 + g * 32 + ql;
+  const bool qv = q < Sq;
+  const HK_G uint16_t* Qr = gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh + q * p.q_ss;
+  const HK_G uint16_t* dOr = gcptr<uint16_t>(p.dout) + b * p.do_sb + hh * p.do_sh + q * p.do_ss;
+  u32x4 qf[2 * DCH], df[2 * DCH];
+#pragma unroll
+  for (int ks = 0; ks < 2 * DCH; ++ks) {
+    qf[ks] = qv ? *reinterpret_cast<const HK_G u32x4*>(Qr + ks * 16 + 8 * hl) : u32x4{0, 0, 0, 0};
+    df[ks] = qv ? *reinterpret_cast<const HK_G u32x4*>(dOr + ks * 16 + 8 * hl) : u32x4{0, 0, 0, 0};
+  }
+  const float nlse2 = qv ? -gcptr<float>(p.lse)[bh * Sq + q] * kLog2e : -INFINITY;  // P = 0 for padded rows
+  float dlt = 0.f;
+  if constexpr (WITH_DELTA) {
+    float part = 0.f;
+    if (qv) {
+      const int64_t orow = ((b * Sq + q) * p.H + hh) * p.D;
+#pragma unroll
+      for (int i = 0; i < KSQ; ++i) {
+        const int d0 = (kq * KSQ + i) * 16 + 8 * hl;
+        const u32x4 dv = *reinterpret_cast<const HK_G u32x4*>(dOr + d0);
+        float ov[8];
+        if constexpr (OF32) {
+          const f32x4 a = *reinterpret_cast<const HK_G f32x4*>(gcptr<float>(p.o) + orow + d0);
+          const f32x4 c = *reinterpret_cast<const HK_G f32x4*>(gcptr<float>(p.o) + orow + d0 + 4);
+          ov[0] = a[0], ov[1] = a[1], ov[2] = a[2], ov[3] = a[3], ov[4] = c[0], ov[5] = c[1], ov[6] = c[2], ov[7] = c[3];
+        } else {
+          const u32x4 a = *reinterpret_cast<const HK_G u32x4*>(gcptr<uint16_t>(p.o) + orow + d0);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) ov[2 * w] = lo16<T>(a[w]), ov[2 * w + 1] = hi16<T>(a[w]);
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) part += ov[2 * w] * lo16<T>(dv[w]) + ov[2 * w + 1] * hi16<T>(dv[w]);
+      }
+    }
+    part = halfswap_sum(part);
+    if (hl == 0) xdel[kq][g * 32 + ql] = part;
+  } else {
+    dlt = qv ? gcptr<float>(p.delta)[bh * Sq + q] : 0.f;
+  }
+
+  int koff[2 * DCH], voff[DCH][2];
+#pragma unroll
+  for (int ks = 0; ks < 2 * DCH; ++ks) koff[ks] = tile_off<NCH>(kq * 32 + ql, 2 * ks + hl);
+#pragma unroll
+  for (int n = 0; n < DCH; ++n)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = kq * 32 + 8 * t + 4 * hl + ((lane & 15) >> 2);
+      const int c = 4 * n + 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+      voff[n][t] = tile_off<NCH>(row, c) + (lane & 1) * 8;
+    }
+  f32x16 acc[DCH];
+#pragma unroll
+  for (int n = 0; n < DCH; ++n) acc[n] = zero16();
+  const float sl2 = p.scale * kLog2e;
+
+  __syncthreads();  // stage 0 in LDS; partial deltas published
+  if constexpr (WITH_DELTA) {
+    dlt = xdel[0][g * 32 + ql] + xdel[1][g * 32 + ql] + xdel[2][g * 32 + ql] + xdel[3][g * 32 + ql];
+    if (kq == 0 && hl == 0 && qv) gptr<float>(p.delta)[bh * Sq + q] = dlt;
+  }
+
+  auto stage = [&](auto bc, int st) {
+    constexpr int BUF = decltype(bc)::value;
+    const int64_t key0 = (int64_t)st * KST2;
+    if (st + 1 < nst) {
+      const int valid = (int)(Sk - key0 - KST2);
+      dma_tile<NCH, KST2, NW>(Kb + (key0 + KST2) * kss, kss, valid, BUF ? K0 : K1, wave, lane, klo);
+      dma_tile<NCH, KST2, NW>(Vb + (key0 + KST2) * vss, vss, valid, BUF ? V0 : V1, wave, lane, vlo);
+    }
+    const HK_L uint8_t* Kt = BUF ? K1 : K0;
+    const HK_L uint8_t* Vt = BUF ? V1 : V0;
+    f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 2 * DCH; ++ks) {
+      s = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]), qf[ks], s);
+      dp = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Vt + koff[ks]), df[ks], dp);
+    }
+    // element 4j+r: key kq*32 + 8j + 4h + r of the stage, query = this lane's
+    if (key0 + KST2 > Sk) {
+      const int64_t kbase = key0 + kq * 32 + 4 * hl;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (kbase + 8 * (e >> 2) + (e & 3) >= Sk) s[e] = -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, nlse2));
+      dp[e] = pv * (dp[e] - dlt);
+    }
+    const u32x4 d0 = pack_slots<T>(dp, 0, 1), d1 = pack_slots<T>(dp, 2, 3);
+#pragma unroll
+    for (int n = 0; n < DCH; ++n)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const u32x2 lo = lds_tr4(Kt + voff[n][0] + kc * 16 * ROWB);
+        const u32x2 hi = lds_tr4(Kt + voff[n][1] + kc * 16 * ROWB);
+        acc[n] = Mfma32<T>::mac(u32x4{lo.x, lo.y, hi.x, hi.y}, kc ? d1 : d0, acc[n]);
+      }
+    __syncthreads();
+  };
+  for (int st = 0; st < nst; st += 2) {
+    stage(std::integral_constant<int, 0>(), st);
+    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1);
+  }
+
+  // ---- sum the four key quarters: piece (g, n) = d block n of group g, finished by wavefront (g, k = n)
+  auto tile_f = [&](int t) -> float* {
+    return reinterpret_cast<float*>(t == 0 ? k0_raw : t == 1 ? k1_raw : t == 2 ? v0_raw : v1_raw);
+  };
+#pragma unroll
+  for (int n = 0; n < DCH; ++n) {
+    if (n == kq) continue;
+    const int pc = g * DCH + n;
+    float* dst = tile_f(pc / PPT) + (pc % PPT) * PIECE + ((kq - n - 1) & 3) * 16 * 64 + lane;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dst[e * 64] = acc[n][e];
+  }
+  __syncthreads();
+  auto finish = [&](auto nc) {
+    constexpr int N = decltype(nc)::value;
+    const int pc = g * DCH + N;
+    float* const area = tile_f(pc / PPT) + (pc % PPT) * PIECE;
+    f32x16 r = acc[N];
+#pragma unroll
+    for (int sl = 0; sl < 3; ++sl)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) r[e] += area[(sl * 16 + e) * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<f32x4*>(area + ql * 36 + 8 * j + 4 * hl) =
+          f32x4{r[4 * j] * p.scale, r[4 * j + 1] * p.scale, r[4 * j + 2] * p.scale, r[4 * j + 3] * p.scale};
+    const int c4 = (lane & 7) * 4;
+#pragma unroll
+    for (int ps = 0; ps < 4; ++ps) {
+      const int qq = ps * 8 + (lane >> 3);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(area + qq * 36 + c4);
+      const int64_t qrow = qb * 64 + g * 32 + qq;
+      if (qrow < Sq)
+        *reinterpret_cast<HK_G u32x2*>(gptr<uint16_t>(p.dq) + ((b * Sq + qrow) * p.H + hh) * p.D + N * 32 + c4) =
+            u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+    }
+  };
+  switch (kq) {
+    case 0: finish(std::integral_constant<int, 0>()); break;
+    case 1: finish(std::integral_constant<int, 1>()); break;
+    case 2: if constexpr (DCH > 2) finish(std::integral_constant<int, 2 % DCH>()); break;
+    default: if constexpr (DCH > 3) finish(std::integral_constant<int, 3 % DCH>()); break;
+  }
+}
+
+// ---- dK / dV fast path: D = 64 or 128, 16-byte aligned rows -------------------------------------------------
+//
+// Per workgroup 64 keys; Q and dO stream through LDS in double-buffered 64-query stages copied global ->
+// LDS directly.  8 wavefronts on v_mfma_f32_16x16x32 (see mfma_common.h for its lane layout): wave
+// (k = w & 3, h = w >> 2) owns keys 16 k .. +15 of the block (their K and V rows held as B fragments) and
+// query rows 32 h .. +31 of every stage, so its dK/dV partials are 16 keys x D each (64 registers for
+// D = 128) and every LDS fragment read is conflict-free.  Per stage and 16-query tile t:
+//   S_t = Q_t K^T, dP_t = dO_t V^T            (lane = key, 4 queries 4 g + i per tile, g = lane / 16)
+//   P = exp2(S sl2 - lse log2e), dS = P (dP - delta)
+//   dV += P^T dO, dK += dS^T Q                (A = P^T / dS^T packed from the two tiles' accumulators as
+//                                              the 32 k-slots {4 g + i, 16 + 4 g + i}; B = dO / Q read
+//                                              column-wise with ds_read_b64_tr_b16 in the same slot order)
+// lse and delta for the next stage are prefetched into registers.  The two query halves are summed through
+// LDS at the end and dK (scaled), dV are written as coalesced rows.  P and dS are rounded to the input
+// dtype before their products, as attn_coop.comp.in:235-236, 283-284.
+constexpr int QST = 64;  // queries per LDS stage
+
+template <typename T, int DCH>
+__global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
+  constexpr int NW = 8;
+  constexpr int NCH = DCH * 4;
+  constexpr int ROWB = NCH * 16;
+  constexpr int TILE = QST * ROWB;   // bytes per Q or dO stage
+  constexpr int NDT = DCH * 2;       // 16-wide d tiles
+  __shared__ __attribute__((aligned(1024))) uint8_t q0_raw[TILE], q1_raw[TILE], o0_raw[TILE], o1_raw[TILE];
+  HK_L uint8_t* const Q0 = (HK_L uint8_t*)q0_raw;
+  HK_L uint8_t* const Q1 = (HK_L uint8_t*)q1_raw;
+  HK_L uint8_t* const O0 = (HK_L uint8_t*)o0_raw;
+  HK_L uint8_t* const O1 = (HK_L uint8_t*)o1_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kg = wave & 3, qh = wave >> 2;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  uint32_t bh32, kb32;
+  xcd_map32(blockIdx.x, (uint32_t)nkb * p.B * p.H, nkb, bh32, kb32);
+  const int64_t bh = bh32, kb = kb32, b = bh32 / (uint32_t)p.H, hh = bh32 % (uint32_t)p.H;
+  const int Sq = p.Sq, Sk = p.Sk;
+  const uint32_t qss = (uint32_t)(p.q_ss * 2), oss = (uint32_t)(p.do_ss * 2);
+  const HK_G uint8_t* Qb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh);
+  const HK_G uint8_t* Ob = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.dout) + b * p.do_sb + hh * p.do_sh);
+  const int nst = (Sq + QST - 1) / QST;
+
+  const int j0 = wave * (QST * NCH / 64 / NW);
+  const DmaLanes qlo = dma_lane_offsets<NCH>(qss, lane, j0), olo = dma_lane_offsets<NCH>(oss, lane, j0);
+  dma_tile<NCH, QST, NW>(Qb, qss, Sq, Q0, wave, lane, qlo);
+  dma_tile<NCH, QST, NW>(Ob, oss, Sq, O0, wave, lane, olo);
+
+  // this lane's key (column l16 of the 16x16 tiles): K and V as B fragments, d = 32 ks + 8 g + i
+  const int64_t key = kb * 64 + kg * 16 + l16;
+  const bool kv = key < Sk;
+  const HK_G uint16_t* Kr = gcptr<uint16_t>(p.k) + b * p.k_sb + hh * p.k_sh + key * p.k_ss;
+  const HK_G uint16_t* Vr = gcptr<uint16_t>(p.v) + b * p.v_sb + hh * p.v_sh + key * p.v_ss;
+  u32x4 kf[DCH], vf[DCH];
+#pragma unroll
+  for (int ks = 0; ks < DCH; ++ks) {
+    kf[ks] = kv ? *reinterpret_cast<const HK_G u32x4*>(Kr + ks * 32 + 8 * g4) : u32x4{0, 0, 0, 0};
+    vf[ks] = kv ? *reinterpret_cast<const HK_G u32x4*>(Vr + ks * 32 + 8 * g4) : u32x4{0, 0, 0, 0};
+  }
+
+  // lse (as -lse log2e) and delta of this lane's 8 queries of a stage: tile t, row 32 qh + 16 t + 4 g + i
+  const HK_G float* lseb = gcptr<float>(p.lse) + bh * Sq;
+  const HK_G float* dltb = gcptr<float>(p.delta) + bh * Sq;
+  float nl[8], dl[8];  // lse, delta
+  auto fetch = [&](int st, float* nlo, float* dlo) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t qq = (int64_t)st * QST + qh * 32 + t * 16 + 4 * g4 + i;
+        nlo[t * 4 + i] = qq < Sq ? lseb[qq] : INFINITY;  // +inf: P = 0 for padded query rows
+        dlo[t * 4 + i] = qq < Sq ? dltb[qq] : 0.f;
+      }
+  };
+  fetch(0, nl, dl);
+
+  // per-lane byte offsets: A-operand rows (query 32 qh + 16 t + l16, chunk 4 ks + g; t adds 16 rows, which
+  // keeps the swizzle) and B-operand column reads (rows 32 qh + 4 g + (l16 >> 2) (+16 for the second read),
+  // columns 16 dt + 4 (l16 & 3))
+  int roff[DCH], coff[NDT];
+#pragma unroll
+  for (int ks = 0; ks < DCH; ++ks) roff[ks] = tile_off<NCH>(qh * 32 + l16, 4 * ks + g4);
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+    coff[dt] = tile_off<NCH>(qh * 32 + 4 * g4 + (l16 >> 2), 2 * dt + ((l16 >> 1) & 1)) + (l16 & 1) * 8;
+
+  f32x4 dk[NDT], dv[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) dk[dt] = dv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float sl2 = p.scale * kLog2e;
+
+  __syncthreads();
+  auto stage = [&](auto bc, int st) {
+    constexpr int BUF = decltype(bc)::value;
+    const int64_t q0 = (int64_t)st * QST;
+    if (st + 1 < nst) {
+      const int valid = (int)(Sq - q0 - QST);
+      dma_tile<NCH, QST, NW>(Qb + (q0 + QST) * qss, qss, valid, BUF ? Q0 : Q1, wave, lane, qlo);
+      dma_tile<NCH, QST, NW>(Ob + (q0 + QST) * oss, oss, valid, BUF ? O0 : O1, wave, lane, olo);
+    }
+    float nn[8], dn[8];
+    if (st + 1 < nst) fetch(st + 1, nn, dn);
+    const HK_L uint8_t* Qt = BUF ? Q1 : Q0;
+    const HK_L uint8_t* Ot = BUF ? O1 : O0;
+    f32x4 s[2], dp[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = dp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < DCH; ++ks) {
+        s[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Qt + roff[ks] + t * 16 * ROWB), kf[ks], s[t]);
+        dp[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Ot + roff[ks] + t * 16 * ROWB), vf[ks], dp[t]);
+      }
+    }
+    float pv[8], ds[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pe = __builtin_amdgcn_exp2f(fmaf(s[t][i], sl2, -nl[t * 4 + i] * kLog2e));
+        pv[t * 4 + i] = pe;
+        ds[t * 4 + i] = pe * (dp[t][i] - dl[t * 4 + i]);
+      }
+    const u32x4 pa = u32x4{cvt2<T>(pv[0], pv[1]), cvt2<T>(pv[2], pv[3]), cvt2<T>(pv[4], pv[5]), cvt2<T>(pv[6], pv[7])};
+    const u32x4 da = u32x4{cvt2<T>(ds[0], ds[1]), cvt2<T>(ds[2], ds[3]), cvt2<T>(ds[4], ds[5]), cvt2<T>(ds[6], ds[7])};
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const u32x2 a0 = lds_tr4(Ot + coff[dt]), a1 = lds_tr4(Ot + coff[dt] + 16 * ROWB);
+      dv[dt] = Mfma<T>::mac(pa, u32x4{a0.x, a0.y, a1.x, a1.y}, dv[dt]);
+      const u32x2 b0 = lds_tr4(Qt + coff[dt]), b1 = lds_tr4(Qt + coff[dt] + 16 * ROWB);
+      dk[dt] = Mfma<T>::mac(da, u32x4{b0.x, b0.y, b1.x, b1.y}, dk[dt]);
+    }
+    if (st + 1 < nst) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) nl[i] = nn[i], dl[i] = dn[i];
+    }
+    __syncthreads();
+  };
+  for (int st = 0; st < nst; st += 2) {
+    stage(std::integral_constant<int, 0>(), st);
+    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1);
+  }
+
+  // ---- sum the two query halves: wave (k, 1) hands its partials to wave (k, 0) through tile k's area, which
+  // wave (k, 0) then reuses to transpose the results into [key][d] rows for coalesced stores
+  float* const area = reinterpret_cast<float*>(kg == 0 ? q0_raw : kg == 1 ? q1_raw : kg == 2 ? o0_raw : o1_raw);
+  static_assert(2 * NDT * 4 * 64 * 4 <= TILE, "partials fit a tile");
+  if (qh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        area[((0 * NDT + dt) * 4 + i) * 64 + lane] = dk[dt][i];
+        area[((1 * NDT + dt) * 4 + i) * 64 + lane] = dv[dt][i];
+      }
+  }
+  __syncthreads();
+  if (qh == 1) return;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dk[dt][i] = (dk[dt][i] + area[((0 * NDT + dt) * 4 + i) * 64 + lane]) * p.scale;
+      dv[dt][i] += area[((1 * NDT + dt) * 4 + i) * 64 + lane];
+    }
+  // accumulator element i of d tile dt: key 4 g + i, d = 16 dt + l16.  Transposed through the area into
+  // [key][d] rows of DP + 4 floats (conflict-free writes), dK then dV, and stored 8 d per lane.
+  constexpr int RS = DCH * 32 + 4;
+  constexpr int LPR = DCH * 4;  // lanes per row
+  static_assert(16 * RS * 4 <= TILE, "transposed results fit a tile");
+  auto emit = [&](const f32x4* acc, uint64_t dst_base) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) area[(4 * g4 + i) * RS + 16 * dt + l16] = acc[dt][i];
+#pragma unroll
+    for (int ps = 0; ps < 16 * LPR / 64; ++ps) {
+      const int r = ps * (64 / LPR) + lane / LPR, c8 = (lane % LPR) * 8;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(area + r * RS + c8);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(area + r * RS + c8 + 4);
+      const int64_t kk = kb * 64 + kg * 16 + r;
+      if (kk < Sk)
+        *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + ((b * Sk + kk) * p.H + hh) * p.D + c8) =
+            u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+    }
+  };
+  emit(dk, p.dk);
+  emit(dv, p.dv);  // same wavefront: its LDS reads of dK's rows complete before these writes
+}
+
+// The direct-to-LDS paths need D = 64 or 128, 16-byte aligned rows (q, k, v, dout) and per-stage row
+// offsets that fit the 32-bit lane offsets of the copies.
+bool bwd_dma_ok(const hrt_attn_args& a) {
+  if (!(a.D == 64 || a.D == 128) || !attn_vec_ok(a, true)) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  return a.k_ss * 2 * (KST2 + 1) < lim && a.v_ss * 2 * (KST2 + 1) < lim && a.q_ss * 2 * (KST2 + 1) < lim &&
+         a.do_ss * 2 * (KST2 + 1) < lim;
+}
+
 template <typename T>
 bool launch_dkdv(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_attn_args*>(pp);
@@ -403,8 +801,15 @@ bool launch_dkdv(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int nkb = (a.Sk + 63) / 64;
   const int64_t total = (int64_t)nkb * a.B * a.H;
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
-  const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
   const dim3 g((uint32_t)total);
+  if (bwd_dma_ok(a)) {
+    if (a.D == 128)
+      hipLaunchKernelGGL((attn_dkdv_dma<T, 4>), g, dim3(512), 0, ctx.stream, a, nkb);
+    else
+      hipLaunchKernelGGL((attn_dkdv_dma<T, 2>), g, dim3(512), 0, ctx.stream, a, nkb);
+    return hrt::launch_ok(hipGetLastError(), ctx, "attn_dkdv_dma");
+  }
+  const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
 #define HK_LAUNCH(DCH)                                                                                   \
   if (lm == LD_FULL)                                                                                \
     hipLaunchKernelGGL((attn_dkdv_mfma<T, DCH, LD_FULL>), g, dim3(256), 0, ctx.stream, a, nkb);        \
@@ -429,8 +834,28 @@ bool launch_dq(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int nqb = (a.Sq + 63) / 64;
   const int64_t total = (int64_t)nqb * a.B * a.H;
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
-  const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
+  const bool with_delta = (a.flags & HRT_ATTN_DQ_DELTA) != 0;
+  const bool of32 = (a.flags & HRT_ATTN_O_F32) != 0;
   const dim3 g((uint32_t)total);
+  if (bwd_dma_ok(a)) {
+    if (with_delta && !ctx.check(a.o, (uint64_t)a.B * a.H * a.Sq * a.D * (of32 ? 4 : 2), "o")) return false;
+#define HK_DQ(DCH)                                                                                          \
+  if (!with_delta)                                                                                          \
+    hipLaunchKernelGGL((attn_dq_dma<T, DCH, false, false>), g, dim3(512), 0, ctx.stream, a, nqb);            \
+  else if (of32)                                                                                            \
+    hipLaunchKernelGGL((attn_dq_dma<T, DCH, true, true>), g, dim3(512), 0, ctx.stream, a, nqb);              \
+  else                                                                                                      \
+    hipLaunchKernelGGL((attn_dq_dma<T, DCH, false, true>), g, dim3(512), 0, ctx.stream, a, nqb);
+    if (a.D == 128) {
+      HK_DQ(4)
+    } else {
+      HK_DQ(2)
+    }
+#undef HK_DQ
+    return hrt::launch_ok(hipGetLastError(), ctx, "attn_dq_dma");
+  }
+  if (with_delta && !launch_delta<T>(pp, nullptr, ctx)) return false;
+  const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
 #define HK_LAUNCH(DCH)                                                                                   \
   if (lm == LD_FULL)                                                                                \
     hipLaunchKernelGGL((attn_dq_mfma<T, DCH, LD_FULL>), g, dim3(256), 0, ctx.stream, a, nqb);        \

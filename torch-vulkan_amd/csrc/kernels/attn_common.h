@@ -144,6 +144,15 @@ __device__ __forceinline__ void xcd_map(int64_t id, int64_t total, int64_t nblk,
   blk = logical % nblk;
 }
 
+// The same mapping in 32-bit arithmetic (grids are below 2^31 workgroups; 64-bit division is a long
+// instruction sequence).
+__device__ __forceinline__ void xcd_map32(uint32_t id, uint32_t total, uint32_t nblk, uint32_t& bh, uint32_t& blk) {
+  uint32_t logical = id;
+  if (total % 8 == 0) logical = (id % 8) * (total / 8) + id / 8;
+  bh = logical / nblk;
+  blk = logical % nblk;
+}
+
 // Natural-log constants for the exp2 formulation.
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -185,35 +194,37 @@ __device__ __forceinline__ void dma16(const HK_G uint8_t* src, HK_L uint8_t* lds
 // The wavefront-uniform part of each address (row0 + the instruction's first row) is kept in scalar
 // registers.  The per-lane part depends only on the lane and on the instruction index modulo the swizzle
 // period (swz uses row bits 0..3 and an instruction covers 64 / NCH rows, so the pattern repeats every
-// 16 NCH / 64 instructions); full tiles use those loop-invariant lane offsets (dma_lane_offsets), ragged
-// tiles recompute clamped offsets.
+// 16 NCH / 64 instructions, a divisor of 4); full tiles use those loop-invariant lane offsets
+// (dma_lane_offsets), ragged tiles recompute clamped offsets.
 struct DmaLanes {
   uint32_t off[4];
 };
+// Lane offsets of instructions j0 .. j0 + 3 (j0 = the wavefront's first instruction index in the tile).
 template <int NCH>
-__device__ __forceinline__ DmaLanes dma_lane_offsets(uint32_t ss, int lane) {
+__device__ __forceinline__ DmaLanes dma_lane_offsets(uint32_t ss, int lane, int j0) {
   constexpr int RPI = 64 / NCH;
   const int rsub = lane / NCH, slot = lane % NCH;
   DmaLanes d;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = i * RPI + rsub;
+    const int row = (j0 + i) * RPI + rsub;
     d.off[i] = (uint32_t)rsub * ss + (uint32_t)((slot ^ tile_swz<NCH>(row)) << 4);
   }
   return d;
 }
+// `lo` must come from dma_lane_offsets with j0 = wave * (ROWS * NCH / 64 / NW).
 template <int NCH, int ROWS, int NW>
 __device__ __forceinline__ void dma_tile(const HK_G uint8_t* src, uint32_t ss, int valid, HK_L uint8_t* tile, int wave,
                                          int lane, const DmaLanes& lo) {
   constexpr int RPI = 64 / NCH;               // rows per instruction
   constexpr int IPW = ROWS * NCH / 64 / NW;   // instructions per wavefront
   constexpr int PERIOD = 16 / RPI;            // swizzle period in instructions
-  static_assert(IPW * NW * 64 == ROWS * NCH && IPW % PERIOD == 0 && PERIOD <= 4, "tile / wavefront split");
+  static_assert(IPW * NW * 64 == ROWS * NCH && 4 % PERIOD == 0, "tile / wavefront split");
   if (valid >= ROWS) {
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       const int j = wave * IPW + i;
-      dma16(src + (uint32_t)(j * RPI) * ss + lo.off[i % PERIOD], tile + j * 1024);
+      dma16(src + (uint32_t)(j * RPI) * ss + lo.off[i % 4], tile + j * 1024);
     }
   } else {
     const int rsub = lane / NCH, slot = lane % NCH;

@@ -239,7 +239,7 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
   constexpr int TILE = KST * ROWB;    // bytes per K or V stage
   constexpr int PIECE = 3 * 16 * 64;  // floats: the three partial blocks merged into one (group, d block)
   constexpr int PPT = TILE / (PIECE * 4);
-  static_assert(PPT >= 1 && PPT * 4 >= 2 * DCH && PPT * PIECE * 4 + 2 * NW * 64 * 4 <= TILE, "merge layout");
+  static_assert(PPT >= 1 && PPT * 4 >= 2 * DCH && PPT * PIECE * 4 + 2 * NW * 64 * 4 <= TILE && 32 * 36 <= PIECE, "merge layout");
   // Four separate LDS objects (not one array), so that the compiler can tell the reads of one buffer from
   // the in-flight copies into the other and does not wait for those copies before every LDS read.
   __shared__ __attribute__((aligned(1024))) uint8_t k0_raw[TILE], k1_raw[TILE], v0_raw[TILE], v1_raw[TILE];
@@ -252,17 +252,17 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = wave & 1, kq = wave >> 1;
   const int ql = lane & 31, hl = lane >> 5;
-  const int64_t total = (int64_t)nqb * p.B * p.H;
-  int64_t bh, qb;
-  xcd_map(blockIdx.x, total, nqb, bh, qb);
-  const int64_t b = bh / p.H, hh = bh % p.H;
+  uint32_t bh32, qb32;
+  xcd_map32(blockIdx.x, (uint32_t)nqb * p.B * p.H, nqb, bh32, qb32);
+  const int64_t bh = bh32, qb = qb32, b = bh32 / (uint32_t)p.H, hh = bh32 % (uint32_t)p.H;
   const int Sq = p.Sq, Sk = p.Sk;
   const uint32_t kss = (uint32_t)(p.k_ss * 2), vss = (uint32_t)(p.v_ss * 2);
   const HK_G uint8_t* Kb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.k) + b * p.k_sb + hh * p.k_sh);
   const HK_G uint8_t* Vb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.v) + b * p.v_sb + hh * p.v_sh);
   const int nst = (Sk + KST - 1) / KST;
 
-  const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane), vlo = dma_lane_offsets<NCH>(vss, lane);
+  const int j0 = wave * (KST * NCH / 64 / NW);
+  const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane, j0), vlo = dma_lane_offsets<NCH>(vss, lane, j0);
   dma_tile<NCH, KST, NW>(Kb, kss, Sk, K0, wave, lane, klo);
   dma_tile<NCH, KST, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
 
@@ -386,11 +386,10 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
       aw[k] = mw[k] == -INFINITY ? 0.f : exp2f(mw[k] - mt);
       L += aw[k] * xml[((2 * k + g) * 2 + 1) * 64 + lane];
     }
-    if (q >= Sq) return;
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    if (N == 0 && hl == 0) gptr<float>(p.lse)[bh * Sq + q] = L > 0.f ? (mt + log2f(L)) * kLn2 : -INFINITY;
+    if (N == 0 && hl == 0 && q < Sq) gptr<float>(p.lse)[bh * Sq + q] = L > 0.f ? (mt + log2f(L)) * kLn2 : -INFINITY;
     const int pc = g * DCH + N;
-    const float* src = tile_f(pc / PPT) + (pc % PPT) * PIECE + lane;
+    float* const area = tile_f(pc / PPT) + (pc % PPT) * PIECE;  // read by this wavefront only
     f32x16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = o[N][e] * aw[N];
@@ -398,16 +397,26 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
     for (int k = 0; k < 4; ++k) {
       if (k == N) continue;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = fmaf(aw[k], src[(((k - N - 1) & 3) * 16 + e) * 64], acc[e]);
+      for (int e = 0; e < 16; ++e) acc[e] = fmaf(aw[k], area[(((k - N - 1) & 3) * 16 + e) * 64 + lane], acc[e]);
     }
-    HK_G typename T::storage* out = gptr<typename T::storage>(p.o) + ((b * Sq + q) * p.H + hh) * p.D;
-    HK_G float* o32 = p.o32 ? gptr<float>(p.o32) + ((b * Sq + q) * p.H + hh) * p.D : nullptr;
+    // transpose the 32 x 32 block through the same area (rows of 36 floats: conflict-free 16-byte writes),
+    // so that 8 lanes store one query's 32 d contiguously (128 bytes of o32, 64 of o) instead of every lane
+    // writing 16-byte pieces of 32 different rows
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = N * 32 + 8 * j + 4 * hl;
-      const float v0 = acc[4 * j] * inv, v1 = acc[4 * j + 1] * inv, v2 = acc[4 * j + 2] * inv, v3 = acc[4 * j + 3] * inv;
-      *reinterpret_cast<HK_G u32x2*>(out + d) = u32x2{pack2<T>(v0, v1), pack2<T>(v2, v3)};
-      if (o32) *reinterpret_cast<HK_G f32x4*>(o32 + d) = f32x4{v0, v1, v2, v3};
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<f32x4*>(area + ql * 36 + 8 * j + 4 * hl) =
+          f32x4{acc[4 * j] * inv, acc[4 * j + 1] * inv, acc[4 * j + 2] * inv, acc[4 * j + 3] * inv};
+    const int c4 = (lane & 7) * 4;
+#pragma unroll
+    for (int ps = 0; ps < 4; ++ps) {
+      const int qq = ps * 8 + (lane >> 3);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(area + qq * 36 + c4);
+      const int64_t qrow = qb * 64 + g * 32 + qq;
+      if (qrow < Sq) {
+        const int64_t off = ((b * Sq + qrow) * p.H + hh) * p.D + N * 32 + c4;
+        *reinterpret_cast<HK_G u32x2*>(gptr<typename T::storage>(p.o) + off) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+        if (p.o32) *reinterpret_cast<HK_G f32x4*>(gptr<float>(p.o32) + off) = v;
+      }
     }
   };
   switch (kq) {

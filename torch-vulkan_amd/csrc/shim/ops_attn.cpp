@@ -153,20 +153,33 @@ BwdRet k_sdpa_bwd(const at::Tensor& grad_out, const at::Tensor& query, const at:
   P.scale = (float)scale.value_or(1.0 / std::sqrt((double)D));
 
   // delta = rowsum(O * dO), from the unrounded fp32 O when the forward kept it
-  hrt_attn_args PD = P;
   at::Tensor o_bshd;
   if (dt != at::kFloat && o32_saved.defined() && o32_saved.scalar_type() == at::kFloat && is_vk(o32_saved) &&
       o32_saved.numel() == B * Sq * H * D && o32_saved.is_contiguous()) {
-    PD.o = addr_of(o32_saved);
-    PD.flags = HRT_ATTN_O_F32;
+    P.o = addr_of(o32_saved);
+    P.flags = HRT_ATTN_O_F32;
   } else {
     o_bshd = (out.scalar_type() == dt ? out : out.to(dt)).permute({0, 2, 1, 3}).contiguous();
-    PD.o = addr_of(o_bshd);
+    P.o = addr_of(o_bshd);
   }
-  launch(std::string("attn_delta_") + kind_name(dt), PD);
-  count_kernel(an);
+  // The matrix-core dQ kernel computes delta itself (HRT_ATTN_DQ_DELTA), so it runs first and dK/dV
+  // reads its delta; otherwise the delta pass runs on its own.
+  const std::string dq_name = kname("dq", dt);
+  const bool fused_delta = mask[0] && dq_name.find("_mfma_") != std::string::npos;
+  if (!fused_delta) {
+    launch(std::string("attn_delta_") + kind_name(dt), P);
+    count_kernel(an);
+  }
 
   at::Tensor dq, dk, dv;
+  if (mask[0]) {
+    dq = alloc_bshd(B, H, Sq, D, q.options());
+    hrt_attn_args P2 = P;
+    P2.dq = addr_of(dq);
+    if (fused_delta) P2.flags |= HRT_ATTN_DQ_DELTA;
+    launch(dq_name, P2);
+    count_kernel(an);
+  }
   if (mask[1] || mask[2]) {
     dk = alloc_bshd(B, H, Sk, D, q.options());
     dv = alloc_bshd(B, H, Sk, D, q.options());
@@ -174,13 +187,6 @@ BwdRet k_sdpa_bwd(const at::Tensor& grad_out, const at::Tensor& query, const at:
     P1.dk = addr_of(dk);
     P1.dv = addr_of(dv);
     launch(kname("dkdv", dt), P1);
-    count_kernel(an);
-  }
-  if (mask[0]) {
-    dq = alloc_bshd(B, H, Sq, D, q.options());
-    hrt_attn_args P2 = P;
-    P2.dq = addr_of(dq);
-    launch(kname("dq", dt), P2);
     count_kernel(an);
   }
   return BwdRet{dq, dk, dv, at::Tensor()};

@@ -14,6 +14,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhrt.so"
 MAX_DIMS = 8
 F32, BF16, F16, RAW8, RAW16, RAW32, RAW64 = range(7)
 ATTN_O_F32 = 1
+ATTN_DQ_DELTA = 2
 
 u64, i64, i32, u32, f32 = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float
 
