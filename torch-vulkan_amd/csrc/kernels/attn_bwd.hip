@@ -612,7 +612,7 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
 // dtype before their products, as attn_coop.comp.in:235-236, 283-284.
 constexpr int QST = 64;  // queries per LDS stage
 
-template <typename T, int DCH>
+template <typename T, int DCH, bool A4>
 __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   constexpr int NW = 8;
   constexpr int NCH = DCH * 4;
@@ -655,19 +655,29 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
     vf[ks] = kv ? *reinterpret_cast<const HK_G u32x4*>(Vr + ks * 32 + 8 * g4) : u32x4{0, 0, 0, 0};
   }
 
-  // lse (as -lse log2e) and delta of this lane's 8 queries of a stage: tile t, row 32 qh + 16 t + 4 g + i
+  // lse and delta of this lane's 8 queries of a stage: tile t, rows 32 qh + 16 t + 4 g + i (i = 0..3, four
+  // consecutive floats: one 16-byte load each when A4, i.e. Sq % 4 == 0 and 16-byte aligned arrays)
   const HK_G float* lseb = gcptr<float>(p.lse) + bh * Sq;
   const HK_G float* dltb = gcptr<float>(p.delta) + bh * Sq;
-  float nl[8], dl[8];  // lse, delta
-  auto fetch = [&](int st, float* nlo, float* dlo) {
+  f32x4 nl[2], dl[2];  // lse, delta
+  auto fetch = [&](int st, f32x4* lo, f32x4* dlo) {
+    const int r0 = st * QST + qh * 32 + 4 * g4;
+    if (A4 && st * QST + QST <= Sq) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t qq = (int64_t)st * QST + qh * 32 + t * 16 + 4 * g4 + i;
-        nlo[t * 4 + i] = qq < Sq ? lseb[qq] : INFINITY;  // +inf: P = 0 for padded query rows
-        dlo[t * 4 + i] = qq < Sq ? dltb[qq] : 0.f;
+      for (int t = 0; t < 2; ++t) {
+        lo[t] = *reinterpret_cast<const HK_G f32x4*>(lseb + r0 + 16 * t);
+        dlo[t] = *reinterpret_cast<const HK_G f32x4*>(dltb + r0 + 16 * t);
       }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int qq = r0 + 16 * t + i;
+          lo[t][i] = qq < Sq ? lseb[qq] : INFINITY;  // +inf: P = 0 for padded query rows
+          dlo[t][i] = qq < Sq ? dltb[qq] : 0.f;
+        }
+    }
   };
   fetch(0, nl, dl);
 
@@ -695,7 +705,7 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
       dma_tile<NCH, QST, NW>(Qb + (q0 + QST) * qss, qss, valid, BUF ? Q0 : Q1, wave, lane, qlo);
       dma_tile<NCH, QST, NW>(Ob + (q0 + QST) * oss, oss, valid, BUF ? O0 : O1, wave, lane, olo);
     }
-    float nn[8], dn[8];
+    f32x4 nn[2], dn[2];
     if (st + 1 < nst) fetch(st + 1, nn, dn);
     const HK_L uint8_t* Qt = BUF ? Q1 : Q0;
     const HK_L uint8_t* Ot = BUF ? O1 : O0;
@@ -714,9 +724,9 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pe = __builtin_amdgcn_exp2f(fmaf(s[t][i], sl2, -nl[t * 4 + i] * kLog2e));
+        const float pe = __builtin_amdgcn_exp2f(fmaf(s[t][i], sl2, -nl[t][i] * kLog2e));
         pv[t * 4 + i] = pe;
-        ds[t * 4 + i] = pe * (dp[t][i] - dl[t * 4 + i]);
+        ds[t * 4 + i] = pe * (dp[t][i] - dl[t][i]);
       }
     const u32x4 pa = u32x4{cvt2<T>(pv[0], pv[1]), cvt2<T>(pv[2], pv[3]), cvt2<T>(pv[4], pv[5]), cvt2<T>(pv[6], pv[7])};
     const u32x4 da = u32x4{cvt2<T>(ds[0], ds[1]), cvt2<T>(ds[2], ds[3]), cvt2<T>(ds[4], ds[5]), cvt2<T>(ds[6], ds[7])};
@@ -728,8 +738,7 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
       dk[dt] = Mfma<T>::mac(da, u32x4{b0.x, b0.y, b1.x, b1.y}, dk[dt]);
     }
     if (st + 1 < nst) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) nl[i] = nn[i], dl[i] = dn[i];
+      nl[0] = nn[0], nl[1] = nn[1], dl[0] = dn[0], dl[1] = dn[1];
     }
     __syncthreads();
   };
@@ -803,10 +812,18 @@ bool launch_dkdv(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
   const dim3 g((uint32_t)total);
   if (bwd_dma_ok(a)) {
-    if (a.D == 128)
-      hipLaunchKernelGGL((attn_dkdv_dma<T, 4>), g, dim3(512), 0, ctx.stream, a, nkb);
-    else
-      hipLaunchKernelGGL((attn_dkdv_dma<T, 2>), g, dim3(512), 0, ctx.stream, a, nkb);
+    const bool a4 = a.Sq % 4 == 0 && a.lse % 16 == 0 && a.delta % 16 == 0;
+#define HK_DKDV(DCH)                                                                        \
+  if (a4)                                                                                   \
+    hipLaunchKernelGGL((attn_dkdv_dma<T, DCH, true>), g, dim3(512), 0, ctx.stream, a, nkb);  \
+  else                                                                                      \
+    hipLaunchKernelGGL((attn_dkdv_dma<T, DCH, false>), g, dim3(512), 0, ctx.stream, a, nkb);
+    if (a.D == 128) {
+      HK_DKDV(4)
+    } else {
+      HK_DKDV(2)
+    }
+#undef HK_DKDV
     return hrt::launch_ok(hipGetLastError(), ctx, "attn_dkdv_dma");
   }
   const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);

@@ -162,23 +162,28 @@ constexpr float kLn2 = 0.6931471805599453f;
 // One instruction copies 16 bytes per lane and lane i's bytes land at lds_base + 16 i (checked on the
 // device), so the LDS layout of a wave's 1 KiB is fixed and any swizzle is applied by choosing which
 // global chunk each lane fetches.  Tiles of 16-bit [row][d] data with NCH 16-byte chunks per row are stored
-// with chunk c of `row` in slot c ^ swz(row).  swz is chosen so that both readers are conflict-free on the
-// 64 x 4-byte LDS banks:
+// with chunk c of `row` in slot c ^ swz(row).  swz is chosen so that every reader is conflict-free on the
+// 64 x 4-byte LDS banks (a 256-byte bank line; 16 lanes of a 128-bit read, 32 lanes of a 64-bit read per
+// cycle):
 //   * 128-bit row reads (MFMA A operand, 16 lanes = 16 consecutive rows at one chunk): swz is a bijection
 //     on every aligned group of 16 rows (NCH = 16) or of 8 same-parity rows (NCH = 8, two rows per bank line);
-//   * ds_read_b64_tr_b16 column reads (4 consecutive rows x 4 consecutive chunks per 32 lanes): the 4 rows
-//     get different values in swz bits 2..3 (NCH = 16) or, per row parity, in bit 2 (NCH = 8).
+//   * ds_read_b64_tr_b16 column reads of the 32x32x16 kernels (4 aligned rows x 4 aligned chunks per 32
+//     lanes): the 4 rows differ in swz bits 2..3 (NCH = 16) or, per row parity, in bit 2 (NCH = 8);
+//   * ds_read_b64_tr_b16 column reads of the 16x16x32 kernels (8 aligned rows x 2 aligned chunks per 32
+//     lanes): the 8 rows differ in swz bits 1..3 (NCH = 16) or, per row parity, in bits 1..2 (NCH = 8).
 #define HK_L __attribute__((address_space(3)))
 
 template <int NCH>
 __device__ __forceinline__ int tile_swz(int row);
+// NCH = 16 (256-byte rows, one row per bank line): slot bits (3, 2, 1, 0) = row bits (1, 0, 2, 3).
 template <>
 __device__ __forceinline__ int tile_swz<16>(int row) {
-  return ((row & 3) << 2) | ((row >> 2) & 3);
+  return ((row & 3) << 2) | (((row >> 2) & 1) << 1) | ((row >> 3) & 1);
 }
+// NCH = 8 (128-byte rows, row bit 0 selects the half bank line): slot bits (2, 1, 0) = row bits (1, 2, 3).
 template <>
 __device__ __forceinline__ int tile_swz<8>(int row) {
-  return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+  return (((row >> 1) & 1) << 2) | (((row >> 2) & 1) << 1) | ((row >> 3) & 1);
 }
 
 __device__ __forceinline__ void dma16(const HK_G uint8_t* src, HK_L uint8_t* lds_base) {

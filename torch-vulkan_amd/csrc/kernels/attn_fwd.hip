@@ -263,8 +263,10 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 
   const int j0 = wave * (KST * NCH / 64 / NW);
   const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane, j0), vlo = dma_lane_offsets<NCH>(vss, lane, j0);
+  // K streams one stage ahead of V: K(0), K(1) and V(0) first
   dma_tile<NCH, KST, NW>(Kb, kss, Sk, K0, wave, lane, klo);
   dma_tile<NCH, KST, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
+  if (nst > 1) dma_tile<NCH, KST, NW>(Kb + (int64_t)KST * kss, kss, Sk - KST, K1, wave, lane, klo);
 
   // Q^T operand fragments of this lane's query
   const HK_G uint16_t* Q = gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh;
@@ -293,21 +295,22 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
   float m = -INFINITY, l = 0.f;  // m in log2 units of the scaled logits
   const float sl2 = p.scale * kLog2e;
 
-  auto stage = [&](auto bc, int st) {
-    constexpr int BUF = decltype(bc)::value;
-    const int64_t key0 = (int64_t)st * KST;
-    if (st + 1 < nst) {  // next stage into the other buffer (its last readers passed the previous barrier)
-      const int valid = (int)(Sk - key0 - KST);
-      dma_tile<NCH, KST, NW>(Kb + (key0 + KST) * kss, kss, valid, BUF ? K0 : K1, wave, lane, klo);
-      dma_tile<NCH, KST, NW>(Vb + (key0 + KST) * vss, vss, valid, BUF ? V0 : V1, wave, lane, vlo);
-    }
-    const HK_L uint8_t* Kt = BUF ? K1 : K0;
-    const HK_L uint8_t* Vt = BUF ? V1 : V0;
+  // S^T = K Q^T for the wavefront's 32 keys of a stage (its K tile in Kt)
+  auto qk = [&](const HK_L uint8_t* Kt) {
+    u32x4 kfr[2 * DCH];
+#pragma unroll
+    for (int ks = 0; ks < 2 * DCH; ++ks) kfr[ks] = *reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]);
     f32x16 s = zero16();
 #pragma unroll
-    for (int ks = 0; ks < 2 * DCH; ++ks) s = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]), qf[ks], s);
-    // element 4j+r: key kq*32 + 8j + 4h + r of the stage
-    if (key0 + KST > Sk) {  // ragged last stage: keys >= Sk do not exist (their rows were clamped)
+    for (int ks = 0; ks < 2 * DCH; ++ks) s = Mfma32<T>::mac(kfr[ks], qf[ks], s);
+    return s;
+  };
+  // Keys >= Sk of stage st masked to -inf (their rows were clamped), then the running max raised when the
+  // stage's row max exceeds it by more than 2^kLazy (O and l rescaled; rare after the first stage).
+  // Element 4j+r of s: key kq*32 + 8j + 4h + r of the stage.
+  auto mask_and_max = [&](f32x16& s, int st) {
+    const int64_t key0 = (int64_t)st * KST;
+    if (key0 + KST > Sk) {
       const int64_t kbase = key0 + kq * 32 + 4 * hl;
 #pragma unroll
       for (int e = 0; e < 16; ++e)
@@ -328,12 +331,48 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
         for (int e = 0; e < 16; ++e) o[n][e] *= alpha;
       m = mn;
     }
+  };
+  // Software pipeline: iteration st computes S(st+1) on the matrix cores while the vector units turn S(st)
+  // into P(st) (the two instruction streams interleaved by sched_group_barrier), then O += V(st)^T P(st),
+  // then masks S(st+1) and updates the running max for it.  K(st) sits in buffer st & 1 and is read one
+  // iteration before V(st); iteration st copies K(st+2) and V(st+1) into the buffers the previous iteration
+  // finished reading, and its closing barrier makes them visible.
+  auto stage = [&](auto bc, int st, f32x16& s, f32x16& sn) {
+    constexpr int BUF = decltype(bc)::value;
+    if (st + 2 < nst) {
+      const int64_t k2 = (int64_t)(st + 2) * KST;
+      dma_tile<NCH, KST, NW>(Kb + k2 * kss, kss, (int)(Sk - k2), BUF ? K1 : K0, wave, lane, klo);
+    }
+    if (st + 1 < nst) {
+      const int64_t k1 = (int64_t)(st + 1) * KST;
+      dma_tile<NCH, KST, NW>(Vb + k1 * vss, vss, (int)(Sk - k1), BUF ? V0 : V1, wave, lane, vlo);
+    }
+    const bool more = st + 1 < nst;
+    const HK_L uint8_t* Kn = BUF ? K0 : K1;
+    const HK_L uint8_t* Vt = BUF ? V1 : V0;
     const float nm = m == -INFINITY ? 0.f : -m;
+    if (more) {
+      sn = qk(Kn);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float pv = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, nm));  // exp2(-inf) = 0 for masked keys
-      s[e] = pv;
-      l += pv;
+      for (int e = 0; e < 16; ++e) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, nm));  // exp2(-inf) = 0 for masked keys
+        s[e] = pv;
+        l += pv;
+      }
+      // 8 (16 for D = 128) K fragment reads first, then each MFMA of S(st+1) followed by VALU of P(st)
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * DCH, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * DCH; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 48 / (2 * DCH), 0);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, nm));
+        s[e] = pv;
+        l += pv;
+      }
     }
     const u32x4 pb0 = pack_slots<T>(s, 0, 1), pb1 = pack_slots<T>(s, 2, 3);
 #pragma unroll
@@ -344,12 +383,16 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
         const u32x2 hi = lds_tr4(Vt + voff[n][1] + kc * 16 * ROWB);
         o[n] = Mfma32<T>::mac(u32x4{lo.x, lo.y, hi.x, hi.y}, kc ? pb1 : pb0, o[n]);
       }
-    __syncthreads();  // waits for this wave's copies of the next stage, then for every wave
+    if (more) mask_and_max(sn, st + 1);
+    __syncthreads();  // waits for this wave's copies, then for every wave
   };
   __syncthreads();
+  f32x16 sa = qk(K0), sb;
+  mask_and_max(sa, 0);
+  __syncthreads();  // every wave is done with K(0) before K(2) is copied over it
   for (int st = 0; st < nst; st += 2) {
-    stage(std::integral_constant<int, 0>(), st);
-    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1);
+    stage(std::integral_constant<int, 0>(), st, sa, sb);
+    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1, sb, sa);
   }
 
   // ---- merge the four key quarters of each query group.  Piece (g, n) = d block n of group g, finished by
