@@ -1,17 +1,21 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X vk hot path (one GPU).
 
-Headline (`value`): bf16 flash-attention forward + backward at B1 H16 S1024 D128 (BASELINE configs 2+3),
-in algorithmic TFLOP/s: 4*B*H*S^2*D forward + 2.5x that backward = 3.006e10 flop per step (the
-convention of the reference's tools/bench_attention.py:39).  A step is the hot path's four kernels
-(forward, delta, dK/dV, dQ) over one batch already resident in HBM, queued through the hrt C ABI exactly
-as the PyTorch shim queues them, replayed as a HIP graph on the runtime's stream and timed with HIP
-events on that stream.  The same JSON line carries the other BASELINE workloads (GEMMs, softmax,
-layer_norm, int8 dequant, the fused int8 linear, attention at S=4096), each as absolute TFLOP/s or GB/s
-and as a fraction of MI355X's published peak, the roofline object of the step's dominant kernel, the
-PyTorch-level step time, and the reference's CPU path (torch CPU aten) timed on this host.
+Headline (`value`): bf16 flash-attention forward + backward at B1 H16 S1024 D128 (the reference's attention
+benchmark shape), in algorithmic TFLOP/s: 4*B*H*S^2*D forward + 2.5x that backward = 3.006e10 flop per
+step (the convention of the reference's tools/bench_attention.py:39).  A step is the hot path's three
+kernels (forward, dQ with the delta pass folded in, dK/dV) over one batch already resident in HBM, queued
+through the hrt C ABI exactly as the PyTorch shim queues them, replayed as a HIP graph on the runtime's
+stream and timed with HIP events on that stream.  The same JSON line carries the other benchmark workloads
+(GEMMs, softmax, layer_norm, int8 dequant, the fused int8 linear, attention at S=4096), each as absolute
+TFLOP/s or GB/s and as a fraction of MI355X's published peak, the roofline object of the step's dominant
+kernel (its HBM traffic from the rocprofv3 counter summary in profiles/, when present), the PyTorch-level
+step time, and the CPU baseline: the oracle's float64 restatement of the same fwd+bwd timed on this host
+(plus, for reference, torch's CPU aten SDPA, which is what the reference runs on CPU).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--skip-cpu] [--only-attn]
+       python bench.py --profile {fwd,dq,dkdv,copy} [--steps K]   (launches only that kernel, for rocprofv3)
+       python bench.py --pmc-summary DIR [DIR ...]                 (per-kernel counters of rocprofv3 --pmc runs)
 """
 
 import argparse
@@ -37,7 +41,51 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
+    ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy"], help="launch one kernel --steps times")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR", help="summarise rocprofv3 --pmc output directories")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "attn_traffic_s1024.txt")
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size) from
+    the committed rocprofv3 counter summary, or None when it has not been measured."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            for line in fh:
+                f = line.split()
+                if len(f) >= 3 and f[0] == kernel and f[1].startswith("hbm_bytes="):
+                    return int(float(f[1].split("=", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def pmc_summary(dirs):
+    """Average counter value per dispatch and kernel over rocprofv3 --pmc --output-format csv directories.
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are also given as bytes scaled by what the same counter reads
+    for the 64 MiB device copy that `--profile copy` performs (bytes read = bytes written = 64 MiB)."""
+    import csv
+    import glob
+
+    agg = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+                agg.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    avg = {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in agg.items()}
+    copy = next((cs for k, cs in avg.items() if "copyBuffer" in k or "ew_copy" in k), {})
+    known_kib = 64 * 1024.0
+    scale = {c: known_kib / copy[c] for c in ("FETCH_SIZE", "WRITE_SIZE") if copy.get(c)}
+    for k, cs in sorted(avg.items()):
+        print(f"== {k}")
+        for c, v in sorted(cs.items()):
+            extra = f"  scaled bytes {v * 1024 * scale[c]:.4g}" if c in scale else ""
+            print(f"  {c:28s} {v:16.1f}{extra}")
+    print("copy-kernel scale factors (64 MiB / counter):", {c: round(f, 4) for c, f in scale.items()})
 
 
 def attn_flops(B, H, Sq, Sk, D):
@@ -148,7 +196,7 @@ class Bench:
         dom = max(("fwd", "dkdv", "dq"), key=lambda n: per[n])
         ach = algo[dom] / (per[dom] * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_TFLOPS["bf16"], 4), "traffic": None, "kernel": names[dom],
+                "frac": round(ach / PEAK_TFLOPS["bf16"], 4), "traffic": load_traffic(names[dom]), "kernel": names[dom],
                 "algo_flop_per_launch": algo[dom], "avg_launch_us": round(per[dom] * 1e3, 3)}
         del keep
         return ms, (fwd_f + bwd_f) / (ms * 1e-3) / 1e12, kstats, roof
@@ -307,47 +355,98 @@ class Bench:
         return self.bw("dq8", R * C + R * (C // 64) * 2 + R * C * 2, sets, mk, ["dq8_bf16"])
 
     # ---- CPU baseline: the reference's CPU path (torch CPU aten) -------------------------------------
+    def profile(self, which, n):
+        """Launch one kernel of the headline step (or a 64 MiB device copy) n times and return: the workload
+        that rocprofv3 --kernel-trace / --pmc runs wrap."""
+        torch = self.torch
+        if which == "copy":
+            src = torch.empty(16 * 1024 * 1024, dtype=torch.float32, device=self.dev).fill_(1.0)
+            dst = torch.empty_like(src)
+            for _ in range(n):
+                dst.copy_(src)
+        else:
+            step, kernels, keep, _ = self.attn_setup(1, 16, 1024, 128)
+            step()  # fwd, dQ (+delta), dK/dV once so that every input of the profiled kernel is valid
+            for i in range(n):
+                kernels[which](i)
+        self.rt.synchronize()
+
     def cpu_baseline(self):
+        """The oracle (the float64 numpy restatement the parity tests check against) running the headline
+        fwd + delta + bwd on a bounded sample (2 of the 16 heads), timed on this host with the BLAS threads
+        numpy uses; plus torch's CPU aten SDPA fwd+bwd in bf16 on the same sample for reference (what the
+        reference itself runs on CPU)."""
+        import numpy as np
         import torch
         import torch.nn.functional as F
 
-        B, H, S, D = 1, 16, 1024, 128
+        sys.path.insert(0, REPO)
+        import oracle
+
+        B, H, S, D = 1, 2, 1024, 128
         g = torch.Generator().manual_seed(0)
         q, k, v, do = (torch.randn((B, H, S, D), generator=g).to(torch.bfloat16) for _ in range(4))
+        qa, ka, va, ga = (t.double().numpy() for t in (q, k, v, do))
+        sc = 1.0 / np.sqrt(D)
 
-        def one():
+        def port():
+            out, lse = oracle.attention_fwd(qa, ka, va, sc)
+            oracle.attention_bwd(qa, ka, va, ga, lse, oracle.attention_delta(out, ga), sc)
+
+        def aten():
             qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
             F.scaled_dot_product_attention(qq, kk, vv).backward(do)
 
-        one()
-        times = []
-        t_end = time.perf_counter() + self.args.cpu_seconds
-        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
-            t0 = time.perf_counter()
-            one()
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
+        def median_time(fn, budget):
+            fn()
+            times = []
+            t_end = time.perf_counter() + budget
+            while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 100):
+                t0 = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t0)
+            return statistics.median(times), len(times)
+
         f, b = attn_flops(B, H, S, S, D)
+        t_port, n_port = median_time(port, self.args.cpu_seconds)
+        t_aten, n_aten = median_time(aten, min(self.args.cpu_seconds, 5.0))
+        threads = None
+        try:
+            from threadpoolctl import threadpool_info
+
+            threads = max((i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"), default=None)
+        except Exception:
+            pass
         model = ""
         try:
             with open("/proc/cpuinfo") as fh:
                 model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), "")
         except OSError:
             pass
-        return {"value": round((f + b) / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-                "kind": "reference", "ms_per_step": round(med * 1e3, 2),
-                "sample": f"torch {torch.__version__} CPU aten F.scaled_dot_product_attention fwd+bwd bf16 "
-                          f"[1,16,1024,128] (the reference's CPU path), median of {len(times)} steps, "
-                          f"{torch.get_num_threads()} threads, {model}"}
+        return {"value": round((f + b) / t_port / 1e12, 5), "unit": "TFLOP/s", "cores": threads or os.cpu_count(),
+                "kind": "port", "ms_per_sample": round(t_port * 1e3, 1),
+                "sample": f"oracle.attention_fwd + attention_delta + attention_bwd (numpy float64) on [1,2,1024,128] "
+                          f"bf16-valued inputs = 2 of the 16 heads of the headline step (TFLOP/s is per-sample work / "
+                          f"time, the same rate as the full step), median of {n_port} runs, {model}",
+                "torch_cpu_aten": {"value": round((f + b) / t_aten / 1e12, 5), "unit": "TFLOP/s",
+                                   "cores": torch.get_num_threads(), "ms_per_sample": round(t_aten * 1e3, 1),
+                                   "sample": f"torch {torch.__version__} F.scaled_dot_product_attention fwd+bwd bf16 "
+                                             f"on the same sample, median of {n_aten} runs"}}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every box here has one "
-              "GPU; the sharding design is described in DESIGN.md)", file=sys.stderr)
+              "GPU; attention shards over independent (batch, head) pairs with no exchange)", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     bench = Bench(args)
+    if args.profile:
+        bench.profile(args.profile, args.steps)
+        return
     print(f"[bench] device: {bench.tv.device_name()}", file=sys.stderr, flush=True)
     ms, tflops, kstats, roof = bench.attn_headline()
     print(f"[bench] attention fwd+bwd step {ms:.4f} ms = {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
@@ -356,7 +455,7 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs, resident in HBM)",
         "config": {"workload": "flash-attention fwd+bwd, B=1 H=16 S=1024 D=128 bf16, non-causal, scale 1/sqrt(128) "
-                               "(BASELINE configs[1]+[2]); one step = fwd, delta, dK/dV, dQ kernels",
+                               "(benchmark configs[1]+[2]); one step = fwd, dQ (+delta), dK/dV kernels",
                    "B": 1, "H": 16, "S": 1024, "D": 128, "parallelism": "single GPU"},
         "frac_of_bf16_peak": round(tflops / PEAK_TFLOPS["bf16"], 4),
         "roofline": roof,
