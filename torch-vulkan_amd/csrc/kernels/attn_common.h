@@ -243,6 +243,30 @@ __device__ __forceinline__ void dma_tile(const HK_G uint8_t* src, uint32_t ss, i
   }
 }
 
+// Instruction i (0 .. IPW-1) of this wavefront's share of a full tile copy: rows [0, ROWS) at `src` all
+// exist (no clamping, no branch), so a caller can place the copies one by one between its MFMAs instead of
+// issuing the whole tile in one burst (a burst of 1 KiB copies from every wavefront stalls each of them at
+// issue until the address unit has drained the others).
+template <int NCH, int ROWS, int NW>
+__device__ __forceinline__ void dma_tile_part(const HK_G uint8_t* src, uint32_t ss, HK_L uint8_t* tile, int wave,
+                                              const DmaLanes& lo, int i) {
+  constexpr int RPI = 64 / NCH;
+  constexpr int IPW = ROWS * NCH / 64 / NW;
+  const int j = wave * IPW + i;
+  dma16(src + (uint32_t)(j * RPI) * ss + lo.off[i % 4], tile + j * 1024);
+}
+
+// First row of the tile that stage st copies when the sequence has more than one stage (len > ROWS): stage
+// st covers rows [st ROWS, (st + 1) ROWS); the last, ragged stage copies the full window that ends at row
+// len - 1 instead (origin len - ROWS), so no copy reads past the sequence, and its rows below st ROWS
+// (processed by the previous stage) are masked by the caller.  Stages past the end repeat the last one.
+template <int ROWS>
+__device__ __forceinline__ int64_t stage_origin(int st, int nst, int64_t len) {
+  const int s = st < nst ? st : nst - 1;
+  const int64_t o = (int64_t)s * ROWS;
+  return o + ROWS <= len ? o : len - ROWS;
+}
+
 // 16 bytes of a swizzled tile at (row, chunk c), as a byte offset.
 template <int NCH>
 __device__ __forceinline__ int tile_off(int row, int c) {

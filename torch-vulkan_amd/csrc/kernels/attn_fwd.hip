@@ -263,18 +263,17 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 
   const int j0 = wave * (KST * NCH / 64 / NW);
   const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane, j0), vlo = dma_lane_offsets<NCH>(vss, lane, j0);
-  // K streams one stage ahead of V: K(0), K(1) and V(0) first
-  dma_tile<NCH, KST, NW>(Kb, kss, Sk, K0, wave, lane, klo);
-  dma_tile<NCH, KST, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
-  if (nst > 1) dma_tile<NCH, KST, NW>(Kb + (int64_t)KST * kss, kss, Sk - KST, K1, wave, lane, klo);
-
-  // Q^T operand fragments of this lane's query
+  // Q^T operand fragments of this lane's query (needed first), then K(0), V(0) and K(1): K streams one
+  // stage ahead of V
   const HK_G uint16_t* Q = gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh;
   const int64_t q = qb * 64 + g * 32 + ql;
   u32x4 qf[2 * DCH];
 #pragma unroll
   for (int ks = 0; ks < 2 * DCH; ++ks)
     qf[ks] = q < Sq ? *reinterpret_cast<const HK_G u32x4*>(Q + q * p.q_ss + ks * 16 + 8 * hl) : u32x4{0, 0, 0, 0};
+  dma_tile<NCH, KST, NW>(Kb, kss, Sk, K0, wave, lane, klo);
+  dma_tile<NCH, KST, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
+  if (nst > 1) dma_tile<NCH, KST, NW>(Kb + stage_origin<KST>(1, nst, Sk) * kss, kss, KST, K1, wave, lane, klo);
 
   // per-lane byte offsets of the A-operand fragments inside a tile
   int koff[2 * DCH], voff[DCH][2];
@@ -305,16 +304,19 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
     for (int ks = 0; ks < 2 * DCH; ++ks) s = Mfma32<T>::mac(kfr[ks], qf[ks], s);
     return s;
   };
-  // Keys >= Sk of stage st masked to -inf (their rows were clamped), then the running max raised when the
-  // stage's row max exceeds it by more than 2^kLazy (O and l rescaled; rare after the first stage).
-  // Element 4j+r of s: key kq*32 + 8j + 4h + r of the stage.
+  // Masking of stage st's tile (keys before the stage, processed already when the last stage's tile was
+  // shifted back, and keys >= Sk), then the running max raised when the stage's row max exceeds it by more
+  // than 2^kLazy (O and l rescaled; rare after the first stage).  Element 4j+r of s: tile row
+  // kq*32 + 8j + 4h + r.
   auto mask_and_max = [&](f32x16& s, int st) {
     const int64_t key0 = (int64_t)st * KST;
     if (key0 + KST > Sk) {
-      const int64_t kbase = key0 + kq * 32 + 4 * hl;
+      const int64_t kbase = (nst > 1 ? stage_origin<KST>(st, nst, Sk) : 0) + kq * 32 + 4 * hl;
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (kbase + 8 * (e >> 2) + (e & 3) >= Sk) s[e] = -INFINITY;
+      for (int e = 0; e < 16; ++e) {
+        const int64_t key = kbase + 8 * (e >> 2) + (e & 3);
+        if (key < key0 || key >= Sk) s[e] = -INFINITY;
+      }
     }
     float mx = fmaxf(s[0], s[1]);
 #pragma unroll
@@ -333,37 +335,44 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
     }
   };
   // Software pipeline: iteration st computes S(st+1) on the matrix cores while the vector units turn S(st)
-  // into P(st) (the two instruction streams interleaved by sched_group_barrier), then O += V(st)^T P(st),
-  // then masks S(st+1) and updates the running max for it.  K(st) sits in buffer st & 1 and is read one
-  // iteration before V(st); iteration st copies K(st+2) and V(st+1) into the buffers the previous iteration
-  // finished reading, and its closing barrier makes them visible.
-  auto stage = [&](auto bc, int st, f32x16& s, f32x16& sn) {
+  // into P(st), with this iteration's copies (K(st+2), V(st+1)) placed one per MFMA (the three streams
+  // interleaved by sched_group_barrier); then O += V(st)^T P(st); then S(st+1) is masked and the running
+  // max updated.  K(st) sits in buffer st & 1 and is read one iteration before V(st); the copies go into
+  // the buffers the previous iteration finished reading and the closing barrier makes them visible.
+  // COPY = false: single-stage sequences (no copies, no next stage).
+  constexpr int IPW = KST * NCH / 64 / NW;  // copy instructions per tile and wavefront
+  auto stage = [&](auto bc, auto cc, int st, f32x16& s, f32x16& sn) {
     constexpr int BUF = decltype(bc)::value;
-    if (st + 2 < nst) {
-      const int64_t k2 = (int64_t)(st + 2) * KST;
-      dma_tile<NCH, KST, NW>(Kb + k2 * kss, kss, (int)(Sk - k2), BUF ? K1 : K0, wave, lane, klo);
-    }
-    if (st + 1 < nst) {
-      const int64_t k1 = (int64_t)(st + 1) * KST;
-      dma_tile<NCH, KST, NW>(Vb + k1 * vss, vss, (int)(Sk - k1), BUF ? V0 : V1, wave, lane, vlo);
-    }
-    const bool more = st + 1 < nst;
-    const HK_L uint8_t* Kn = BUF ? K0 : K1;
-    const HK_L uint8_t* Vt = BUF ? V1 : V0;
+    constexpr bool COPY = decltype(cc)::value;
     const float nm = m == -INFINITY ? 0.f : -m;
-    if (more) {
-      sn = qk(Kn);
+    if constexpr (COPY) {
+      const HK_G uint8_t* ksrc = Kb + stage_origin<KST>(st + 2, nst, Sk) * kss;
+      const HK_G uint8_t* vsrc = Vb + stage_origin<KST>(st + 1, nst, Sk) * vss;
+      // S(st+1) (in the last iteration unused; its tile holds valid data) with this iteration's copies
+      // placed after its MFMAs, one per MFMA, then P(st); the VALU work of P(st) is interleaved with the
+      // MFMAs by sched_group_barrier
+      const HK_L uint8_t* Kt = BUF ? K0 : K1;
+      u32x4 kfr[2 * DCH];
+#pragma unroll
+      for (int ks = 0; ks < 2 * DCH; ++ks) kfr[ks] = *reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]);
+      sn = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 2 * DCH; ++ks) {
+        sn = Mfma32<T>::mac(kfr[ks], qf[ks], sn);
+        if (ks < IPW) dma_tile_part<NCH, KST, NW>(ksrc, kss, BUF ? K1 : K0, wave, klo, ks);
+        else if (ks < 2 * IPW) dma_tile_part<NCH, KST, NW>(vsrc, vss, BUF ? V0 : V1, wave, vlo, ks - IPW);
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const float pv = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, nm));  // exp2(-inf) = 0 for masked keys
         s[e] = pv;
         l += pv;
       }
-      // 8 (16 for D = 128) K fragment reads first, then each MFMA of S(st+1) followed by VALU of P(st)
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * DCH, 0);
 #pragma unroll
       for (int i = 0; i < 2 * DCH; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i < 2 * IPW) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 48 / (2 * DCH), 0);
       }
     } else {
@@ -374,6 +383,7 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
         l += pv;
       }
     }
+    const HK_L uint8_t* Vt = BUF ? V1 : V0;
     const u32x4 pb0 = pack_slots<T>(s, 0, 1), pb1 = pack_slots<T>(s, 2, 3);
 #pragma unroll
     for (int n = 0; n < DCH; ++n)
@@ -383,16 +393,20 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
         const u32x2 hi = lds_tr4(Vt + voff[n][1] + kc * 16 * ROWB);
         o[n] = Mfma32<T>::mac(u32x4{lo.x, lo.y, hi.x, hi.y}, kc ? pb1 : pb0, o[n]);
       }
-    if (more) mask_and_max(sn, st + 1);
+    if (COPY && st + 1 < nst) mask_and_max(sn, st + 1);
     __syncthreads();  // waits for this wave's copies, then for every wave
   };
   __syncthreads();
   f32x16 sa = qk(K0), sb;
   mask_and_max(sa, 0);
-  __syncthreads();  // every wave is done with K(0) before K(2) is copied over it
-  for (int st = 0; st < nst; st += 2) {
-    stage(std::integral_constant<int, 0>(), st, sa, sb);
-    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1, sb, sa);
+  __syncthreads();  // every wave is done with K(0) before it is copied over
+  if (nst == 1) {
+    stage(std::integral_constant<int, 0>(), std::false_type(), 0, sa, sb);
+  } else {
+    for (int st = 0; st < nst; st += 2) {
+      stage(std::integral_constant<int, 0>(), std::true_type(), st, sa, sb);
+      if (st + 1 < nst) stage(std::integral_constant<int, 1>(), std::true_type(), st + 1, sb, sa);
+    }
   }
 
   // ---- merge the four key quarters of each query group.  Piece (g, n) = d block n of group g, finished by
