@@ -506,14 +506,17 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
     if (kq == 0 && hl == 0 && qv) gptr<float>(p.delta)[bh * Sq + q] = dlt;
   }
 
-  auto stage = [&](auto bc, int st) {
+  // COPY: stage st + 1 is copied into the other buffers while stage st computes, the copies placed between
+  // the MFMAs of S^T / dP^T (the buffers' previous readers passed the last barrier).  With more than one
+  // stage the copies are branch-free (stage_origin: the last, ragged stage is the window ending at Sk,
+  // its keys before the stage masked; copies past the end repeat the last stage into a buffer nobody reads).
+  constexpr int IPW = KST2 * NCH / 64 / NW;
+  auto stage = [&](auto bc, auto cc, int st) {
     constexpr int BUF = decltype(bc)::value;
+    constexpr bool COPY = decltype(cc)::value;
     const int64_t key0 = (int64_t)st * KST2;
-    if (st + 1 < nst) {
-      const int valid = (int)(Sk - key0 - KST2);
-      dma_tile<NCH, KST2, NW>(Kb + (key0 + KST2) * kss, kss, valid, BUF ? K0 : K1, wave, lane, klo);
-      dma_tile<NCH, KST2, NW>(Vb + (key0 + KST2) * vss, vss, valid, BUF ? V0 : V1, wave, lane, vlo);
-    }
+    const HK_G uint8_t* ksrc = Kb + stage_origin<KST2>(st + 1, nst, Sk) * kss;
+    const HK_G uint8_t* vsrc = Vb + stage_origin<KST2>(st + 1, nst, Sk) * vss;
     const HK_L uint8_t* Kt = BUF ? K1 : K0;
     const HK_L uint8_t* Vt = BUF ? V1 : V0;
     f32x16 s = zero16(), dp = zero16();
@@ -521,13 +524,19 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
     for (int ks = 0; ks < 2 * DCH; ++ks) {
       s = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]), qf[ks], s);
       dp = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Vt + koff[ks]), df[ks], dp);
+      if constexpr (COPY) {
+        if (ks < IPW) dma_tile_part<NCH, KST2, NW>(ksrc, kss, BUF ? K0 : K1, wave, klo, ks);
+        else if (ks < 2 * IPW) dma_tile_part<NCH, KST2, NW>(vsrc, vss, BUF ? V0 : V1, wave, vlo, ks - IPW);
+      }
     }
-    // element 4j+r: key kq*32 + 8j + 4h + r of the stage, query = this lane's
+    // element 4j+r: tile row kq*32 + 8j + 4h + r of the stage, query = this lane's
     if (key0 + KST2 > Sk) {
-      const int64_t kbase = key0 + kq * 32 + 4 * hl;
+      const int64_t kbase = (nst > 1 ? stage_origin<KST2>(st, nst, Sk) : 0) + kq * 32 + 4 * hl;
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (kbase + 8 * (e >> 2) + (e & 3) >= Sk) s[e] = -INFINITY;
+      for (int e = 0; e < 16; ++e) {
+        const int64_t key = kbase + 8 * (e >> 2) + (e & 3);
+        if (key < key0 || key >= Sk) s[e] = -INFINITY;
+      }
     }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -545,9 +554,13 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
       }
     __syncthreads();
   };
-  for (int st = 0; st < nst; st += 2) {
-    stage(std::integral_constant<int, 0>(), st);
-    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1);
+  if (nst == 1) {
+    stage(std::integral_constant<int, 0>(), std::false_type(), 0);
+  } else {
+    for (int st = 0; st < nst; st += 2) {
+      stage(std::integral_constant<int, 0>(), std::true_type(), st);
+      if (st + 1 < nst) stage(std::integral_constant<int, 1>(), std::true_type(), st + 1);
+    }
   }
 
   // ---- sum the four key quarters: piece (g, n) = d block n of group g, finished by wavefront (g, k = n)
@@ -660,8 +673,11 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   const HK_G float* lseb = gcptr<float>(p.lse) + bh * Sq;
   const HK_G float* dltb = gcptr<float>(p.delta) + bh * Sq;
   f32x4 nl[2], dl[2];  // lse, delta
+  // Stage st's tile starts at query row origin(st) (stage_origin when there is more than one stage); its
+  // rows outside [st QST, Sq) get lse = +inf, so P = dS = 0 for them.
   auto fetch = [&](int st, f32x4* lo, f32x4* dlo) {
-    const int r0 = st * QST + qh * 32 + 4 * g4;
+    const int64_t org = nst > 1 ? stage_origin<QST>(st, nst, Sq) : 0;
+    const int r0 = (int)org + qh * 32 + 4 * g4;
     if (A4 && st * QST + QST <= Sq) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -674,8 +690,9 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int qq = r0 + 16 * t + i;
-          lo[t][i] = qq < Sq ? lseb[qq] : INFINITY;  // +inf: P = 0 for padded query rows
-          dlo[t][i] = qq < Sq ? dltb[qq] : 0.f;
+          const bool ok = qq >= st * QST && qq < Sq;
+          lo[t][i] = ok ? lseb[qq] : INFINITY;
+          dlo[t][i] = ok ? dltb[qq] : 0.f;
         }
     }
   };
@@ -697,14 +714,14 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   const float sl2 = p.scale * kLog2e;
 
   __syncthreads();
-  auto stage = [&](auto bc, int st) {
+  // COPY: stage st + 1 is copied while stage st computes, the copies placed between the MFMAs of S / dP;
+  // with more than one stage they are branch-free (stage_origin, as in the other attention kernels).
+  constexpr int IPW = QST * NCH / 64 / NW;
+  auto stage = [&](auto bc, auto cc, int st) {
     constexpr int BUF = decltype(bc)::value;
-    const int64_t q0 = (int64_t)st * QST;
-    if (st + 1 < nst) {
-      const int valid = (int)(Sq - q0 - QST);
-      dma_tile<NCH, QST, NW>(Qb + (q0 + QST) * qss, qss, valid, BUF ? Q0 : Q1, wave, lane, qlo);
-      dma_tile<NCH, QST, NW>(Ob + (q0 + QST) * oss, oss, valid, BUF ? O0 : O1, wave, lane, olo);
-    }
+    constexpr bool COPY = decltype(cc)::value;
+    const HK_G uint8_t* qsrc = Qb + stage_origin<QST>(st + 1, nst, Sq) * qss;
+    const HK_G uint8_t* osrc = Ob + stage_origin<QST>(st + 1, nst, Sq) * oss;
     f32x4 nn[2], dn[2];
     if (st + 1 < nst) fetch(st + 1, nn, dn);
     const HK_L uint8_t* Qt = BUF ? Q1 : Q0;
@@ -717,6 +734,11 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
       for (int ks = 0; ks < DCH; ++ks) {
         s[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Qt + roff[ks] + t * 16 * ROWB), kf[ks], s[t]);
         dp[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Ot + roff[ks] + t * 16 * ROWB), vf[ks], dp[t]);
+        if constexpr (COPY) {
+          const int c = t * DCH + ks;
+          if (c < IPW) dma_tile_part<NCH, QST, NW>(qsrc, qss, BUF ? Q0 : Q1, wave, qlo, c);
+          else if (c < 2 * IPW) dma_tile_part<NCH, QST, NW>(osrc, oss, BUF ? O0 : O1, wave, olo, c - IPW);
+        }
       }
     }
     float pv[8], ds[8];
@@ -742,9 +764,13 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
     }
     __syncthreads();
   };
-  for (int st = 0; st < nst; st += 2) {
-    stage(std::integral_constant<int, 0>(), st);
-    if (st + 1 < nst) stage(std::integral_constant<int, 1>(), st + 1);
+  if (nst == 1) {
+    stage(std::integral_constant<int, 0>(), std::false_type(), 0);
+  } else {
+    for (int st = 0; st < nst; st += 2) {
+      stage(std::integral_constant<int, 0>(), std::true_type(), st);
+      if (st + 1 < nst) stage(std::integral_constant<int, 1>(), std::true_type(), st + 1);
+    }
   }
 
   // ---- sum the two query halves: wave (k, 1) hands its partials to wave (k, 0) through tile k's area, which
