@@ -158,6 +158,32 @@ def test_mfma_agrees_with_fma_kernel():
     assert torch.allclose(out_mfma, out_fma, rtol=1.5e-2, atol=3e-2), (out_mfma - out_fma).abs().max()
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,k,n", [(1024, 192, 6144), (10240, 64, 640)])
+def test_tile_aligned_fast_path_layouts_and_bias(dt, ta, tb, m, k, n):
+    """Problems that fill the GPU with 128x256 (first shape) or 256x128 (second) tiles take the
+    direct-to-LDS kernel; every operand layout, bias broadcast over rows, alpha and beta."""
+    a = randn((k, m) if ta else (m, k), dt, 13)
+    b = randn((n, k) if tb else (k, n), dt, 14)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), dt, 15)
+    out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=2.0)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 2.0)
+    check(out, ref, dt, k)
+    assert oracle.rel_l2(f64(out), ref) <= (1e-2 if dt == torch.bfloat16 else 2e-3)
+
+
+def test_tile_aligned_fast_path_batched_and_full_bias():
+    bt, m, k, n = 2, 1024, 128, 6144
+    a, b = randn((bt, m, k), torch.bfloat16, 16), randn((bt, k, n), torch.bfloat16, 17)
+    bias = randn((bt, m, n), torch.bfloat16, 18)
+    out = torch.baddbmm(bias.to(dev), a.to(dev), b.to(dev), alpha=1.5, beta=-1.0)
+    ref = np.stack([oracle.gemm(f64(a[i]), f64(b[i]), f64(bias[i]), 1.5, -1.0) for i in range(bt)])
+    check(out, ref, torch.bfloat16, k)
+
+
 def test_baseline_addmm_1024_cubed_with_bias():
     a, b, bias = randn((1024, 1024), torch.bfloat16, 1), randn((1024, 1024), torch.bfloat16, 2), randn((1024,), torch.bfloat16, 3)
     out = torch.addmm(bias.to(dev), a.to(dev), b.to(dev))

@@ -15,7 +15,7 @@
 //   * tiles are numbered N-fastest so the default round-robin placement of workgroups over the 8 XCDs
 //     gives each XCD a band of N-panels that it reads once into its own L2.
 #include "../hrt/registry.h"
-#include "mfma_common.h"
+#include "lds_stage.h"
 
 namespace hk {
 
@@ -278,6 +278,201 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
                                    1, p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N);
 }
 
+// ---- fast path: tile-aligned GEMMs, operands copied global -> LDS directly ------------------------------------
+//
+// C tile BM x BN (128 x 256 or 256 x 128) per workgroup of 8 wavefronts (two per SIMD); each wavefront owns
+// a 64 x 64 sub-tile as 2 x 2 v_mfma_f32_32x32x16 accumulators (64 registers).  K advances in steps of 64
+// through double-buffered LDS filled by global_load_lds_dwordx4 copies of the operands' raw rows, spread
+// over the previous step's MFMAs, one barrier per step.  An operand whose K axis is contiguous (A [M][K],
+// or B given as [N][K]) is staged as [row][k] and read with 128-bit row reads; an operand contiguous along
+// M or N (A given as [K][M], B as [K][N]) is staged as [k][row] and read with ds_read_b64_tr_b16 column
+// reads, so all four layouts need no register transposes.  Epilogue: alpha * acc + beta * bias in fp32,
+// one rounding, transposed through LDS so that C is written as 16-byte row pieces.
+constexpr int GBK = 64;
+
+template <typename T, int BM, int BN, bool ATR, bool BTR>
+__global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int tiles_n) {
+  constexpr int NW = 8;
+  constexpr int WNN = BN / 64;  // wavefronts along n
+  static_assert((BM / 64) * WNN == NW, "eight 64 x 64 sub-tiles");
+  constexpr int A_ROWS = ATR ? GBK : BM, A_NCH = ATR ? BM / 8 : GBK / 8;
+  constexpr int B_ROWS = BTR ? GBK : BN, B_NCH = BTR ? BN / 8 : GBK / 8;
+  constexpr int A_ROWB = A_NCH * 16, B_ROWB = B_NCH * 16;
+  constexpr int A_TILE = A_ROWS * A_ROWB, B_TILE = B_ROWS * B_ROWB;
+  constexpr int IPA = A_ROWS * A_NCH / 64 / NW, IPB = B_ROWS * B_NCH / 64 / NW;  // copies per wavefront
+  constexpr int RS = 40;                  // epilogue row stride (floats): conflict-free half-wave writes
+  constexpr int AREA = 64 * RS * 4;       // one wavefront's epilogue area (bytes)
+  constexpr int PA = A_TILE / AREA, PB = B_TILE / AREA;  // epilogue areas per A / B tile
+  static_assert(2 * PA + 2 * PB >= NW, "epilogue areas fit the tiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], b0_raw[B_TILE], b1_raw[B_TILE];
+  HK_L uint8_t* const A0 = (HK_L uint8_t*)a0_raw;
+  HK_L uint8_t* const A1 = (HK_L uint8_t*)a1_raw;
+  HK_L uint8_t* const B0 = (HK_L uint8_t*)b0_raw;
+  HK_L uint8_t* const B1 = (HK_L uint8_t*)b1_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WNN, wn = wave % WNN;
+  const int l32 = lane & 31, h = lane >> 5, s16 = lane & 15, g2 = (lane >> 4) & 1;
+  // tiles numbered n-fastest: the workgroups of one XCD (round-robin placement) share a band of B panels
+  const uint32_t tile = blockIdx.x;
+  const uint32_t tn = tile % (uint32_t)tiles_n, tm = (tile / (uint32_t)tiles_n) % (uint32_t)tiles_m;
+  const uint32_t bz = tile / ((uint32_t)tiles_n * (uint32_t)tiles_m);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int nk = (int)(p.K / GBK);
+
+  // copy sources (bytes) of K step 0 and the per-step advance
+  const HK_G uint8_t* Ab = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.a) + bz * p.a_sb +
+                                                                 (ATR ? m0 : m0 * p.a_sm));
+  const HK_G uint8_t* Bb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.b) + bz * p.b_sb +
+                                                                 (BTR ? n0 : n0 * p.b_sn));
+  const uint32_t ass = (uint32_t)((ATR ? p.a_sk : p.a_sm) * 2), bss = (uint32_t)((BTR ? p.b_sk : p.b_sn) * 2);
+  const int64_t astep = ATR ? (int64_t)GBK * p.a_sk * 2 : GBK * 2, bstep = BTR ? (int64_t)GBK * p.b_sk * 2 : GBK * 2;
+  const DmaLanes alo = dma_lane_offsets<A_NCH>(ass, lane, wave * IPA), blo = dma_lane_offsets<B_NCH>(bss, lane, wave * IPB);
+
+  // fragment offsets inside a tile for m (n) sub-tile i (j) and 16-wide K slice kk
+  int aoff[2][4], boff[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if constexpr (!ATR) {
+        aoff[i][kk] = tile_off<A_NCH>(wm * 64 + i * 32 + l32, 2 * kk + h);
+      } else {  // two column reads per fragment: rows 16 kk + 8 h + 4 t + (s >> 2), t = kk & 1 here; kk >> 1 unused
+        const int t = kk & 1;
+        const int col = wm * 64 + i * 32 + 16 * g2 + 4 * (s16 & 3);
+        aoff[i][kk] = kk < 2 ? tile_off<A_NCH>(8 * h + 4 * t + (s16 >> 2), col >> 3) + (s16 & 1) * 8 : 0;
+      }
+      if constexpr (!BTR) {
+        boff[i][kk] = tile_off<B_NCH>(wn * 64 + i * 32 + l32, 2 * kk + h);
+      } else {
+        const int t = kk & 1;
+        const int col = wn * 64 + i * 32 + 16 * g2 + 4 * (s16 & 3);
+        boff[i][kk] = kk < 2 ? tile_off<B_NCH>(8 * h + 4 * t + (s16 >> 2), col >> 3) + (s16 & 1) * 8 : 0;
+      }
+    }
+  auto afrag = [&](const HK_L uint8_t* At, int i, int kk) -> u32x4 {
+    if constexpr (!ATR) {
+      return *reinterpret_cast<const HK_L u32x4*>(At + aoff[i][kk]);
+    } else {
+      const u32x2 lo = lds_tr4(At + aoff[i][0] + kk * 16 * A_ROWB), hi = lds_tr4(At + aoff[i][1] + kk * 16 * A_ROWB);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
+  };
+  auto bfrag = [&](const HK_L uint8_t* Bt, int j, int kk) -> u32x4 {
+    if constexpr (!BTR) {
+      return *reinterpret_cast<const HK_L u32x4*>(Bt + boff[j][kk]);
+    } else {
+      const u32x2 lo = lds_tr4(Bt + boff[j][0] + kk * 16 * B_ROWB), hi = lds_tr4(Bt + boff[j][1] + kk * 16 * B_ROWB);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+
+#pragma unroll
+  for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
+#pragma unroll
+  for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
+  __syncthreads();
+
+  // K step kt: MFMAs from buffer kt & 1, copies of step min(kt + 1, nk - 1) into the other buffer placed
+  // after the first MFMAs (the last step re-copies itself into a buffer nobody reads again)
+  auto step = [&](auto bc, int kt) {
+    constexpr int BUF = decltype(bc)::value;
+    const int kn = kt + 1 < nk ? kt + 1 : nk - 1;
+    const HK_G uint8_t* an = Ab + kn * astep;
+    const HK_G uint8_t* bn = Bb + kn * bstep;
+    const HK_L uint8_t* At = BUF ? A1 : A0;
+    const HK_L uint8_t* Bt = BUF ? B1 : B0;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 a0 = afrag(At, 0, kk), a1 = afrag(At, 1, kk), b0 = bfrag(Bt, 0, kk), b1 = bfrag(Bt, 1, kk);
+      acc[0][0] = Mfma32<T>::mac(a0, b0, acc[0][0]);
+      acc[0][1] = Mfma32<T>::mac(a0, b1, acc[0][1]);
+      acc[1][0] = Mfma32<T>::mac(a1, b0, acc[1][0]);
+      acc[1][1] = Mfma32<T>::mac(a1, b1, acc[1][1]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = kk * 4 + q;
+        if (c < IPA) dma_tile_part<A_NCH, A_ROWS, NW>(an, ass, BUF ? A0 : A1, wave, alo, c);
+        else if (c < IPA + IPB) dma_tile_part<B_NCH, B_ROWS, NW>(bn, bss, BUF ? B0 : B1, wave, blo, c - IPA);
+      }
+    }
+    __syncthreads();
+  };
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(std::integral_constant<int, 0>(), kt);
+    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+  }
+
+  // ---- epilogue: per n sub-tile j, the 64 x 32 fp32 block goes through this wavefront's area as [m][n]
+  float* const area = reinterpret_cast<float*>(wave < PA            ? a0_raw + wave * AREA
+                                              : wave < 2 * PA        ? a1_raw + (wave - PA) * AREA
+                                              : wave < 2 * PA + PB   ? b0_raw + (wave - 2 * PA) * AREA
+                                                                     : b1_raw + (wave - 2 * PA - PB) * AREA);
+  const bool has_bias = p.has_bias != 0;
+  const HK_G uint16_t* bias = gcptr<uint16_t>(p.bias) + bz * p.bias_sb;
+  HK_G uint16_t* C = gptr<uint16_t>(p.c) + bz * p.c_sb;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t gn = n0 + wn * 64 + j * 32 + l32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        float v = p.alpha * acc[i][j][e];
+        if (has_bias) v += p.beta * T::to_f32(bias[(m0 + wm * 64 + r) * p.bias_sm + gn * p.bias_sn]);
+        area[r * RS + l32] = v;
+      }
+    // 4 lanes per 32-wide row, 8 floats each: 16 rows per pass
+#pragma unroll
+    for (int ps = 0; ps < 4; ++ps) {
+      const int r = ps * 16 + (lane >> 2), c8 = (lane & 3) * 8;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(area + r * RS + c8);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(area + r * RS + c8 + 4);
+      *reinterpret_cast<HK_G u32x4*>(C + (m0 + wm * 64 + r) * p.c_sm + n0 + wn * 64 + j * 32 + c8) =
+          u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+    }
+  }
+}
+
+// The fast path applies to tile-aligned problems whose operands are contiguous along one axis with 16-byte
+// aligned rows, a row-contiguous C, and per-tile row offsets that fit the copies' 32-bit lane offsets.
+bool mm_dma_ok(const hrt_mm_args& a, int BM, int BN, bool& atr, bool& btr) {
+  if (a.M % BM || a.N % BN || a.K % GBK || a.K < GBK) return false;
+  const auto al = [](uint64_t x) { return x % 16 == 0; };
+  if (!al(a.a) || !al(a.b) || !al(a.c) || a.c_sn != 1 || a.c_sm % 8 || (a.batch > 1 && (a.a_sb % 8 || a.b_sb % 8 || a.c_sb % 8)))
+    return false;
+  if (a.a_sk == 1 && a.a_sm % 8 == 0) atr = false;
+  else if (a.a_sm == 1 && a.a_sk % 8 == 0) atr = true;
+  else return false;
+  if (a.b_sk == 1 && a.b_sn % 8 == 0) btr = false;
+  else if (a.b_sn == 1 && a.b_sk % 8 == 0) btr = true;
+  else return false;
+  const int64_t lim = (int64_t)1 << 31;
+  const int64_t arows = atr ? GBK : BM, brows = btr ? GBK : BN;
+  return (atr ? a.a_sk : a.a_sm) * 2 * (arows + 1) < lim && (btr ? a.b_sk : a.b_sn) * 2 * (brows + 1) < lim;
+}
+
+template <typename T, int BM, int BN>
+bool queue_dma(const hrt_mm_args& a, hipStream_t s) {
+  bool atr = false, btr = false;
+  if (!mm_dma_ok(a, BM, BN, atr, btr)) return false;
+  const int tm = (int)(a.M / BM), tn = (int)(a.N / BN);
+  const dim3 g((uint32_t)((int64_t)tm * tn * a.batch));
+  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, false, false>), g, dim3(512), 0, s, a, tm, tn);
+  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, false, true>), g, dim3(512), 0, s, a, tm, tn);
+  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, true, false>), g, dim3(512), 0, s, a, tm, tn);
+  else hipLaunchKernelGGL((mm_dma<T, BM, BN, true, true>), g, dim3(512), 0, s, a, tm, tn);
+  return true;
+}
+
 // Which loader an operand can use.  rows = M (A) or N (B); s_r / s_k its strides.
 int pick_mode(uint64_t ptr, int64_t s_b, int64_t s_r, int64_t s_k, int64_t rows, int64_t K, int64_t batch) {
   const bool aligned = ptr % 16 == 0 && (batch == 1 || s_b % 8 == 0);
@@ -328,6 +523,11 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int64_t med = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
   const int64_t small = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
   if (small > 0x7fffffffLL) return ctx.fail("GEMM grid too large");
+  // fast path when the problem fills the GPU with 128 x 256 (or 256 x 128) tiles
+  if (a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
+  if (a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (am == GATHER || bm == GATHER) {
     dispatch_gather<T>(a, am, bm, ctx.stream);
   } else if (big >= 240) {
