@@ -282,8 +282,9 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 //
 // C tile BM x BN (128 x 256 or 256 x 128) per workgroup of 8 wavefronts (two per SIMD); each wavefront owns
 // a 64 x 64 sub-tile as 2 x 2 v_mfma_f32_32x32x16 accumulators (64 registers).  K advances in steps of 64
-// through double-buffered LDS filled by global_load_lds_dwordx4 copies of the operands' raw rows, spread
-// over the previous step's MFMAs, one barrier per step.  An operand whose K axis is contiguous (A [M][K],
+// through a ring of three LDS buffers filled by global_load_lds_dwordx4 copies of the operands' raw rows:
+// the copies of step kt + 2 are spread over the MFMAs of step kt, so a copy has two steps to land (one step
+// of compute is shorter than the L2 latency plus the transfer of a 48 KiB step), one barrier per step.  An operand whose K axis is contiguous (A [M][K],
 // or B given as [N][K]) is staged as [row][k] and read with 128-bit row reads; an operand contiguous along
 // M or N (A given as [K][M], B as [K][N]) is staged as [k][row] and read with ds_read_b64_tr_b16 column
 // reads, so all four layouts need no register transposes.  Epilogue: alpha * acc + beta * bias in fp32,
@@ -304,11 +305,17 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
   constexpr int AREA = 64 * RS * 4;       // one wavefront's epilogue area (bytes)
   constexpr int PA = A_TILE / AREA, PB = B_TILE / AREA;  // epilogue areas per A / B tile
   static_assert(2 * PA + 2 * PB >= NW, "epilogue areas fit the tiles");
-  __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], b0_raw[B_TILE], b1_raw[B_TILE];
+  // separate LDS objects per buffer, so that reads of one are known not to alias copies into another
+  __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], a2_raw[A_TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t b0_raw[B_TILE], b1_raw[B_TILE], b2_raw[B_TILE];
   HK_L uint8_t* const A0 = (HK_L uint8_t*)a0_raw;
   HK_L uint8_t* const A1 = (HK_L uint8_t*)a1_raw;
+  HK_L uint8_t* const A2 = (HK_L uint8_t*)a2_raw;
   HK_L uint8_t* const B0 = (HK_L uint8_t*)b0_raw;
   HK_L uint8_t* const B1 = (HK_L uint8_t*)b1_raw;
+  HK_L uint8_t* const B2 = (HK_L uint8_t*)b2_raw;
+  auto abuf = [&](auto ic) { constexpr int I = decltype(ic)::value; return I == 0 ? A0 : I == 1 ? A1 : A2; };
+  auto bbuf = [&](auto ic) { constexpr int I = decltype(ic)::value; return I == 0 ? B0 : I == 1 ? B1 : B2; };
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -374,21 +381,31 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
 
+  // steps 0 and 1 (step min(1, nk - 1): a single-step K re-copies step 0 into a buffer nobody reads)
 #pragma unroll
   for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
 #pragma unroll
   for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
-  __syncthreads();
+  const int k1 = nk > 1 ? 1 : 0;
+#pragma unroll
+  for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab + k1 * astep, ass, A1, wave, alo, c);
+#pragma unroll
+  for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb + k1 * bstep, bss, B1, wave, blo, c);
+  barrier_keep_vm<IPA + IPB>();  // step 0 landed everywhere, step 1 in flight
 
-  // K step kt: MFMAs from buffer kt & 1, copies of step min(kt + 1, nk - 1) into the other buffer placed
-  // after the first MFMAs (the last step re-copies itself into a buffer nobody reads again)
+  // K step kt: MFMAs from buffer kt % 3, copies of step min(kt + 2, nk - 1) into buffer (kt + 2) % 3 (read
+  // by step kt - 1, whose readers all passed the previous barrier) placed after the first MFMAs; steps
+  // past the end re-copy the last step into a buffer nobody reads again.  Before the barrier that ends
+  // the step each wavefront waits for its copies of the previous step only, so step kt + 1's buffer is
+  // complete after the barrier while the copies of step kt + 2 stay in flight.
   auto step = [&](auto bc, int kt) {
     constexpr int BUF = decltype(bc)::value;
-    const int kn = kt + 1 < nk ? kt + 1 : nk - 1;
+    constexpr int NXT = (BUF + 2) % 3;
+    const int kn = kt + 2 < nk ? kt + 2 : nk - 1;
     const HK_G uint8_t* an = Ab + kn * astep;
     const HK_G uint8_t* bn = Bb + kn * bstep;
-    const HK_L uint8_t* At = BUF ? A1 : A0;
-    const HK_L uint8_t* Bt = BUF ? B1 : B0;
+    const HK_L uint8_t* At = abuf(bc);
+    const HK_L uint8_t* Bt = bbuf(bc);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const u32x4 a0 = afrag(At, 0, kk), a1 = afrag(At, 1, kk), b0 = bfrag(Bt, 0, kk), b1 = bfrag(Bt, 1, kk);
@@ -399,16 +416,22 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int c = kk * 4 + q;
-        if (c < IPA) dma_tile_part<A_NCH, A_ROWS, NW>(an, ass, BUF ? A0 : A1, wave, alo, c);
-        else if (c < IPA + IPB) dma_tile_part<B_NCH, B_ROWS, NW>(bn, bss, BUF ? B0 : B1, wave, blo, c - IPA);
+        if (c < IPA) dma_tile_part<A_NCH, A_ROWS, NW>(an, ass, abuf(std::integral_constant<int, NXT>()), wave, alo, c);
+        else if (c < IPA + IPB)
+          dma_tile_part<B_NCH, B_ROWS, NW>(bn, bss, bbuf(std::integral_constant<int, NXT>()), wave, blo, c - IPA);
       }
     }
-    __syncthreads();
+    barrier_keep_vm<IPA + IPB>();
   };
-  for (int kt = 0; kt < nk; kt += 2) {
+  int kt = 0;
+  for (; kt + 3 <= nk; kt += 3) {
     step(std::integral_constant<int, 0>(), kt);
-    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+    step(std::integral_constant<int, 1>(), kt + 1);
+    step(std::integral_constant<int, 2>(), kt + 2);
   }
+  if (kt < nk) step(std::integral_constant<int, 0>(), kt);
+  if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+  __syncthreads();  // the last copies have landed before the epilogue reuses the tiles
 
   // ---- epilogue: per n sub-tile j, the 64 x 32 fp32 block goes through this wavefront's area as [m][n]
   float* const area = reinterpret_cast<float*>(wave < PA            ? a0_raw + wave * AREA
@@ -422,14 +445,24 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
   for (int j = 0; j < 2; ++j) {
     const int64_t gn = n0 + wn * 64 + j * 32 + l32;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+      float bv[16];  // beta * bias, all 16 loads in flight together
+      if (has_bias) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          bv[e] = p.beta * T::to_f32(bias[(m0 + wm * 64 + r) * p.bias_sm + gn * p.bias_sn]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) bv[e] = 0.f;
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-        float v = p.alpha * acc[i][j][e];
-        if (has_bias) v += p.beta * T::to_f32(bias[(m0 + wm * 64 + r) * p.bias_sm + gn * p.bias_sn]);
-        area[r * RS + l32] = v;
+        area[r * RS + l32] = p.alpha * acc[i][j][e] + bv[e];
       }
+    }
     // 4 lanes per 32-wide row, 8 floats each: 16 rows per pass
 #pragma unroll
     for (int ps = 0; ps < 4; ++ps) {

@@ -170,6 +170,20 @@ __device__ __forceinline__ u32x2 lds_tr4(const HK_L uint8_t* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((HK_L i16x4_t*)p));
 }
 
+// Workgroup barrier that lets the N most recently issued vector-memory operations of this wavefront (the
+// copies of a later stage) stay in flight: waits until at most N are outstanding, then joins the barrier.
+// __syncthreads() would wait for all of them (its release fence waits for every outstanding load).  The
+// wait is the s_waitcnt builtin (vmcnt in bits 3:0 and 15:14, expcnt 7 and lgkmcnt 15 = no wait), which
+// the compiler's wait-insertion pass takes into account: reads of a stage whose copies it has seen
+// complete get no further wait.  The barrier is an asm statement with a memory clobber, so the compiler
+// moves no memory access across it.
+template <int N>
+__device__ __forceinline__ void barrier_keep_vm() {
+  static_assert(N >= 0 && N < 64, "the vmcnt field holds 0..63");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Max of the two half-waves' values (lane and lane ^ 32) without an LDS round trip.
 __device__ __forceinline__ float halfswap_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
