@@ -387,6 +387,7 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
 #pragma unroll
   for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
   const int k1 = nk > 1 ? 1 : 0;
+  issue_order_fence();
 #pragma unroll
   for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab + k1 * astep, ass, A1, wave, alo, c);
 #pragma unroll

@@ -145,6 +145,24 @@ __device__ __forceinline__ void dma_tile_part(const HK_G uint8_t* src, uint32_t 
   dma16(src + (uint32_t)(j * RPI) * ss + lo.off[i % 4], tile + j * 1024);
 }
 
+// The same copy through a raw buffer resource (buffer_load_dwordx4 ... lds, same LDS layout: lane i's 16
+// bytes at the instruction's LDS base + 16 i, checked on the device): the resource holds the 64-bit base in
+// scalar registers and the wavefront-uniform row offset goes in the scalar offset, so a copy needs no
+// per-lane 64-bit address arithmetic, only the 32-bit lane offsets of dma_lane_offsets.  The range check
+// is disabled (num_records = 2^32 - 1): callers copy only rows that exist.  Word 3 = 0x00020000 selects the
+// 32-bit data format used for raw byte-addressed buffers on CDNA.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_rsrc(const HK_G uint8_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(base), (short)0, -1, 0x00020000);
+}
+template <int NCH, int ROWS, int NW>
+__device__ __forceinline__ void dma_tile_part_rs(__amdgpu_buffer_rsrc_t rs, uint32_t ss, HK_L uint8_t* tile, int wave,
+                                                 const DmaLanes& lo, int i) {
+  constexpr int RPI = 64 / NCH;
+  constexpr int IPW = ROWS * NCH / 64 / NW;
+  const int j = wave * IPW + i;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + j * 1024, 16, (int)lo.off[i % 4], (int)((uint32_t)(j * RPI) * ss), 0, 0);
+}
+
 // First row of the tile that stage st copies when the sequence has more than one stage (len > ROWS): stage
 // st covers rows [st ROWS, (st + 1) ROWS); the last, ragged stage copies the full window that ends at row
 // len - 1 instead (origin len - ROWS), so no copy reads past the sequence, and its rows below st ROWS
@@ -183,6 +201,10 @@ __device__ __forceinline__ void barrier_keep_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
   asm volatile("s_barrier" ::: "memory");
 }
+
+// Keeps the compiler from moving memory accesses (copies included) across this point, so that the copies
+// before it are issued before those after it, as barrier_keep_vm's count assumes.
+__device__ __forceinline__ void issue_order_fence() { asm volatile("" ::: "memory"); }
 
 // Max of the two half-waves' values (lane and lane ^ 32) without an LDS round trip.
 __device__ __forceinline__ float halfswap_max(float v) {

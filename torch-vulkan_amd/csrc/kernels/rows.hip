@@ -374,9 +374,9 @@ __global__ __launch_bounds__(256) void ln_fwd_row(const typename T::storage* __r
   }
 }
 
-// Backward, register path: workgroup = one chunk of 4 rows, one wavefront per row.  dx per row;
-// the per-column partial sums of g*xhat and g of the 4 rows are combined in LDS and written as one
-// ws row pair per chunk.
+// Backward, register path: workgroup = one chunk of 4 rows, one wavefront per row.  dx per row; the
+// per-column partial sums of g*xhat and g of the 4 rows are combined through LDS (every wavefront stores
+// its row, then each thread sums the 4 rows of its columns) and written as one ws row pair per chunk.
 template <typename T, int NV>
 __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __restrict__ x,
                                                   const typename T::storage* __restrict__ g,
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
                                                   typename T::storage* __restrict__ dx, float* __restrict__ ws, int64_t rows,
                                                   int64_t D) {
   constexpr int V = Vec<T>::N;
-  extern __shared__ float part[];  // [2][D] when ws != nullptr
+  extern __shared__ float part[];  // [4 rows][D] when ws != nullptr
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
   const bool live = row < rows;
@@ -434,30 +434,29 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
     }
   }
   if (!ws) return;  // uniform across the workgroup: no barrier below is skipped by only some waves
-  for (int step = 0; step < 4; ++step) {
-    if (wave == step) {
+  // rows past the end hold zeros (xh = gv = 0 above)
+  float* out = ws + (int64_t)blockIdx.x * 2 * D;
 #pragma unroll
-      for (int c = 0; c < NV; ++c) {
-        const int64_t col = (int64_t)(c * 64 + lane) * V;
-        if (col < D) {
+  for (int qn = 0; qn < 2; ++qn) {  // qn = 0: g * xhat, 1: g
+    if (qn) __syncthreads();         // the previous quantity's sums have been read
 #pragma unroll
-          for (int e = 0; e < V; ++e) {
-            const float pw = gv[c][e] * xh[c][e], pb = gv[c][e];
-            if (step == 0) {
-              part[col + e] = pw;
-              part[D + col + e] = pb;
-            } else {
-              part[col + e] += pw;
-              part[D + col + e] += pb;
-            }
-          }
-        }
+    for (int c = 0; c < NV; ++c) {
+      const int64_t col = (int64_t)(c * 64 + lane) * V;
+      if (col < D) {
+        float o[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = qn ? gv[c][e] : gv[c][e] * xh[c][e];
+        Vec<F32>::store(part + wave * D + col, o);
+        if constexpr (V == 8) Vec<F32>::store(part + wave * D + col + 4, o + 4);
       }
     }
     __syncthreads();
+    for (int64_t i = (int64_t)threadIdx.x * 4; i < D; i += 256 * 4) {
+      const f32x4 r0 = *reinterpret_cast<const f32x4*>(part + i), r1 = *reinterpret_cast<const f32x4*>(part + D + i);
+      const f32x4 r2 = *reinterpret_cast<const f32x4*>(part + 2 * D + i), r3 = *reinterpret_cast<const f32x4*>(part + 3 * D + i);
+      *reinterpret_cast<f32x4*>(out + qn * D + i) = (r0 + r1) + (r2 + r3);
+    }
   }
-  float* out = ws + (int64_t)blockIdx.x * 2 * D;
-  for (int64_t i = threadIdx.x; i < 2 * D; i += 256) out[i] = part[i];
 }
 
 // Backward, generic path: workgroup per chunk of 4 rows; ws accumulated in place (each thread owns its
@@ -506,29 +505,31 @@ __global__ __launch_bounds__(256) void ln_bwd_row(const typename T::storage* __r
   }
 }
 
-// dw[d] = sum_c ws[c][0][d], db[d] = sum_c ws[c][1][d]: 64 columns x 4 chunk groups per workgroup.
+// dw[d] = sum_c ws[c][0][d], db[d] = sum_c ws[c][1][d]: workgroup (column block of 64, quantity) with
+// 4 chunk groups of 64 threads; each thread keeps 8 loads in flight (independent partial sums), and the
+// groups are combined in a fixed order, so the result does not depend on timing.
 template <typename T>
 __global__ __launch_bounds__(256) void ln_wgrad_reduce(const float* __restrict__ ws, typename T::storage* __restrict__ dw,
                                                        typename T::storage* __restrict__ db, int64_t chunks, int64_t D) {
-  __shared__ float sw[4][64], sb[4][64];
+  __shared__ float sp[4][64];
   const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int qn = blockIdx.y;  // 0: dw, 1: db
+  typename T::storage* dst = qn ? db : dw;
+  if (!dst) return;  // uniform over the workgroup
   const int64_t col = (int64_t)blockIdx.x * 64 + cl;
-  float aw = 0.f, ab = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (col < D) {
-    for (int64_t c = grp; c < chunks; c += 4) {
-      aw += ws[c * 2 * D + col];
-      ab += ws[c * 2 * D + D + col];
+    const float* src = ws + qn * D + col;
+    int64_t c = grp;
+    for (; c + 28 < chunks; c += 32) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += src[(c + 4 * u) * 2 * D];
     }
+    for (int u = 0; c < chunks; c += 4, ++u) acc[u & 7] += src[c * 2 * D];
   }
-  sw[grp][cl] = aw;
-  sb[grp][cl] = ab;
+  sp[grp][cl] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (grp == 0 && col < D) {
-    const float tw = sw[0][cl] + sw[1][cl] + sw[2][cl] + sw[3][cl];
-    const float tb = sb[0][cl] + sb[1][cl] + sb[2][cl] + sb[3][cl];
-    if (dw) dw[col] = T::from_f32(tw);
-    if (db) db[col] = T::from_f32(tb);
-  }
+  if (grp == 0 && col < D) dst[col] = T::from_f32((sp[0][cl] + sp[1][cl]) + (sp[2][cl] + sp[3][cl]));
 }
 
 template <typename T>
@@ -576,8 +577,8 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   float* ws = (float*)a.ws;
   const float *mu = (const float*)a.mean, *rs = (const float*)a.rstd;
   int nv = reg_nv<T>(a.D, {a.x, a.g, a.w, a.dx});
-  const size_t lds = ws ? (size_t)(2 * a.D) * 4 : 0;
-  if (lds > 64 * 1024) nv = 0;
+  const size_t lds = ws ? (size_t)(4 * a.D) * 4 : 0;
+  if (lds > 64 * 1024 || a.D % 4) nv = 0;
   const dim3 grid((uint32_t)chunks);
   switch (nv) {
     case 1: hipLaunchKernelGGL((ln_bwd_reg<T, 1>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
@@ -599,7 +600,7 @@ bool launch_ln_wgrad(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws") || (a.dw && !ctx.check(a.dw, a.D * sizeof(S), "dw")) ||
       (a.db && !ctx.check(a.db, a.D * sizeof(S), "db")))
     return false;
-  hipLaunchKernelGGL(ln_wgrad_reduce<T>, dim3((uint32_t)cdiv(a.D, 64)), dim3(256), 0, ctx.stream, (const float*)a.ws,
+  hipLaunchKernelGGL(ln_wgrad_reduce<T>, dim3((uint32_t)cdiv(a.D, 64), 2), dim3(256), 0, ctx.stream, (const float*)a.ws,
                      (S*)a.dw, (S*)a.db, chunks, a.D);
   return hrt::launch_ok(hipGetLastError(), ctx, "ln_wgrad");
 }
