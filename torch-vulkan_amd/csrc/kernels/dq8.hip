@@ -2,18 +2,21 @@
 // torch_vulkan/__init__.py:203-205):  out[r, c] = round_dt(float(q[r, c]) * float(scale[r, c / 64])).
 //
 // HBM-bound: 1 byte in + 2 (bf16/f16) or 4 (f32) bytes out per element plus 2 bytes of scale per 64.
-// Fast path: each thread moves 16 int8 with one 128-bit load and writes them with 128-bit stores
-// (a 16-element chunk never crosses a row or a 64-column scale block when cols % 16 == 0); two chunks
-// per thread are loaded before any store to keep more bytes in flight.  Any other shape or alignment
-// takes the per-element path.  Results are bit-exact: the fp32 product of an int8 and a bf16 is exact,
-// so the only rounding is the final RNE store.
+// Fast path: each thread moves 16 int8 with one streaming 128-bit load and writes them with 128-bit
+// streaming stores (a 16-element chunk never crosses a row or a 64-column scale block when cols % 16 == 0);
+// one chunk per thread and many workgroups streams best (measured against 1-8 chunks per thread).  The
+// chunk's row comes from a double-precision reciprocal of the chunks-per-row count corrected by one step,
+// which is exact for every chunk index below 2^40 (the product is then within 2^-12 of ch / cpr, so the
+// truncation is off by at most one; no 64-bit integer division).  Any other shape or alignment takes the
+// per-element path.  Results are bit-exact: the fp32 product of an int8 and a bf16 is exact, so the only
+// rounding is the final RNE store.
 #include "../hrt/registry.h"
 #include "device_common.h"
 
 namespace hk {
 namespace {
 
-constexpr int kChunks = 2;  // 16-element chunks per thread
+constexpr int kChunks = 1;  // 16-element chunks per thread
 
 template <typename T>
 __device__ __forceinline__ void store16(typename T::storage* out, int64_t e, const float* v);
@@ -63,17 +66,20 @@ __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)(int8_
 template <typename T>
 __global__ __launch_bounds__(256) void dq8_vec(const int8_t* __restrict__ q, const uint16_t* __restrict__ scale,
                                                typename T::storage* __restrict__ out, int64_t cols, int64_t nblocks,
-                                               int64_t nchunks) {
+                                               int64_t nchunks, double inv_cpr) {
   const int64_t base = (int64_t)blockIdx.x * (256 * kChunks) + threadIdx.x;
+  const int64_t cpr = cols >> 4;  // chunks per row
   u32x4 qv[kChunks];
   float sv[kChunks];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     const int64_t ch = base + c * 256;
     if (ch < nchunks) {
-      const int64_t e = ch * 16;
-      qv[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + e));
-      const int64_t r = e / cols, col = e - r * cols;
+      qv[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + ch * 16));
+      int64_t r = (int64_t)((double)ch * inv_cpr);
+      if (r * cpr > ch) --r;
+      else if ((r + 1) * cpr <= ch) ++r;
+      const int64_t col = (ch - r * cpr) << 4;
       sv[c] = bf16_bits_to_f32(scale[r * nblocks + (col >> 6)]);
     }
   }
@@ -112,12 +118,13 @@ bool launch_dq8(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!ctx.check(a.q, (uint64_t)total, "q") || !ctx.check(a.scale, (uint64_t)(a.rows * a.nblocks) * 2, "scale") ||
       !ctx.check(a.out, (uint64_t)total * osz, "out"))
     return false;
-  const bool vec = a.cols % 16 == 0 && a.q % 16 == 0 && a.out % 16 == 0;
+  const bool vec = a.cols % 16 == 0 && a.q % 16 == 0 && a.out % 16 == 0 && total / 16 < ((int64_t)1 << 40);
   if (vec) {
     const int64_t nchunks = total / 16;
     const int64_t grid = cdiv(nchunks, 256 * kChunks);
     hipLaunchKernelGGL(dq8_vec<T>, dim3((uint32_t)grid), dim3(256), 0, ctx.stream, (const int8_t*)a.q,
-                       (const uint16_t*)a.scale, (typename T::storage*)a.out, a.cols, a.nblocks, nchunks);
+                       (const uint16_t*)a.scale, (typename T::storage*)a.out, a.cols, a.nblocks, nchunks,
+                       1.0 / (double)(a.cols / 16));
   } else {
     int64_t grid = cdiv(total, 256);
     if (grid > 16384) grid = 16384;

@@ -20,23 +20,28 @@ constexpr int kMaxNV = 8;  // 16-byte vectors per lane on the register path
 // Load / store 16 bytes as float values.
 template <typename T>
 struct Vec;
+// 16-byte raw access: rd / wr go through the caches, rd_nt / wr_nt are streaming (nontemporal) accesses
+// for data that is touched once; unpack / pack convert between the raw vector and N floats.
+__device__ __forceinline__ u32x4 rd(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 rd_nt(const void* p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)); }
+__device__ __forceinline__ void wr_nt(void* p, u32x4 w) { __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p)); }
+
 template <>
 struct Vec<F32> {
   static constexpr int N = 4;
-  __device__ __forceinline__ static void load(const float* p, float* v) {
-    f32x4 w = *reinterpret_cast<const f32x4*>(p);
-    v[0] = w.x, v[1] = w.y, v[2] = w.z, v[3] = w.w;
+  __device__ __forceinline__ static void unpack(u32x4 w, float* v) {
+    v[0] = __uint_as_float(w.x), v[1] = __uint_as_float(w.y), v[2] = __uint_as_float(w.z), v[3] = __uint_as_float(w.w);
   }
-  __device__ __forceinline__ static void store(float* p, const float* v) {
-    f32x4 w = {v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4*>(p) = w;
+  __device__ __forceinline__ static u32x4 pack(const float* v) {
+    return u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
   }
+  __device__ __forceinline__ static void load(const float* p, float* v) { unpack(rd(p), v); }
+  __device__ __forceinline__ static void store(float* p, const float* v) { *reinterpret_cast<u32x4*>(p) = pack(v); }
 };
 template <typename T16>
 struct Vec16 {
   static constexpr int N = 8;
-  __device__ __forceinline__ static void load(const uint16_t* p, float* v) {
-    u32x4 w = *reinterpret_cast<const u32x4*>(p);
+  __device__ __forceinline__ static void unpack(u32x4 w, float* v) {
     const uint32_t a[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -44,14 +49,11 @@ struct Vec16 {
       v[2 * i + 1] = hi16<T16>(a[i]);
     }
   }
-  __device__ __forceinline__ static void store(uint16_t* p, const float* v) {
-    u32x4 w;
-    w.x = pack2<T16>(v[0], v[1]);
-    w.y = pack2<T16>(v[2], v[3]);
-    w.z = pack2<T16>(v[4], v[5]);
-    w.w = pack2<T16>(v[6], v[7]);
-    *reinterpret_cast<u32x4*>(p) = w;
+  __device__ __forceinline__ static u32x4 pack(const float* v) {
+    return u32x4{pack2<T16>(v[0], v[1]), pack2<T16>(v[2], v[3]), pack2<T16>(v[4], v[5]), pack2<T16>(v[6], v[7])};
   }
+  __device__ __forceinline__ static void load(const uint16_t* p, float* v) { unpack(rd(p), v); }
+  __device__ __forceinline__ static void store(uint16_t* p, const float* v) { *reinterpret_cast<u32x4*>(p) = pack(v); }
 };
 template <>
 struct Vec<BF16> : Vec16<BF16> {};
@@ -75,16 +77,27 @@ __global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage
   const typename T::storage* xr = x + row * R;
   float v[NV][V];
   float m = -INFINITY;
+  u32x4 raw[NV];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < R) raw[c] = rd_nt(xr + col);  // every load in flight before the first use
+  }
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
     if (col < R) {
-      Vec<T>::load(xr + col, v[c]);
+      Vec<T>::unpack(raw[c], v[c]);
 #pragma unroll
       for (int e = 0; e < V; ++e) m = fmaxf(m, v[c][e]);
     }
   }
   m = wave_max(m);
+  // exp(x - m) = exp2(x log2e - m log2e) in one fma + v_exp_f32; special values behave as exp(x - m):
+  // m = -inf (all -inf) or x = m = +inf give NaN, finite x under m = +inf gives 0.  The rounding of
+  // m log2e scales every element of the row by the same factor, which the normalisation cancels.
+  constexpr float kL2e = 1.4426950408889634f;
+  const float nm = -m * kL2e;
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
@@ -92,21 +105,22 @@ __global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage
     if (col < R) {
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        v[c][e] = expf(v[c][e] - m);
+        v[c][e] = __builtin_amdgcn_exp2f(fmaf(v[c][e], kL2e, nm));
         s += v[c][e];
       }
     }
   }
   s = wave_sum(s);
   const bool zero = safe && m == -INFINITY;
+  const float inv = 1.f / s;
   typename T::storage* yr = y + row * R;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
     if (col < R) {
 #pragma unroll
-      for (int e = 0; e < V; ++e) v[c][e] = zero ? 0.f : v[c][e] / s;
-      Vec<T>::store(yr + col, v[c]);
+      for (int e = 0; e < V; ++e) v[c][e] = zero ? 0.f : v[c][e] * inv;
+      wr_nt(yr + col, Vec<T>::pack(v[c]));
     }
   }
 }
@@ -121,12 +135,21 @@ __global__ __launch_bounds__(256) void softmax_bwd_reg(const typename T::storage
   if (row >= rows) return;
   float yv[NV][V], gv[NV][V];
   float d = 0.f;
+  u32x4 ry[NV], rg[NV];
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
     if (col < R) {
-      Vec<T>::load(y + row * R + col, yv[c]);
-      Vec<T>::load(g + row * R + col, gv[c]);
+      ry[c] = rd_nt(y + row * R + col);
+      rg[c] = rd_nt(g + row * R + col);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < R) {
+      Vec<T>::unpack(ry[c], yv[c]);
+      Vec<T>::unpack(rg[c], gv[c]);
 #pragma unroll
       for (int e = 0; e < V; ++e) d += gv[c][e] * yv[c][e];
     }
@@ -138,7 +161,7 @@ __global__ __launch_bounds__(256) void softmax_bwd_reg(const typename T::storage
     if (col < R) {
 #pragma unroll
       for (int e = 0; e < V; ++e) yv[c][e] = yv[c][e] * (gv[c][e] - d);
-      Vec<T>::store(dx + row * R + col, yv[c]);
+      wr_nt(dx + row * R + col, Vec<T>::pack(yv[c]));
     }
   }
 }
@@ -298,11 +321,22 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
   if (row >= rows) return;
   float v[NV][V];
   float s = 0.f;
+  // x, w and b all requested before the reductions (w, b are shared by every row: cached loads)
+  u32x4 rx[NV], rw[NV], rb[NV];
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
     if (col < D) {
-      Vec<T>::load(x + row * D + col, v[c]);
+      rx[c] = rd_nt(x + row * D + col);
+      if (w) rw[c] = rd(w + col);
+      if (b) rb[c] = rd(b + col);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (col < D) {
+      Vec<T>::unpack(rx[c], v[c]);
 #pragma unroll
       for (int e = 0; e < V; ++e) s += v[c][e];
     }
@@ -327,8 +361,8 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
     const int64_t col = (int64_t)(c * 64 + lane) * V;
     if (col < D) {
       float wv[V], bv[V];
-      if (w) Vec<T>::load(w + col, wv);
-      if (b) Vec<T>::load(b + col, bv);
+      if (w) Vec<T>::unpack(rw[c], wv);
+      if (b) Vec<T>::unpack(rb[c], bv);
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         float o = (v[c][e] - mean) * rstd;
@@ -336,7 +370,7 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
         if (b) o += bv[e];
         v[c][e] = o;
       }
-      Vec<T>::store(y + row * D + col, v[c]);
+      wr_nt(y + row * D + col, Vec<T>::pack(v[c]));
     }
   }
   if (lane == 0) {
@@ -391,6 +425,16 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
   const bool live = row < rows;
   float xh[NV][V], gv[NV][V];
   float s1 = 0.f, s2 = 0.f, mean = 0.f, rstd = 0.f;
+  u32x4 rx[NV], rg[NV], rw[NV];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int64_t col = (int64_t)(c * 64 + lane) * V;
+    if (live && col < D) {
+      rx[c] = rd_nt(x + row * D + col);
+      rg[c] = rd_nt(g + row * D + col);
+      if (w) rw[c] = rd(w + col);
+    }
+  }
   if (live) {
     mean = mean_in[row];
     rstd = rstd_in[row];
@@ -400,9 +444,9 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
     const int64_t col = (int64_t)(c * 64 + lane) * V;
     if (live && col < D) {
       float wv[V];
-      Vec<T>::load(x + row * D + col, xh[c]);
-      Vec<T>::load(g + row * D + col, gv[c]);
-      if (w) Vec<T>::load(w + col, wv);
+      Vec<T>::unpack(rx[c], xh[c]);
+      Vec<T>::unpack(rg[c], gv[c]);
+      if (w) Vec<T>::unpack(rw[c], wv);
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         xh[c][e] = (xh[c][e] - mean) * rstd;
@@ -423,13 +467,13 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
       const int64_t col = (int64_t)(c * 64 + lane) * V;
       if (col < D) {
         float wv[V], o[V];
-        if (w) Vec<T>::load(w + col, wv);
+        if (w) Vec<T>::unpack(rw[c], wv);
 #pragma unroll
         for (int e = 0; e < V; ++e) {
           const float gw = w ? gv[c][e] * wv[e] : gv[c][e];
           o[e] = rstd * (gw - s1 - xh[c][e] * s2);
         }
-        Vec<T>::store(dx + row * D + col, o);
+        wr_nt(dx + row * D + col, Vec<T>::pack(o));
       }
     }
   }
