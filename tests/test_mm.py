@@ -175,6 +175,23 @@ def test_tile_aligned_fast_path_layouts_and_bias(dt, ta, tb, m, k, n):
     assert oracle.rel_l2(f64(out), ref) <= (1e-2 if dt == torch.bfloat16 else 2e-3)
 
 
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,k,n", [(1024, 128, 1024), (512, 1088, 1024)])
+def test_small_tile_fast_path_layouts_and_bias(ta, tb, m, k, n):
+    """Tile-aligned problems too small for 128 x 256 tiles take the 64 x 64-tile direct-to-LDS kernel (the
+    second shape has a K step count that is not a multiple of the three-buffer ring)."""
+    dt = torch.bfloat16
+    a = randn((k, m) if ta else (m, k), dt, 23)
+    b = randn((n, k) if tb else (k, n), dt, 24)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), dt, 25)
+    out = torch.addmm(bias.to(dev), A, B, alpha=1.5, beta=0.5)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 1.5, 0.5)
+    check(out, ref, dt, k)
+    assert oracle.rel_l2(f64(out), ref) <= 1e-2
+
+
 def test_tile_aligned_fast_path_batched_and_full_bias():
     bt, m, k, n = 2, 1024, 128, 6144
     a, b = randn((bt, m, k), torch.bfloat16, 16), randn((bt, k, n), torch.bfloat16, 17)

@@ -280,8 +280,12 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 
 // ---- fast path: tile-aligned GEMMs, operands copied global -> LDS directly ------------------------------------
 //
-// C tile BM x BN (128 x 256 or 256 x 128) per workgroup of 8 wavefronts (two per SIMD); each wavefront owns
-// a 64 x 64 sub-tile as 2 x 2 v_mfma_f32_32x32x16 accumulators (64 registers).  K advances in steps of 64
+// C tile BM x BN per workgroup of (BM / WM) x (BN / WN) wavefronts; each wavefront owns a WM x WN sub-tile as
+// (WM / 32) x (WN / 32) v_mfma_f32_32x32x16 accumulators.  Shapes: 128 x 256 or 256 x 128 tiles of 64 x 64
+// sub-tiles (8 wavefronts, two per SIMD) for problems that fill the GPU with them, else 64 x 64 tiles of
+// 32 x 32 sub-tiles (4 wavefronts, several workgroups per CU), so that a 1024 x 1024 product still spreads
+// over 256 workgroups (measured faster than 128 x 128 tiles of 64 x 64 at 1024 x {1024, 2048, 8192} x N).
+// K advances in steps of 64
 // through a ring of three LDS buffers filled by global_load_lds_dwordx4 copies of the operands' raw rows:
 // the copies of step kt + 2 are spread over the MFMAs of step kt, so a copy has two steps to land (one step
 // of compute is shorter than the L2 latency plus the transfer of a 48 KiB step), one barrier per step.  An operand whose K axis is contiguous (A [M][K],
@@ -291,18 +295,21 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 // one rounding, transposed through LDS so that C is written as 16-byte row pieces.
 constexpr int GBK = 64;
 
-template <typename T, int BM, int BN, bool ATR, bool BTR>
-__global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int tiles_n) {
-  constexpr int NW = 8;
-  constexpr int WNN = BN / 64;  // wavefronts along n
-  static_assert((BM / 64) * WNN == NW, "eight 64 x 64 sub-tiles");
+template <typename T, int BM, int BN, int WM, int WN, bool ATR, bool BTR>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args p, int tiles_m, int tiles_n) {
+  constexpr int WNN = BN / WN;         // wavefronts along n
+  constexpr int NW = (BM / WM) * WNN;  // wavefronts
+  constexpr int FM = WM / 32, FN = WN / 32;  // 32 x 32 accumulators per wavefront along m, n
+  static_assert(BM % WM == 0 && BN % WN == 0 && WM % 32 == 0 && WN % 32 == 0 && NW >= 4, "tile shape");
   constexpr int A_ROWS = ATR ? GBK : BM, A_NCH = ATR ? BM / 8 : GBK / 8;
   constexpr int B_ROWS = BTR ? GBK : BN, B_NCH = BTR ? BN / 8 : GBK / 8;
   constexpr int A_ROWB = A_NCH * 16, B_ROWB = B_NCH * 16;
   constexpr int A_TILE = A_ROWS * A_ROWB, B_TILE = B_ROWS * B_ROWB;
   constexpr int IPA = A_ROWS * A_NCH / 64 / NW, IPB = B_ROWS * B_NCH / 64 / NW;  // copies per wavefront
+  static_assert(IPA >= 1 && IPB >= 1 && IPA * NW * 64 == A_ROWS * A_NCH && IPB * NW * 64 == B_ROWS * B_NCH &&
+                    IPA + IPB <= 16, "copy split");
   constexpr int RS = 40;                  // epilogue row stride (floats): conflict-free half-wave writes
-  constexpr int AREA = 64 * RS * 4;       // one wavefront's epilogue area (bytes)
+  constexpr int AREA = WM * RS * 4;       // one wavefront's epilogue area (bytes)
   constexpr int PA = A_TILE / AREA, PB = B_TILE / AREA;  // epilogue areas per A / B tile
   static_assert(2 * PA + 2 * PB >= NW, "epilogue areas fit the tiles");
   // separate LDS objects per buffer, so that reads of one are known not to alias copies into another
@@ -337,27 +344,30 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
   const int64_t astep = ATR ? (int64_t)GBK * p.a_sk * 2 : GBK * 2, bstep = BTR ? (int64_t)GBK * p.b_sk * 2 : GBK * 2;
   const DmaLanes alo = dma_lane_offsets<A_NCH>(ass, lane, wave * IPA), blo = dma_lane_offsets<B_NCH>(bss, lane, wave * IPB);
 
-  // fragment offsets inside a tile for m (n) sub-tile i (j) and 16-wide K slice kk
-  int aoff[2][4], boff[2][4];
+  // fragment offsets inside a tile for m (n) sub-tile i (j) and 16-wide K slice kk; a transposed operand
+  // uses two column reads per fragment (rows 16 kk + 8 h + 4 t + (s >> 2), t = 0, 1: entries kk = 0, 1)
+  int aoff[FM][4], boff[FN][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int i = 0; i < FM; ++i) {
       if constexpr (!ATR) {
-        aoff[i][kk] = tile_off<A_NCH>(wm * 64 + i * 32 + l32, 2 * kk + h);
-      } else {  // two column reads per fragment: rows 16 kk + 8 h + 4 t + (s >> 2), t = kk & 1 here; kk >> 1 unused
-        const int t = kk & 1;
-        const int col = wm * 64 + i * 32 + 16 * g2 + 4 * (s16 & 3);
-        aoff[i][kk] = kk < 2 ? tile_off<A_NCH>(8 * h + 4 * t + (s16 >> 2), col >> 3) + (s16 & 1) * 8 : 0;
-      }
-      if constexpr (!BTR) {
-        boff[i][kk] = tile_off<B_NCH>(wn * 64 + i * 32 + l32, 2 * kk + h);
+        aoff[i][kk] = tile_off<A_NCH>(wm * WM + i * 32 + l32, 2 * kk + h);
       } else {
-        const int t = kk & 1;
-        const int col = wn * 64 + i * 32 + 16 * g2 + 4 * (s16 & 3);
-        boff[i][kk] = kk < 2 ? tile_off<B_NCH>(8 * h + 4 * t + (s16 >> 2), col >> 3) + (s16 & 1) * 8 : 0;
+        const int col = wm * WM + i * 32 + 16 * g2 + 4 * (s16 & 3);
+        aoff[i][kk] = kk < 2 ? tile_off<A_NCH>(8 * h + 4 * (kk & 1) + (s16 >> 2), col >> 3) + (s16 & 1) * 8 : 0;
       }
     }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (!BTR) {
+        boff[j][kk] = tile_off<B_NCH>(wn * WN + j * 32 + l32, 2 * kk + h);
+      } else {
+        const int col = wn * WN + j * 32 + 16 * g2 + 4 * (s16 & 3);
+        boff[j][kk] = kk < 2 ? tile_off<B_NCH>(8 * h + 4 * (kk & 1) + (s16 >> 2), col >> 3) + (s16 & 1) * 8 : 0;
+      }
+    }
+  }
   auto afrag = [&](const HK_L uint8_t* At, int i, int kk) -> u32x4 {
     if constexpr (!ATR) {
       return *reinterpret_cast<const HK_L u32x4*>(At + aoff[i][kk]);
@@ -375,11 +385,11 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
     }
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+    for (int j = 0; j < FN; ++j) acc[i][j] = zero16();
 
   // steps 0 and 1 (step min(1, nk - 1): a single-step K re-copies step 0 into a buffer nobody reads)
 #pragma unroll
@@ -409,11 +419,15 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
     const HK_L uint8_t* Bt = bbuf(bc);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 a0 = afrag(At, 0, kk), a1 = afrag(At, 1, kk), b0 = bfrag(Bt, 0, kk), b1 = bfrag(Bt, 1, kk);
-      acc[0][0] = Mfma32<T>::mac(a0, b0, acc[0][0]);
-      acc[0][1] = Mfma32<T>::mac(a0, b1, acc[0][1]);
-      acc[1][0] = Mfma32<T>::mac(a1, b0, acc[1][0]);
-      acc[1][1] = Mfma32<T>::mac(a1, b1, acc[1][1]);
+      u32x4 af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = afrag(At, i, kk);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = bfrag(Bt, j, kk);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = Mfma32<T>::mac(af[i], bf[j], acc[i][j]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int c = kk * 4 + q;
@@ -434,7 +448,7 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
   if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
   __syncthreads();  // the last copies have landed before the epilogue reuses the tiles
 
-  // ---- epilogue: per n sub-tile j, the 64 x 32 fp32 block goes through this wavefront's area as [m][n]
+  // ---- epilogue: per n sub-tile j, the WM x 32 fp32 block goes through this wavefront's area as [m][n]
   float* const area = reinterpret_cast<float*>(wave < PA            ? a0_raw + wave * AREA
                                               : wave < 2 * PA        ? a1_raw + (wave - PA) * AREA
                                               : wave < 2 * PA + PB   ? b0_raw + (wave - 2 * PA) * AREA
@@ -443,16 +457,16 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
   const HK_G uint16_t* bias = gcptr<uint16_t>(p.bias) + bz * p.bias_sb;
   HK_G uint16_t* C = gptr<uint16_t>(p.c) + bz * p.c_sb;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t gn = n0 + wn * 64 + j * 32 + l32;
+  for (int j = 0; j < FN; ++j) {
+    const int64_t gn = n0 + wn * WN + j * 32 + l32;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < FM; ++i) {
       float bv[16];  // beta * bias, all 16 loads in flight together
       if (has_bias) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int r = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-          bv[e] = p.beta * T::to_f32(bias[(m0 + wm * 64 + r) * p.bias_sm + gn * p.bias_sn]);
+          bv[e] = p.beta * T::to_f32(bias[(m0 + wm * WM + r) * p.bias_sm + gn * p.bias_sn]);
         }
       } else {
 #pragma unroll
@@ -466,11 +480,11 @@ __global__ __launch_bounds__(512) void mm_dma(hrt_mm_args p, int tiles_m, int ti
     }
     // 4 lanes per 32-wide row, 8 floats each: 16 rows per pass
 #pragma unroll
-    for (int ps = 0; ps < 4; ++ps) {
+    for (int ps = 0; ps < WM / 16; ++ps) {
       const int r = ps * 16 + (lane >> 2), c8 = (lane & 3) * 8;
       const f32x4 x = *reinterpret_cast<const f32x4*>(area + r * RS + c8);
       const f32x4 y = *reinterpret_cast<const f32x4*>(area + r * RS + c8 + 4);
-      *reinterpret_cast<HK_G u32x4*>(C + (m0 + wm * 64 + r) * p.c_sm + n0 + wn * 64 + j * 32 + c8) =
+      *reinterpret_cast<HK_G u32x4*>(C + (m0 + wm * WM + r) * p.c_sm + n0 + wn * WN + j * 32 + c8) =
           u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
     }
   }
@@ -494,16 +508,16 @@ bool mm_dma_ok(const hrt_mm_args& a, int BM, int BN, bool& atr, bool& btr) {
   return (atr ? a.a_sk : a.a_sm) * 2 * (arows + 1) < lim && (btr ? a.b_sk : a.b_sn) * 2 * (brows + 1) < lim;
 }
 
-template <typename T, int BM, int BN>
+template <typename T, int BM, int BN, int WM, int WN>
 bool queue_dma(const hrt_mm_args& a, hipStream_t s) {
   bool atr = false, btr = false;
   if (!mm_dma_ok(a, BM, BN, atr, btr)) return false;
   const int tm = (int)(a.M / BM), tn = (int)(a.N / BN);
-  const dim3 g((uint32_t)((int64_t)tm * tn * a.batch));
-  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, false, false>), g, dim3(512), 0, s, a, tm, tn);
-  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, false, true>), g, dim3(512), 0, s, a, tm, tn);
-  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, true, false>), g, dim3(512), 0, s, a, tm, tn);
-  else hipLaunchKernelGGL((mm_dma<T, BM, BN, true, true>), g, dim3(512), 0, s, a, tm, tn);
+  const dim3 g((uint32_t)((int64_t)tm * tn * a.batch)), blk((BM / WM) * (BN / WN) * 64);
+  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false>), g, blk, 0, s, a, tm, tn);
+  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, true>), g, blk, 0, s, a, tm, tn);
+  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false>), g, blk, 0, s, a, tm, tn);
+  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, true>), g, blk, 0, s, a, tm, tn);
   return true;
 }
 
@@ -557,10 +571,12 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int64_t med = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
   const int64_t small = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
   if (small > 0x7fffffffLL) return ctx.fail("GEMM grid too large");
-  // fast path when the problem fills the GPU with 128 x 256 (or 256 x 128) tiles
-  if (a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256>(a, ctx.stream))
+  // fast path: the largest tile that still gives enough workgroups
+  if (a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256, 64, 64>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
-  if (a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128>(a, ctx.stream))
+  if (a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128, 64, 64>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
+  if (a.batch * (a.M / 64) * (a.N / 64) >= 128 && queue_dma<T, 64, 64, 32, 32>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (am == GATHER || bm == GATHER) {
     dispatch_gather<T>(a, am, bm, ctx.stream);
