@@ -83,13 +83,17 @@ typedef struct hrt_mm_args {
  *   y[m, n] = alpha * sum_k x[m, k] * deq(q)[n, k] + beta * bias[n]
  *   deq(q)[n, k] = round_dtype(float(q[n, k]) * float(scale[n, k / 64]))      (bit-exact dequant value)
  * x: [M, K] with strides (x_sm, x_sk); q: int8 [N, K] contiguous; scale: bf16 [N, nblocks] contiguous,
- * nblocks = ceil(K / 64); bias: [N] (if has_bias); y: [M, N] contiguous, dtype of x. */
+ * nblocks = ceil(K / 64); bias: [N] (if has_bias); y: [M, N] contiguous, dtype of x.
+ * ws (optional, 0 = none): 16-byte aligned workspace of N * K elements of x's dtype.  For large M (the
+ * weights would otherwise be converted once per 256-row block of x) the weights are dequantized into it
+ * once and the product runs on them; the values are the same either way. */
 typedef struct hrt_mm_dq8_args {
   uint64_t x, q, scale, bias, y;
   int64_t M, N, K, nblocks;
   int64_t x_sm, x_sk;
   float alpha, beta;
   uint32_t has_bias, flags;
+  uint64_t ws;
 } hrt_mm_dq8_args;
 
 /* Fused scaled-dot-product attention, non-causal, no mask, D <= 128 (vkrt/shaders/attn.comp.in:1-14,

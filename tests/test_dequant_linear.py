@@ -62,6 +62,28 @@ def test_dequant_linear_equals_dequant_then_mm():
     assert oracle.rel_l2(f64(fused), f64(unfused)) < 1e-3
 
 
+@pytest.mark.parametrize("M,N,K,per_channel,xt,bias", [(1024, 1024, 1088, False, False, True),
+                                                       (1024, 8192, 2048, True, False, False),
+                                                       (512, 1024, 512, False, True, True),
+                                                       (2048, 8192, 1024, True, False, True)])
+def test_fast_path_bit_identical_to_dequant_then_mm(M, N, K, per_channel, xt, bias):
+    """Tile-aligned shapes take the direct-to-LDS GEMM with the dequant done in LDS (or, from M = 2048, a
+    dequant pass into a workspace followed by the GEMM); the unfused dequant_int8 + mm accumulates every
+    output element in the same order on the same dequantized weights, so the outputs must be bit-identical
+    (per-block scales, 17 K steps, x given transposed, the workspace path)."""
+    q, s = weights(N, K, 31 + K, per_channel)
+    x = randn((K, M) if xt else (M, K), torch.bfloat16, 8)
+    X = x.to(dev).t() if xt else x.to(dev)
+    b = randn((N,), torch.bfloat16, 9).to(dev) if bias else None
+    fused = torch_vulkan.dequant_int8_linear(X, q.to(dev), s.to(dev), b)
+    w = torch_vulkan.dequant_int8(q.to(dev), s.to(dev), torch.bfloat16)
+    unfused = torch.addmm(b, X, w.t()) if bias else torch.mm(X, w.t())
+    assert torch.equal(fused.cpu(), unfused.cpu())
+    rows = slice(0, 64)
+    ref = oracle.gemm(f64(x.t() if xt else x)[rows], deq64(q, s).T, f64(b) if bias else None, 1.0, 1.0 if bias else 0.0)
+    check(fused[rows], ref, K)
+
+
 def test_dequant_linear_3d_input_and_f16():
     q, s = weights(128, 256, 11)
     x = randn((2, 5, 256), torch.float16, 6)

@@ -14,6 +14,9 @@
 //   * odd shapes / strides / alignments use a per-element gather loader on the same MMA core;
 //   * tiles are numbered N-fastest so the default round-robin placement of workgroups over the 8 XCDs
 //     gives each XCD a band of N-panels that it reads once into its own L2.
+#include <cstring>
+#include <type_traits>
+
 #include "../hrt/registry.h"
 #include "lds_stage.h"
 
@@ -293,10 +296,20 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 // M or N (A given as [K][M], B as [K][N]) is staged as [k][row] and read with ds_read_b64_tr_b16 column
 // reads, so all four layouts need no register transposes.  Epilogue: alpha * acc + beta * bias in fp32,
 // one rounding, transposed through LDS so that C is written as 16-byte row pieces.
+//
+// DQ8 (the fused int8 linear y = x deq(q)^T + bias): B is int8 q [N][K] with one bf16 scale per row and
+// 64-column block, so a K step covers exactly one scale block.  The raw int8 rows of step kt + 3 are copied
+// global -> LDS during step kt (a ring of three int8 tiles: a copy still has two steps to land before it
+// is converted); during step kt every thread converts one 16-byte int8 chunk (or more) of step kt + 1's
+// tile to deq = round(float(q) * float(scale)) in the input dtype (the exact product, one RNE rounding,
+// as the standalone dequant) and writes it into the swizzled B tile of step kt + 1 (two such tiles), which
+// the MFMAs then read exactly as a copied B tile.  The step barrier also waits for these LDS writes.
 constexpr int GBK = 64;
 
-template <typename T, int BM, int BN, int WM, int WN, bool ATR, bool BTR>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args p, int tiles_m, int tiles_n) {
+template <typename T, int BM, int BN, int WM, int WN, bool ATR, bool BTR, bool DQ8>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args p, int tiles_m, int tiles_n,
+                                                                   uint64_t dq_scale, int64_t dq_nblocks) {
+  static_assert(!DQ8 || !BTR, "int8 B is staged as [n][k] rows");
   constexpr int WNN = BN / WN;         // wavefronts along n
   constexpr int NW = (BM / WM) * WNN;  // wavefronts
   constexpr int FM = WM / 32, FN = WN / 32;  // 32 x 32 accumulators per wavefront along m, n
@@ -312,9 +325,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   constexpr int AREA = WM * RS * 4;       // one wavefront's epilogue area (bytes)
   constexpr int PA = A_TILE / AREA, PB = B_TILE / AREA;  // epilogue areas per A / B tile
   static_assert(2 * PA + 2 * PB >= NW, "epilogue areas fit the tiles");
+  // DQ8: int8 tiles of BN rows x 64 bytes (4 chunks, unswizzled), chunks converted per thread per step
+  constexpr int Q_TILE = DQ8 ? BN * GBK : 16, IPQ = DQ8 ? BN * 4 / 64 / NW : 1, CPT = DQ8 ? BN * 4 / (NW * 64) : 1;
+  static_assert(!DQ8 || (IPQ >= 1 && IPA + IPQ <= 16 && CPT * NW * 64 == BN * 4), "int8 copy split");
   // separate LDS objects per buffer, so that reads of one are known not to alias copies into another
   __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], a2_raw[A_TILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t b0_raw[B_TILE], b1_raw[B_TILE], b2_raw[B_TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t b0_raw[B_TILE], b1_raw[B_TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t b2_raw[DQ8 ? Q_TILE : B_TILE];  // DQ8: int8 tile 0
+  __shared__ __attribute__((aligned(DQ8 ? 1024 : 16))) uint8_t q1_raw[Q_TILE], q2_raw[Q_TILE];
   HK_L uint8_t* const A0 = (HK_L uint8_t*)a0_raw;
   HK_L uint8_t* const A1 = (HK_L uint8_t*)a1_raw;
   HK_L uint8_t* const A2 = (HK_L uint8_t*)a2_raw;
@@ -323,6 +341,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   HK_L uint8_t* const B2 = (HK_L uint8_t*)b2_raw;
   auto abuf = [&](auto ic) { constexpr int I = decltype(ic)::value; return I == 0 ? A0 : I == 1 ? A1 : A2; };
   auto bbuf = [&](auto ic) { constexpr int I = decltype(ic)::value; return I == 0 ? B0 : I == 1 ? B1 : B2; };
+  HK_L uint8_t* const Q0 = (HK_L uint8_t*)b2_raw;
+  HK_L uint8_t* const Q1 = (HK_L uint8_t*)q1_raw;
+  HK_L uint8_t* const Q2 = (HK_L uint8_t*)q2_raw;
+  auto qbuf = [&](auto ic) { constexpr int I = decltype(ic)::value; return I == 0 ? Q0 : I == 1 ? Q1 : Q2; };
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -338,11 +360,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   // copy sources (bytes) of K step 0 and the per-step advance
   const HK_G uint8_t* Ab = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.a) + bz * p.a_sb +
                                                                  (ATR ? m0 : m0 * p.a_sm));
-  const HK_G uint8_t* Bb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.b) + bz * p.b_sb +
-                                                                 (BTR ? n0 : n0 * p.b_sn));
-  const uint32_t ass = (uint32_t)((ATR ? p.a_sk : p.a_sm) * 2), bss = (uint32_t)((BTR ? p.b_sk : p.b_sn) * 2);
-  const int64_t astep = ATR ? (int64_t)GBK * p.a_sk * 2 : GBK * 2, bstep = BTR ? (int64_t)GBK * p.b_sk * 2 : GBK * 2;
-  const DmaLanes alo = dma_lane_offsets<A_NCH>(ass, lane, wave * IPA), blo = dma_lane_offsets<B_NCH>(bss, lane, wave * IPB);
+  // (DQ8: B = q, strides in bytes, one byte per element)
+  constexpr int BEL = DQ8 ? 1 : 2;
+  const HK_G uint8_t* Bb = DQ8 ? gcptr<uint8_t>(p.b) + n0 * p.b_sn
+                               : reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.b) + bz * p.b_sb +
+                                                                       (BTR ? n0 : n0 * p.b_sn));
+  const uint32_t ass = (uint32_t)((ATR ? p.a_sk : p.a_sm) * 2), bss = (uint32_t)((BTR ? p.b_sk : p.b_sn) * BEL);
+  const int64_t astep = ATR ? (int64_t)GBK * p.a_sk * 2 : GBK * 2;
+  const int64_t bstep = BTR ? (int64_t)GBK * p.b_sk * BEL : GBK * BEL;
+  const DmaLanes alo = dma_lane_offsets<A_NCH>(ass, lane, wave * IPA);
+  const DmaLanes blo = DQ8 ? dma_lane_offsets<4>(bss, lane, wave * IPQ) : dma_lane_offsets<B_NCH>(bss, lane, wave * IPB);
 
   // fragment offsets inside a tile for m (n) sub-tile i (j) and 16-wide K slice kk; a transposed operand
   // uses two column reads per fragment (rows 16 kk + 8 h + 4 t + (s >> 2), t = 0, 1: entries kk = 0, 1)
@@ -391,32 +418,89 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = zero16();
 
-  // steps 0 and 1 (step min(1, nk - 1): a single-step K re-copies step 0 into a buffer nobody reads)
+  // DQ8 conversion: chunk u of this thread in the int8 tile of K step ks (buffer Qt) -> B tile Bt
+  const HK_G uint16_t* scl = gcptr<uint16_t>(dq_scale) + (DQ8 ? n0 * dq_nblocks : 0);
+  auto dq_scales = [&](int ks, float* sv) {
 #pragma unroll
-  for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
+    for (int u = 0; u < CPT; ++u) {
+      const int row = (u * NW * 64 + (int)threadIdx.x) >> 2;
+      sv[u] = bf16_bits_to_f32(scl[row * dq_nblocks + ks]);
+    }
+  };
+  auto dq_convert = [&](const HK_L uint8_t* Qt, HK_L uint8_t* Bt, const float* sv) {
 #pragma unroll
-  for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
-  const int k1 = nk > 1 ? 1 : 0;
-  issue_order_fence();
+    for (int u = 0; u < CPT; ++u) {
+      const int c = u * NW * 64 + (int)threadIdx.x, row = c >> 2, q16 = c & 3;
+      const u32x4 w = *reinterpret_cast<const HK_L u32x4*>(Qt + c * 16);
+      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+      float v[16];
 #pragma unroll
-  for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab + k1 * astep, ass, A1, wave, alo, c);
+      for (int i = 0; i < 16; ++i) v[i] = (float)(int8_t)((wv[i >> 2] >> (8 * (i & 3))) & 0xffu) * sv[u];
+      *reinterpret_cast<HK_L u32x4*>(Bt + tile_off<B_NCH>(row, 2 * q16)) =
+          u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
+      *reinterpret_cast<HK_L u32x4*>(Bt + tile_off<B_NCH>(row, 2 * q16 + 1)) =
+          u32x4{pack2<T>(v[8], v[9]), pack2<T>(v[10], v[11]), pack2<T>(v[12], v[13]), pack2<T>(v[14], v[15])};
+    }
+  };
+  const int k1 = nk > 1 ? 1 : 0, k2 = nk > 2 ? 2 : nk - 1;
+  float svq[CPT];  // DQ8: scales of the int8 tile that the next step converts (loaded a step ahead)
+  if constexpr (!DQ8) {
+    // steps 0 and 1 (step min(1, nk - 1): a single-step K re-copies step 0 into a buffer nobody reads)
 #pragma unroll
-  for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb + k1 * bstep, bss, B1, wave, blo, c);
-  barrier_keep_vm<IPA + IPB>();  // step 0 landed everywhere, step 1 in flight
+    for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
+#pragma unroll
+    for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
+    issue_order_fence();
+#pragma unroll
+    for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab + k1 * astep, ass, A1, wave, alo, c);
+#pragma unroll
+    for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb + k1 * bstep, bss, B1, wave, blo, c);
+    barrier_keep_vm<IPA + IPB>();  // step 0 landed everywhere, step 1 in flight
+  } else {
+    // int8 steps 0, 1, 2 and A steps 0, 1; step 0's int8 tile converted before the loop
+    float sv[CPT];
+    dq_scales(0, sv);
+#pragma unroll
+    for (int c = 0; c < IPQ; ++c) dma_tile_part<4, BN, NW>(Bb, bss, Q0, wave, blo, c);
+#pragma unroll
+    for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
+    issue_order_fence();
+#pragma unroll
+    for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab + k1 * astep, ass, A1, wave, alo, c);
+#pragma unroll
+    for (int c = 0; c < IPQ; ++c) dma_tile_part<4, BN, NW>(Bb + k1 * bstep, bss, Q1, wave, blo, c);
+#pragma unroll
+    for (int c = 0; c < IPQ; ++c) dma_tile_part<4, BN, NW>(Bb + k2 * bstep, bss, Q2, wave, blo, c);
+    barrier_keep_vm<IPA + 2 * IPQ>();  // int8 step 0 and A step 0 landed everywhere
+    dq_scales(k1, svq);
+    dq_convert(Q0, B0, sv);
+    __syncthreads();  // B tile 0 written; the other copies landed
+  }
 
   // K step kt: MFMAs from buffer kt % 3, copies of step min(kt + 2, nk - 1) into buffer (kt + 2) % 3 (read
   // by step kt - 1, whose readers all passed the previous barrier) placed after the first MFMAs; steps
   // past the end re-copy the last step into a buffer nobody reads again.  Before the barrier that ends
   // the step each wavefront waits for its copies of the previous step only, so step kt + 1's buffer is
-  // complete after the barrier while the copies of step kt + 2 stay in flight.
-  auto step = [&](auto bc, int kt) {
+  // complete after the barrier while the copies of step kt + 2 stay in flight.  DQ8: B tiles alternate
+  // (kt % 2), int8 step min(kt + 3, nk - 1) is copied into int8 buffer kt % 3 (converted during step
+  // kt - 1) and int8 step kt + 1 (buffer (kt + 1) % 3, landed at the last barrier) is converted into B
+  // tile (kt + 1) % 2 (last read in step kt - 1); steps past the end convert a repeat nobody reads.
+  auto step = [&](auto bc, auto bq, int kt) {
     constexpr int BUF = decltype(bc)::value;
     constexpr int NXT = (BUF + 2) % 3;
+    constexpr int BB = decltype(bq)::value;  // DQ8: B tile kt % 2
     const int kn = kt + 2 < nk ? kt + 2 : nk - 1;
     const HK_G uint8_t* an = Ab + kn * astep;
-    const HK_G uint8_t* bn = Bb + kn * bstep;
     const HK_L uint8_t* At = abuf(bc);
-    const HK_L uint8_t* Bt = bbuf(bc);
+    const HK_L uint8_t* Bt = DQ8 ? bbuf(bq) : bbuf(bc);
+    const int kq = DQ8 ? (kt + 3 < nk ? kt + 3 : nk - 1) : kn;
+    const HK_G uint8_t* bn = Bb + kq * bstep;
+    float sv[CPT];
+    if constexpr (DQ8) {
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) sv[u] = svq[u];
+      dq_scales(kt + 2 < nk ? kt + 2 : nk - 1, svq);
+    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       u32x4 af[FM], bf[FN];
@@ -431,21 +515,51 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int c = kk * 4 + q;
-        if (c < IPA) dma_tile_part<A_NCH, A_ROWS, NW>(an, ass, abuf(std::integral_constant<int, NXT>()), wave, alo, c);
-        else if (c < IPA + IPB)
-          dma_tile_part<B_NCH, B_ROWS, NW>(bn, bss, bbuf(std::integral_constant<int, NXT>()), wave, blo, c - IPA);
+        if (c < IPA) {
+          dma_tile_part<A_NCH, A_ROWS, NW>(an, ass, abuf(std::integral_constant<int, NXT>()), wave, alo, c);
+        } else if constexpr (!DQ8) {
+          if (c < IPA + IPB)
+            dma_tile_part<B_NCH, B_ROWS, NW>(bn, bss, bbuf(std::integral_constant<int, NXT>()), wave, blo, c - IPA);
+        } else {
+          if (c < IPA + IPQ) dma_tile_part<4, BN, NW>(bn, bss, qbuf(std::integral_constant<int, BUF>()), wave, blo, c - IPA);
+        }
+      }
+      if constexpr (DQ8) {
+        if (kk == 1) dq_convert(qbuf(std::integral_constant<int, (BUF + 1) % 3>()), bbuf(std::integral_constant<int, BB ^ 1>()), sv);
       }
     }
-    barrier_keep_vm<IPA + IPB>();
+    if constexpr (DQ8) barrier_keep_vm_lds<IPA + IPQ>();
+    else barrier_keep_vm<IPA + IPB>();
   };
-  int kt = 0;
-  for (; kt + 3 <= nk; kt += 3) {
-    step(std::integral_constant<int, 0>(), kt);
-    step(std::integral_constant<int, 1>(), kt + 1);
-    step(std::integral_constant<int, 2>(), kt + 2);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  if constexpr (!DQ8) {
+    int kt = 0;
+    for (; kt + 3 <= nk; kt += 3) {
+      step(I0(), I0(), kt);
+      step(I1(), I0(), kt + 1);
+      step(I2(), I0(), kt + 2);
+    }
+    if (kt < nk) step(I0(), I0(), kt);
+    if (kt + 1 < nk) step(I1(), I0(), kt + 1);
+  } else {
+    // A and int8 buffers rotate by 3, B tiles by 2: blocks of 6 steps, leaving after any step
+    for (int kt = 0;; kt += 6) {
+      step(I0(), I0(), kt);
+      if (kt + 1 >= nk) break;
+      step(I1(), I1(), kt + 1);
+      if (kt + 2 >= nk) break;
+      step(I2(), I0(), kt + 2);
+      if (kt + 3 >= nk) break;
+      step(I0(), I1(), kt + 3);
+      if (kt + 4 >= nk) break;
+      step(I1(), I0(), kt + 4);
+      if (kt + 5 >= nk) break;
+      step(I2(), I1(), kt + 5);
+      if (kt + 6 >= nk) break;
+    }
   }
-  if (kt < nk) step(std::integral_constant<int, 0>(), kt);
-  if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
   __syncthreads();  // the last copies have landed before the epilogue reuses the tiles
 
   // ---- epilogue: per n sub-tile j, the WM x 32 fp32 block goes through this wavefront's area as [m][n]
@@ -514,10 +628,30 @@ bool queue_dma(const hrt_mm_args& a, hipStream_t s) {
   if (!mm_dma_ok(a, BM, BN, atr, btr)) return false;
   const int tm = (int)(a.M / BM), tn = (int)(a.N / BN);
   const dim3 g((uint32_t)((int64_t)tm * tn * a.batch)), blk((BM / WM) * (BN / WN) * 64);
-  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false>), g, blk, 0, s, a, tm, tn);
-  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, true>), g, blk, 0, s, a, tm, tn);
-  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false>), g, blk, 0, s, a, tm, tn);
-  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, true>), g, blk, 0, s, a, tm, tn);
+  const uint64_t ns = 0;
+  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false, false>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, true, false>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false, false>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, true, false>), g, blk, 0, s, a, tm, tn, ns, 0);
+  return true;
+}
+
+// The fused int8 linear on the fast path: y = alpha x deq(q)^T + beta bias as the GEMM A = x [M][K] (either
+// layout), B = q read as [N][K] int8 rows with the per-64 scales, C = y [M][N].
+template <typename T, int BM, int BN, int WM, int WN>
+bool queue_dma_dq8(const hrt_mm_dq8_args& d, hipStream_t s) {
+  if (d.K % GBK || d.q % 16 || d.scale % 2) return false;
+  hrt_mm_args a{};
+  a.a = d.x, a.b = d.q, a.c = d.y, a.bias = d.bias;
+  a.M = d.M, a.N = d.N, a.K = d.K, a.batch = 1;
+  a.a_sm = d.x_sm, a.a_sk = d.x_sk, a.b_sk = 1, a.b_sn = d.K, a.c_sm = d.N, a.c_sn = 1, a.bias_sn = 1;
+  a.alpha = d.alpha, a.beta = d.beta, a.has_bias = d.has_bias;
+  bool atr = false, btr = false;
+  if (!mm_dma_ok(a, BM, BN, atr, btr) || btr) return false;
+  const int tm = (int)(a.M / BM), tn = (int)(a.N / BN);
+  const dim3 g((uint32_t)((int64_t)tm * tn)), blk((BM / WM) * (BN / WN) * 64);
+  if (!atr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false, true>), g, blk, 0, s, a, tm, tn, d.scale, d.nblocks);
+  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false, true>), g, blk, 0, s, a, tm, tn, d.scale, d.nblocks);
   return true;
 }
 
@@ -596,6 +730,11 @@ void queue_dq8(const hrt_mm_dq8_args& a, hipStream_t s) {
   hipLaunchKernelGGL((mm_dq8_mfma<T, BM, BN, 2, 2, AM>), dim3((uint32_t)(tm * tn)), dim3(256), 0, s, a, tm, tn);
 }
 
+// Smallest M at which the fused int8 linear dequantizes into the caller's workspace first: the fused kernel
+// converts every weight once per 256-row block of x, which costs more than one standalone dequant pass
+// beyond a few blocks (M = 4096: 222 us fused vs ~157 us dequant + GEMM for 8192 x 2048 weights).
+constexpr int64_t kDq8WsMinM = 2048;
+
 template <typename T>
 bool launch_mm_dq8(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_mm_dq8_args*>(pp);
@@ -608,6 +747,34 @@ bool launch_mm_dq8(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
       !ctx.check(a.scale, (uint64_t)(a.N * a.nblocks) * 2, "scale") || !ctx.check(a.y, (uint64_t)(a.M * a.N) * 2, "y") ||
       (a.has_bias && !ctx.check(a.bias, (uint64_t)a.N * 2, "bias")))
     return false;
+  // large M with a workspace: dequantize once (the dq8 kernel), then the fast GEMM on the bf16 / f16 weights
+  if (a.ws && a.M >= kDq8WsMinM && a.K % GBK == 0 && a.ws % 16 == 0) {
+    hrt_mm_args m{};
+    m.a = a.x, m.b = a.ws, m.c = a.y, m.bias = a.bias;
+    m.M = a.M, m.N = a.N, m.K = a.K, m.batch = 1;
+    m.a_sm = a.x_sm, m.a_sk = a.x_sk, m.b_sk = 1, m.b_sn = a.K, m.c_sm = a.N, m.c_sn = 1, m.bias_sn = 1;
+    m.alpha = a.alpha, m.beta = a.beta, m.has_bias = a.has_bias;
+    bool atr = false, btr = false;
+    if (mm_dma_ok(m, 128, 256, atr, btr) && (a.M / 128) * (a.N / 256) >= 192) {
+      if (!ctx.check(a.ws, (uint64_t)(a.N * a.K) * 2, "ws")) return false;
+      hrt_dq8_args d{};
+      d.q = a.q, d.scale = a.scale, d.out = a.ws, d.rows = a.N, d.cols = a.K, d.nblocks = a.nblocks;
+      const char* dq = sizeof(typename T::storage) == 2 && std::is_same<T, BF16>::value ? "dq8_bf16" : "dq8_f16";
+      for (auto& e : hrt::kernel_table())
+        if (!strcmp(e.name, dq)) {
+          if (!e.launch(&d, nullptr, ctx)) return false;
+          if (queue_dma<T, 128, 256, 64, 64>(m, ctx.stream)) return hrt::launch_ok(hipGetLastError(), ctx, "mm_dq8_ws");
+        }
+      return ctx.fail("mm_dq8: workspace path unavailable");
+    }
+  }
+  // fast path (tile-aligned, K % 64 == 0): dequant fused into the direct-to-LDS GEMM
+  if ((a.M / 256) * (a.N / 128) >= 192 && queue_dma_dq8<T, 256, 128, 64, 64>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dq8_dma");
+  if ((a.M / 128) * (a.N / 256) >= 192 && queue_dma_dq8<T, 128, 256, 64, 64>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dq8_dma");
+  if ((a.M / 64) * (a.N / 64) >= 128 && queue_dma_dq8<T, 64, 64, 32, 32>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dq8_dma");
   const int am = pick_mode(a.x, 0, a.x_sm, a.x_sk, a.M, a.K, 1);
   const int64_t big = cdiv(a.M, 128) * cdiv(a.N, 256);
   if (big >= 240) {

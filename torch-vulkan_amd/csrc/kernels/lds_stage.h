@@ -69,6 +69,11 @@ template <>
 __device__ __forceinline__ int tile_swz<32>(int row) {
   return (row & 3) << 2;
 }
+// NCH = 4 (64-byte rows of int8 staging tiles, read linearly): no swizzle.
+template <>
+__device__ __forceinline__ int tile_swz<4>(int) {
+  return 0;
+}
 // Rows after which tile_swz repeats.
 template <int NCH>
 constexpr int swz_period_rows() {
@@ -199,6 +204,15 @@ template <int N>
 __device__ __forceinline__ void barrier_keep_vm() {
   static_assert(N >= 0 && N < 64, "the vmcnt field holds 0..63");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// The same, also waiting for this wavefront's LDS accesses (for stages that write LDS with ds_write before
+// the barrier that publishes them).
+template <int N>
+__device__ __forceinline__ void barrier_keep_vm_lds() {
+  static_assert(N >= 0 && N < 64, "the vmcnt field holds 0..63");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
   asm volatile("s_barrier" ::: "memory");
 }
 

@@ -51,6 +51,11 @@ at::Tensor dequant_int8_linear_vk(const at::Tensor& x, const at::Tensor& q, cons
   A.x_sk = x2.stride(1);
   A.alpha = 1.f;
   A.beta = 1.f;
+  at::Tensor ws;  // large M: the weights are dequantized once into this workspace (same values)
+  if (M >= 2048) {
+    ws = at::empty({N, K}, x.options());
+    A.ws = addr_of(ws);
+  }
   if (bias.has_value() && bias->defined()) {
     TORCH_CHECK(is_vk(*bias) && bias->scalar_type() == x.scalar_type() && bias->numel() == N && bias->is_contiguous(),
                 "dequant_int8_linear: bias must be a contiguous vk tensor of N elements in x's dtype");

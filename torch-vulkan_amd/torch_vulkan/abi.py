@@ -43,7 +43,7 @@ class MmArgs(ctypes.Structure):
 class MmDq8Args(ctypes.Structure):
     _fields_ = [("x", u64), ("q", u64), ("scale", u64), ("bias", u64), ("y", u64), ("M", i64), ("N", i64), ("K", i64),
                 ("nblocks", i64), ("x_sm", i64), ("x_sk", i64), ("alpha", f32), ("beta", f32), ("has_bias", u32),
-                ("flags", u32)]
+                ("flags", u32), ("ws", u64)]
 
 
 class AttnArgs(ctypes.Structure):
