@@ -14,7 +14,8 @@ step time, and the CPU baseline: the oracle's float64 restatement of the same fw
 (plus, for reference, torch's CPU aten SDPA, which is what the reference runs on CPU).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--skip-cpu] [--only-attn]
-       python bench.py --profile {fwd,dq,dkdv,copy} [--steps K]   (launches only that kernel, for rocprofv3)
+       python bench.py --profile {fwd,dq,dkdv,copy,gemm,gemm1024,dq8,softmax,ln,dequant} [--steps K]
+                                                                   (launches only that workload, for rocprofv3)
        python bench.py --pmc-summary DIR [DIR ...]                 (per-kernel counters of rocprofv3 --pmc runs)
 """
 
@@ -41,7 +42,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
-    ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy"], help="launch one kernel --steps times")
+    ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy", "gemm", "gemm1024", "dq8", "softmax", "ln", "dequant"],
+                    help="launch one kernel (or one benchmark workload) --steps times, untimed")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR", help="summarise rocprofv3 --pmc output directories")
     return ap.parse_args()
 
@@ -77,7 +79,7 @@ def pmc_summary(dirs):
                 name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
                 agg.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
     avg = {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in agg.items()}
-    copy = next((cs for k, cs in avg.items() if "copyBuffer" in k or "ew_copy" in k), {})
+    copy = next((cs for k, cs in avg.items() if "ew_copy" in k or "copy_nd" in k), {})
     known_kib = 64 * 1024.0
     scale = {c: known_kib / copy[c] for c in ("FETCH_SIZE", "WRITE_SIZE") if copy.get(c)}
     for k, cs in sorted(avg.items()):
@@ -104,6 +106,7 @@ class Bench:
         self.rt = abi.Runtime()
         self.dev = torch.device("vk")
         self.args = args
+        self.profile_n = 0  # > 0: time_graph only enqueues that many calls (rocprofv3 runs)
 
     # ---- helpers --------------------------------------------------------------------------------------
     def randn(self, shape, dtype, seed, scale=1.0):
@@ -114,6 +117,11 @@ class Bench:
         """Average GPU time of one enqueue() call: a graph of `reps` calls, replayed `launches` times
         between two events on the runtime stream (after one untimed replay)."""
         rt = self.rt
+        if self.profile_n:
+            for i in range(self.profile_n):
+                enqueue(i)
+            rt.synchronize()
+            return 1.0
         gid = rt.graph(lambda: [enqueue(i) for i in range(reps)])
         try:
             rt.graph_launch(gid)
@@ -363,11 +371,22 @@ class Bench:
         """Launch one kernel of the headline step (or a 64 MiB device copy) n times and return: the workload
         that rocprofv3 --kernel-trace / --pmc runs wrap."""
         torch = self.torch
-        if which == "copy":
+        workloads = {"gemm": lambda: self.gemm(1024, 2048, 8192, "nt"), "gemm1024": lambda: self.gemm(1024, 1024, 1024, "nn", True),
+                     "dq8": lambda: self.dq8_linear(1024), "softmax": self.softmax, "ln": self.layer_norm,
+                     "dequant": self.dequant}
+        if which in workloads:
+            self.profile_n = n
+            workloads[which]()
+            self.profile_n = 0
+        elif which == "copy":  # the runtime's own ew_copy kernel over 64 MiB: the counters' calibration
+            abi = self.abi
             src = torch.empty(16 * 1024 * 1024, dtype=torch.float32, device=self.dev).fill_(1.0)
             dst = torch.empty_like(src)
+            a = abi.CopyArgs()
+            a.dst, a.src, a.ndim, a.dst_dtype, a.src_dtype = dst.data_ptr(), src.data_ptr(), 1, 0, 0
+            a.sizes[0], a.dst_strides[0], a.src_strides[0] = src.numel(), 1, 1
             for _ in range(n):
-                dst.copy_(src)
+                self.rt.dispatch("ew_copy", a)
         else:
             step, kernels, keep, _ = self.attn_setup(1, 16, 1024, 128)
             step()  # fwd, dQ (+delta), dK/dV once so that every input of the profiled kernel is valid

@@ -632,6 +632,7 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   constexpr int ROWB = NCH * 16;
   constexpr int TILE = QST * ROWB;   // bytes per Q or dO stage
   constexpr int NDT = DCH * 2;       // 16-wide d tiles
+  constexpr int SW = NCH == 16 ? 1 : 0;  // the 16x16x32 tile layout (conflict-free reads, lds_stage.h)
   __shared__ __attribute__((aligned(1024))) uint8_t q0_raw[TILE], q1_raw[TILE], o0_raw[TILE], o1_raw[TILE];
   HK_L uint8_t* const Q0 = (HK_L uint8_t*)q0_raw;
   HK_L uint8_t* const Q1 = (HK_L uint8_t*)q1_raw;
@@ -652,9 +653,9 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   const int nst = (Sq + QST - 1) / QST;
 
   const int j0 = wave * (QST * NCH / 64 / NW);
-  const DmaLanes qlo = dma_lane_offsets<NCH>(qss, lane, j0), olo = dma_lane_offsets<NCH>(oss, lane, j0);
-  dma_tile<NCH, QST, NW>(Qb, qss, Sq, Q0, wave, lane, qlo);
-  dma_tile<NCH, QST, NW>(Ob, oss, Sq, O0, wave, lane, olo);
+  const DmaLanes qlo = dma_lane_offsets<NCH, SW>(qss, lane, j0), olo = dma_lane_offsets<NCH, SW>(oss, lane, j0);
+  dma_tile<NCH, QST, NW, SW>(Qb, qss, Sq, Q0, wave, lane, qlo);
+  dma_tile<NCH, QST, NW, SW>(Ob, oss, Sq, O0, wave, lane, olo);
 
   // this lane's key (column l16 of the 16x16 tiles): K and V as B fragments, d = 32 ks + 8 g + i
   const int64_t key = kb * 64 + kg * 16 + l16;
@@ -703,10 +704,10 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   // columns 16 dt + 4 (l16 & 3))
   int roff[DCH], coff[NDT];
 #pragma unroll
-  for (int ks = 0; ks < DCH; ++ks) roff[ks] = tile_off<NCH>(qh * 32 + l16, 4 * ks + g4);
+  for (int ks = 0; ks < DCH; ++ks) roff[ks] = tile_off<NCH, SW>(qh * 32 + l16, 4 * ks + g4);
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
-    coff[dt] = tile_off<NCH>(qh * 32 + 4 * g4 + (l16 >> 2), 2 * dt + ((l16 >> 1) & 1)) + (l16 & 1) * 8;
+    coff[dt] = tile_off<NCH, SW>(qh * 32 + 4 * g4 + (l16 >> 2), 2 * dt + ((l16 >> 1) & 1)) + (l16 & 1) * 8;
 
   f32x4 dk[NDT], dv[NDT];
 #pragma unroll

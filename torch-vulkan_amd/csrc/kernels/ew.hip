@@ -118,6 +118,13 @@ __global__ __launch_bounds__(256) void cast_1d(void* dst, const void* src, int64
   }
 }
 
+// Contiguous same-type copy of 16-byte chunks: one chunk per thread, streaming loads and stores (one
+// chunk per thread over many workgroups measured fastest on MI355X: 6.5 TB/s for a 512 MiB copy).
+__global__ __launch_bounds__(256) void ew_copy_vec16(u32x4* __restrict__ dst, const u32x4* __restrict__ src, int64_t n16) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 template <typename S>
 __global__ __launch_bounds__(256) void raw_nd(void* dst, const void* src, Shape sh, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -201,6 +208,10 @@ bool launch_copy(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
       case HRT_F16 * 3 + HRT_BF16: queue_cast<HRT_F16, HRT_BF16>(a, sh, n, contig, s); break;
       default: return ctx.fail("unsupported cast");
     }
+  } else if (contig && (n * de) % 16 == 0 && a.dst % 16 == 0 && a.src % 16 == 0 && (n * de) / 16 < ((int64_t)1 << 39)) {
+    const int64_t n16 = (int64_t)(n * de) / 16;
+    hipLaunchKernelGGL(ew_copy_vec16, dim3((uint32_t)((n16 + 255) / 256)), dim3(256), 0, s, (u32x4*)a.dst,
+                       (const u32x4*)a.src, n16);
   } else {
     dim3 g(grid_for(n, 1));
     switch (de) {

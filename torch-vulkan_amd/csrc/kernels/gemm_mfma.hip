@@ -300,8 +300,8 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 // DQ8 (the fused int8 linear y = x deq(q)^T + bias): B is int8 q [N][K] with one bf16 scale per row and
 // 64-column block, so a K step covers exactly one scale block.  The raw int8 rows of step kt + 3 are copied
 // global -> LDS during step kt (a ring of three int8 tiles: a copy still has two steps to land before it
-// is converted); during step kt every thread converts one 16-byte int8 chunk (or more) of step kt + 1's
-// tile to deq = round(float(q) * float(scale)) in the input dtype (the exact product, one RNE rounding,
+// is converted); during step kt every thread converts 8-element pieces of step kt + 1's tile to
+// deq = round(float(q) * float(scale)) in the input dtype (the exact product, one RNE rounding,
 // as the standalone dequant) and writes it into the swizzled B tile of step kt + 1 (two such tiles), which
 // the MFMAs then read exactly as a copied B tile.  The step barrier also waits for these LDS writes.
 constexpr int GBK = 64;
@@ -325,9 +325,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   constexpr int AREA = WM * RS * 4;       // one wavefront's epilogue area (bytes)
   constexpr int PA = A_TILE / AREA, PB = B_TILE / AREA;  // epilogue areas per A / B tile
   static_assert(2 * PA + 2 * PB >= NW, "epilogue areas fit the tiles");
-  // DQ8: int8 tiles of BN rows x 64 bytes (4 chunks, unswizzled), chunks converted per thread per step
-  constexpr int Q_TILE = DQ8 ? BN * GBK : 16, IPQ = DQ8 ? BN * 4 / 64 / NW : 1, CPT = DQ8 ? BN * 4 / (NW * 64) : 1;
-  static_assert(!DQ8 || (IPQ >= 1 && IPA + IPQ <= 16 && CPT * NW * 64 == BN * 4), "int8 copy split");
+  // DQ8: int8 tiles of BN rows x 64 bytes (4 chunks, unswizzled); each thread converts CPT 8-element pieces
+  // per step, piece c = row c / 8, bf16 chunk c % 8
+  constexpr int Q_TILE = DQ8 ? BN * GBK : 16, IPQ = DQ8 ? BN * 4 / 64 / NW : 1, CPT = DQ8 ? BN * 8 / (NW * 64) : 1;
+  static_assert(!DQ8 || (IPQ >= 1 && IPA + IPQ <= 16 && CPT * NW * 64 == BN * 8), "int8 copy split");
   // separate LDS objects per buffer, so that reads of one are known not to alias copies into another
   __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], a2_raw[A_TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t b0_raw[B_TILE], b1_raw[B_TILE];
@@ -423,23 +424,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   auto dq_scales = [&](int ks, float* sv) {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-      const int row = (u * NW * 64 + (int)threadIdx.x) >> 2;
+      const int row = (u * NW * 64 + (int)threadIdx.x) >> 3;
       sv[u] = bf16_bits_to_f32(scl[row * dq_nblocks + ks]);
     }
   };
+  // 8 int8 -> 8 values of T per piece: the 8 lanes of a group write the 8 chunks of one 128-byte B row
+  // (LDS writes are conflict-free when each group of 8 consecutive lanes stays inside one 128-byte row,
+  // measured), and the int8 reads are contiguous 8-byte pieces.
   auto dq_convert = [&](const HK_L uint8_t* Qt, HK_L uint8_t* Bt, const float* sv) {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-      const int c = u * NW * 64 + (int)threadIdx.x, row = c >> 2, q16 = c & 3;
-      const u32x4 w = *reinterpret_cast<const HK_L u32x4*>(Qt + c * 16);
-      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-      float v[16];
+      const int c = u * NW * 64 + (int)threadIdx.x, row = c >> 3, ch = c & 7;
+      const u32x2 w = *reinterpret_cast<const HK_L u32x2*>(Qt + c * 8);
+      float v[8];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = (float)(int8_t)((wv[i >> 2] >> (8 * (i & 3))) & 0xffu) * sv[u];
-      *reinterpret_cast<HK_L u32x4*>(Bt + tile_off<B_NCH>(row, 2 * q16)) =
-          u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
-      *reinterpret_cast<HK_L u32x4*>(Bt + tile_off<B_NCH>(row, 2 * q16 + 1)) =
-          u32x4{pack2<T>(v[8], v[9]), pack2<T>(v[10], v[11]), pack2<T>(v[12], v[13]), pack2<T>(v[14], v[15])};
+      for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)(((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xffu) * sv[u];
+      // round to the input dtype: the hardware pack (RNE) when the products are finite, which they are
+      // unless the scale is inf or NaN; then the software rounding, which maps NaN to 0x7FC0 like dq8_*
+      const u32x4 h = __builtin_isfinite(sv[u]) ? u32x4{cvt2<T>(v[0], v[1]), cvt2<T>(v[2], v[3]), cvt2<T>(v[4], v[5]), cvt2<T>(v[6], v[7])}
+                                                 : u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
+      *reinterpret_cast<HK_L u32x4*>(Bt + tile_off<B_NCH>(row, ch)) = h;
     }
   };
   const int k1 = nk > 1 ? 1 : 0, k2 = nk > 2 ? 2 : nk - 1;

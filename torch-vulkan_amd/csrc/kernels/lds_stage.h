@@ -51,28 +51,31 @@ __device__ __forceinline__ f32x16 zero16() {
 //     lanes): the 8 rows differ in swz bits 1..3 (NCH = 16) or, per row parity, in bits 1..2 (NCH = 8).
 #define HK_L __attribute__((address_space(3)))
 
-template <int NCH>
-__device__ __forceinline__ int tile_swz(int row);
-// NCH = 16 (256-byte rows, one row per bank line): slot bits (3, 2, 1, 0) = row bits (1, 0, 2, 3).
-template <>
-__device__ __forceinline__ int tile_swz<16>(int row) {
-  return ((row & 3) << 2) | (((row >> 2) & 1) << 1) | ((row >> 3) & 1);
-}
-// NCH = 8 (128-byte rows, row bit 0 selects the half bank line): slot bits (2, 1, 0) = row bits (1, 2, 3).
-template <>
-__device__ __forceinline__ int tile_swz<8>(int row) {
-  return (((row >> 1) & 1) << 2) | (((row >> 2) & 1) << 1) | ((row >> 3) & 1);
-}
-// NCH = 32 (512-byte rows, two bank lines per row), read only column-wise by the 32x32x16 transpose reads
-// (4 aligned rows x 4 aligned chunks per 32 lanes): slot bits (3, 2) = row bits (1, 0).
-template <>
-__device__ __forceinline__ int tile_swz<32>(int row) {
-  return (row & 3) << 2;
-}
-// NCH = 4 (64-byte rows of int8 staging tiles, read linearly): no swizzle.
-template <>
-__device__ __forceinline__ int tile_swz<4>(int) {
-  return 0;
+// SW = 0: the layouts above.  SW = 1 (NCH = 16 only): the layout of the 16x16x32 kernels' tiles (dK/dV),
+// whose 128-bit A-operand reads (16 rows x 4 chunks per wavefront) are 2-way conflicted under SW = 0 on the
+// device although that layout gives every 16 consecutive lanes distinct banks; slot = chunk ^ (row bits
+// 0..3 -> 2, 8, 14, 13), found by measuring 200 XOR maps on the device (SQ_LDS_BANK_CONFLICT): zero
+// conflicts for those reads and for the kernels' transpose reads (8 rows x 2 chunks per 32 lanes) at every
+// chunk offset.
+template <int NCH, int SW = 0>
+__device__ __forceinline__ int tile_swz(int row) {
+  static_assert(SW == 0 || NCH == 16, "the second layout exists for 256-byte rows only");
+  if constexpr (NCH == 16 && SW == 1) {
+    return (-(row & 1) & 2) ^ (-((row >> 1) & 1) & 8) ^ (-((row >> 2) & 1) & 14) ^ (-((row >> 3) & 1) & 13);
+  } else if constexpr (NCH == 16) {
+    // 256-byte rows, one row per bank line: slot bits (3, 2, 1, 0) = row bits (1, 0, 2, 3)
+    return ((row & 3) << 2) | (((row >> 2) & 1) << 1) | ((row >> 3) & 1);
+  } else if constexpr (NCH == 8) {
+    // 128-byte rows, row bit 0 selects the half bank line: slot bits (2, 1, 0) = row bits (1, 2, 3)
+    return (((row >> 1) & 1) << 2) | (((row >> 2) & 1) << 1) | ((row >> 3) & 1);
+  } else if constexpr (NCH == 32) {
+    // 512-byte rows (two bank lines per row), read only column-wise by the 32x32x16 transpose reads
+    // (4 aligned rows x 4 aligned chunks per 32 lanes): slot bits (3, 2) = row bits (1, 0)
+    return (row & 3) << 2;
+  } else {
+    static_assert(NCH == 4, "tile width");
+    return 0;  // 64-byte rows of int8 staging tiles, read linearly
+  }
 }
 // Rows after which tile_swz repeats.
 template <int NCH>
@@ -99,7 +102,7 @@ struct DmaLanes {
   uint32_t off[4];
 };
 // Lane offsets of instructions j0 .. j0 + 3 (j0 = the wavefront's first instruction index in the tile).
-template <int NCH>
+template <int NCH, int SW = 0>
 __device__ __forceinline__ DmaLanes dma_lane_offsets(uint32_t ss, int lane, int j0) {
   constexpr int RPI = 64 / NCH;
   const int rsub = lane / NCH, slot = lane % NCH;
@@ -107,12 +110,12 @@ __device__ __forceinline__ DmaLanes dma_lane_offsets(uint32_t ss, int lane, int 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = (j0 + i) * RPI + rsub;
-    d.off[i] = (uint32_t)rsub * ss + (uint32_t)((slot ^ tile_swz<NCH>(row)) << 4);
+    d.off[i] = (uint32_t)rsub * ss + (uint32_t)((slot ^ tile_swz<NCH, SW>(row)) << 4);
   }
   return d;
 }
 // `lo` must come from dma_lane_offsets with j0 = wave * (ROWS * NCH / 64 / NW).
-template <int NCH, int ROWS, int NW>
+template <int NCH, int ROWS, int NW, int SW = 0>
 __device__ __forceinline__ void dma_tile(const HK_G uint8_t* src, uint32_t ss, int valid, HK_L uint8_t* tile, int wave,
                                          int lane, const DmaLanes& lo) {
   constexpr int RPI = 64 / NCH;               // rows per instruction
@@ -132,7 +135,7 @@ __device__ __forceinline__ void dma_tile(const HK_G uint8_t* src, uint32_t ss, i
       const int j = wave * IPW + i;
       const int row = j * RPI + rsub;
       const int r = row < valid ? row : valid - 1;
-      dma16(src + ((uint32_t)r * ss + (uint32_t)((slot ^ tile_swz<NCH>(row)) << 4)), tile + j * 1024);
+      dma16(src + ((uint32_t)r * ss + (uint32_t)((slot ^ tile_swz<NCH, SW>(row)) << 4)), tile + j * 1024);
     }
   }
 }
@@ -180,9 +183,9 @@ __device__ __forceinline__ int64_t stage_origin(int st, int nst, int64_t len) {
 }
 
 // 16 bytes of a swizzled tile at (row, chunk c), as a byte offset.
-template <int NCH>
+template <int NCH, int SW = 0>
 __device__ __forceinline__ int tile_off(int row, int c) {
-  return row * (NCH * 16) + ((c ^ tile_swz<NCH>(row)) << 4);
+  return row * (NCH * 16) + ((c ^ tile_swz<NCH, SW>(row)) << 4);
 }
 
 // ds_read_b64_tr_b16 on 16-bit data: within each group of 16 lanes, if lane s addresses row k0 + (s >> 2),
