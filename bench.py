@@ -5,8 +5,8 @@ Headline (`value`): bf16 flash-attention forward + backward at B1 H16 S1024 D128
 benchmark shape), in algorithmic TFLOP/s: 4*B*H*S^2*D forward + 2.5x that backward = 3.006e10 flop per
 step (the convention of the reference's tools/bench_attention.py:39).  A step is the hot path's three
 kernels (forward, dQ with the delta pass folded in, dK/dV) over one batch already resident in HBM, queued
-through the hrt C ABI exactly as the PyTorch shim queues them, replayed as a HIP graph on the runtime's
-stream and timed with HIP events on that stream.  The same JSON line carries the other benchmark workloads
+through the hrt C ABI exactly as the PyTorch shim queues them, directly on the runtime's stream, and timed
+with HIP events on that stream.  The same JSON line carries the other benchmark workloads
 (GEMMs, softmax, layer_norm, int8 dequant, the fused int8 linear, attention at S=4096), each as absolute
 TFLOP/s or GB/s and as a fraction of MI355X's published peak, the roofline object of the step's dominant
 kernel (its HBM traffic from the rocprofv3 counter summary in profiles/, when present), the PyTorch-level
@@ -179,17 +179,22 @@ class Bench:
         B, H, S, D = 1, 16, 1024, 128
         step, kernels, keep, names = self.attn_setup(B, H, S, D)
         fwd_f, bwd_f = attn_flops(B, H, S, S, D)
-        gid = rt.graph(step)
+        # the steps are queued directly on the runtime stream, as the shim queues them (replaying the step as
+        # a 3-node HIP graph costs ~10 us more per step on this runtime: each graph launch carries a fixed cost)
         for _ in range(args.warmup):
-            rt.graph_launch(gid)
+            step()
         rt.synchronize()
         rt.event_record(0)
         for _ in range(args.steps):
-            rt.graph_launch(gid)
+            step()
         rt.event_record(1)
         rt.synchronize()
         ms = rt.elapsed_ms(0, 1) / args.steps
-        rt.graph_destroy(gid)
+        gid = rt.graph(step)
+        try:
+            self.graph_step_ms = self.time_graph(lambda i: rt.graph_launch(gid), 1, launches=args.steps)
+        finally:
+            rt.graph_destroy(gid)
         # per-kernel average launch durations (20 back-to-back launches each)
         per = {n: self.time_graph(kernels[n], 20) for n in ("fwd", "dq", "dkdv")}
         unit = 2.0 * B * H * S * S * D  # one S x S x D product
@@ -483,6 +488,7 @@ def main():
         "frac_of_bf16_peak": round(tflops / PEAK_TFLOPS["bf16"], 4),
         "roofline": roof,
         "attn_kernels": kstats,
+        "ms_per_step_graph_replay": round(bench.graph_step_ms, 5),
     }
     if not args.only_attn:
         line["attn_torch_path"] = bench.attn_torch_step()

@@ -441,48 +441,46 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
 
   const int j0 = wave * (KST2 * NCH / 64 / NW);
   const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane, j0), vlo = dma_lane_offsets<NCH>(vss, lane, j0);
-  dma_tile<NCH, KST2, NW>(Kb, kss, Sk, K0, wave, lane, klo);
-  dma_tile<NCH, KST2, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
+  // The block's 64 rows of Q and dO go to the stage-1 buffers (free until stage 0 copies into them), copied
+  // once for the four wavefronts that share them, ahead of K(0), V(0); rows past Sq hold copies of the last
+  // row (P = 0 for them: lse = -inf below)
+  const uint32_t qss = (uint32_t)(p.q_ss * 2), oss = (uint32_t)(p.do_ss * 2);
+  const int qvalid = (int)(Sq - qb * 64);
+  {
+    const int jq = wave * (64 * NCH / 64 / NW);
+    const HK_G uint8_t* Qblk = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh) +
+                               qb * 64 * (int64_t)qss;
+    const HK_G uint8_t* Oblk = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.dout) + b * p.do_sb + hh * p.do_sh) +
+                               qb * 64 * (int64_t)oss;
+    dma_tile<NCH, 64, NW>(Qblk, qss, qvalid, K1, wave, lane, dma_lane_offsets<NCH>(qss, lane, jq));
+    dma_tile<NCH, 64, NW>(Oblk, oss, qvalid, V1, wave, lane, dma_lane_offsets<NCH>(oss, lane, jq));
+  }
 
   const int64_t q = qb * 64 + g * 32 + ql;
   const bool qv = q < Sq;
-  const HK_G uint16_t* Qr = gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh + q * p.q_ss;
-  const HK_G uint16_t* dOr = gcptr<uint16_t>(p.dout) + b * p.do_sb + hh * p.do_sh + q * p.do_ss;
-  u32x4 qf[2 * DCH], df[2 * DCH];
-#pragma unroll
-  for (int ks = 0; ks < 2 * DCH; ++ks) {
-    qf[ks] = qv ? *reinterpret_cast<const HK_G u32x4*>(Qr + ks * 16 + 8 * hl) : u32x4{0, 0, 0, 0};
-    df[ks] = qv ? *reinterpret_cast<const HK_G u32x4*>(dOr + ks * 16 + 8 * hl) : u32x4{0, 0, 0, 0};
-  }
-  const float nlse2 = qv ? -gcptr<float>(p.lse)[bh * Sq + q] * kLog2e : -INFINITY;  // P = 0 for padded rows
-  float dlt = 0.f;
+  // lse (used after the first barrier: a use here would wait for every copy issued so far)
+  const float lse_raw = gcptr<float>(p.lse)[bh * Sq + (qv ? q : 0)];
+  // delta: this wave's quarter of d of its row's o (fp32 when OF32), loaded now; dO comes from LDS below
+  constexpr int OV = OF32 ? 2 : 1;  // 16-byte pieces of o per 8 elements
+  u32x4 oraw[WITH_DELTA ? KSQ * OV : 1];
   if constexpr (WITH_DELTA) {
-    float part = 0.f;
-    if (qv) {
-      const int64_t orow = ((b * Sq + q) * p.H + hh) * p.D;
+    const int64_t orow = ((b * Sq + (qv ? q : 0)) * p.H + hh) * p.D;
 #pragma unroll
-      for (int i = 0; i < KSQ; ++i) {
-        const int d0 = (kq * KSQ + i) * 16 + 8 * hl;
-        const u32x4 dv = *reinterpret_cast<const HK_G u32x4*>(dOr + d0);
-        float ov[8];
-        if constexpr (OF32) {
-          const f32x4 a = *reinterpret_cast<const HK_G f32x4*>(gcptr<float>(p.o) + orow + d0);
-          const f32x4 c = *reinterpret_cast<const HK_G f32x4*>(gcptr<float>(p.o) + orow + d0 + 4);
-          ov[0] = a[0], ov[1] = a[1], ov[2] = a[2], ov[3] = a[3], ov[4] = c[0], ov[5] = c[1], ov[6] = c[2], ov[7] = c[3];
-        } else {
-          const u32x4 a = *reinterpret_cast<const HK_G u32x4*>(gcptr<uint16_t>(p.o) + orow + d0);
-#pragma unroll
-          for (int w = 0; w < 4; ++w) ov[2 * w] = lo16<T>(a[w]), ov[2 * w + 1] = hi16<T>(a[w]);
-        }
-#pragma unroll
-        for (int w = 0; w < 4; ++w) part += ov[2 * w] * lo16<T>(dv[w]) + ov[2 * w + 1] * hi16<T>(dv[w]);
+    for (int i = 0; i < KSQ; ++i) {
+      const int d0 = (kq * KSQ + i) * 16 + 8 * hl;
+      if constexpr (OF32) {
+        oraw[2 * i] = *reinterpret_cast<const HK_G u32x4*>(gcptr<float>(p.o) + orow + d0);
+        oraw[2 * i + 1] = *reinterpret_cast<const HK_G u32x4*>(gcptr<float>(p.o) + orow + d0 + 4);
+      } else {
+        oraw[i] = *reinterpret_cast<const HK_G u32x4*>(gcptr<uint16_t>(p.o) + orow + d0);
       }
     }
-    part = halfswap_sum(part);
-    if (hl == 0) xdel[kq][g * 32 + ql] = part;
-  } else {
-    dlt = qv ? gcptr<float>(p.delta)[bh * Sq + q] : 0.f;
   }
+  float dlt = 0.f;
+  if constexpr (!WITH_DELTA) dlt = gcptr<float>(p.delta)[bh * Sq + (qv ? q : 0)];
+  issue_order_fence();  // the first barrier counts on K(0), V(0) being the last copies issued
+  dma_tile<NCH, KST2, NW>(Kb, kss, Sk, K0, wave, lane, klo);
+  dma_tile<NCH, KST2, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
 
   int koff[2 * DCH], voff[DCH][2];
 #pragma unroll
@@ -500,7 +498,44 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
   for (int n = 0; n < DCH; ++n) acc[n] = zero16();
   const float sl2 = p.scale * kLog2e;
 
-  __syncthreads();  // stage 0 in LDS; partial deltas published
+  // Q and dO rows (and o) landed; K(0), V(0), issued last, may still be in flight
+  barrier_keep_vm<2 * (KST2 * NCH / 64 / NW)>();
+  const float nlse2 = qv ? -lse_raw * kLog2e : -INFINITY;  // P = 0 for padded rows
+  if constexpr (!WITH_DELTA) dlt = qv ? dlt : 0.f;
+  u32x4 qf[2 * DCH], df[2 * DCH];
+#pragma unroll
+  for (int ks = 0; ks < 2 * DCH; ++ks) {
+    qf[ks] = *reinterpret_cast<const HK_L u32x4*>(K1 + tile_off<NCH>(g * 32 + ql, 2 * ks + hl));
+    df[ks] = *reinterpret_cast<const HK_L u32x4*>(V1 + tile_off<NCH>(g * 32 + ql, 2 * ks + hl));
+  }
+  if constexpr (WITH_DELTA) {
+    float part = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 2 * DCH; ++ks) {
+      // d = 16 ks + 8 hl .. +7 is this wave's quarter when ks / KSQ == kq (constant indices: a runtime
+      // index would move df to scratch memory)
+      if (ks / KSQ != kq) continue;
+      const int i = ks % KSQ;
+      const u32x4 dv = df[ks];
+      float ov[8];
+      if constexpr (OF32) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          // __uint_as_float: __builtin_bit_cast of a vector element miscompiles here (wrong element read)
+          ov[w] = __uint_as_float(oraw[2 * i][w]);
+          ov[4 + w] = __uint_as_float(oraw[2 * i + 1][w]);
+        }
+      } else {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) ov[2 * w] = lo16<T>(oraw[i][w]), ov[2 * w + 1] = hi16<T>(oraw[i][w]);
+      }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) part += ov[2 * w] * lo16<T>(dv[w]) + ov[2 * w + 1] * hi16<T>(dv[w]);
+    }
+    part = halfswap_sum(qv ? part : 0.f);
+    if (hl == 0) xdel[kq][g * 32 + ql] = part;
+  }
+  __syncthreads();  // stage 0 in LDS; partial deltas published; Q / dO read out of the stage-1 buffers
   if constexpr (WITH_DELTA) {
     dlt = xdel[0][g * 32 + ql] + xdel[1][g * 32 + ql] + xdel[2][g * 32 + ql] + xdel[3][g * 32 + ql];
     if (kq == 0 && hl == 0 && qv) gptr<float>(p.delta)[bh * Sq + q] = dlt;
@@ -610,20 +645,23 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
 
 // ---- dK / dV fast path: D = 64 or 128, 16-byte aligned rows -------------------------------------------------
 //
-// Per workgroup 64 keys; Q and dO stream through LDS in double-buffered 64-query stages copied global ->
-// LDS directly.  8 wavefronts on v_mfma_f32_16x16x32 (see mfma_common.h for its lane layout): wave
-// (k = w & 3, h = w >> 2) owns keys 16 k .. +15 of the block (their K and V rows held as B fragments) and
-// query rows 32 h .. +31 of every stage, so its dK/dV partials are 16 keys x D each (64 registers for
-// D = 128) and every LDS fragment read is conflict-free.  Per stage and 16-query tile t:
+// Per workgroup 64 keys; Q and dO stream through LDS in double-buffered 128-query stages copied global ->
+// LDS directly, each stage computed as two 64-query halves (one barrier per 128 queries).  8 wavefronts on
+// v_mfma_f32_16x16x32 (see mfma_common.h for its lane layout): wave (k = w & 3, h = w >> 2) owns keys
+// 16 k .. +15 of the block (their K and V rows held as B fragments) and query rows 32 h .. +31 of every
+// 64-query half, so its dK/dV partials are 16 keys x D each (64 registers for D = 128) and every LDS
+// fragment read is conflict-free.  Per half and 16-query tile t:
 //   S_t = Q_t K^T, dP_t = dO_t V^T            (lane = key, 4 queries 4 g + i per tile, g = lane / 16)
 //   P = exp2(S sl2 - lse log2e), dS = P (dP - delta)
 //   dV += P^T dO, dK += dS^T Q                (A = P^T / dS^T packed from the two tiles' accumulators as
 //                                              the 32 k-slots {4 g + i, 16 + 4 g + i}; B = dO / Q read
 //                                              column-wise with ds_read_b64_tr_b16 in the same slot order)
-// lse and delta for the next stage are prefetched into registers.  The two query halves are summed through
-// LDS at the end and dK (scaled), dV are written as coalesced rows.  P and dS are rounded to the input
-// dtype before their products, as attn_coop.comp.in:235-236, 283-284.
-constexpr int QST = 64;  // queries per LDS stage
+// lse and delta of the next half are prefetched into registers.  At the end the two query halves swap
+// partials through LDS (wave (k, 1) hands over its dK, wave (k, 0) its dV), so wave (k, 0) writes dK
+// (scaled) and wave (k, 1) writes dV, both as coalesced rows.  P and dS are rounded to the input dtype
+// before their products, as attn_coop.comp.in:235-236, 283-284.
+constexpr int QST = 128;  // queries per LDS stage
+constexpr int QHALF = 64;  // queries per computed half
 
 template <typename T, int DCH, bool A4>
 __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
@@ -654,31 +692,35 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
 
   const int j0 = wave * (QST * NCH / 64 / NW);
   const DmaLanes qlo = dma_lane_offsets<NCH, SW>(qss, lane, j0), olo = dma_lane_offsets<NCH, SW>(oss, lane, j0);
+  // The block's 64 K and V rows go to the stage-1 buffers (free until stage 0 copies into them), copied once
+  // for the two wavefronts that share them (rows past Sk hold copies of the last key; their dK / dV rows
+  // are never stored), then stage 0 of Q and dO
+  {
+    const uint32_t kss = (uint32_t)(p.k_ss * 2), vss = (uint32_t)(p.v_ss * 2);
+    const int kvalid = (int)(Sk - kb * 64);
+    const int jk = wave * (64 * NCH / 64 / NW);
+    const HK_G uint8_t* Kblk = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.k) + b * p.k_sb + hh * p.k_sh) +
+                               kb * 64 * (int64_t)kss;
+    const HK_G uint8_t* Vblk = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.v) + b * p.v_sb + hh * p.v_sh) +
+                               kb * 64 * (int64_t)vss;
+    dma_tile<NCH, 64, NW, SW>(Kblk, kss, kvalid, Q1, wave, lane, dma_lane_offsets<NCH, SW>(kss, lane, jk));
+    dma_tile<NCH, 64, NW, SW>(Vblk, vss, kvalid, O1, wave, lane, dma_lane_offsets<NCH, SW>(vss, lane, jk));
+  }
+  issue_order_fence();  // the first barrier counts on stage 0's copies being the last ones issued
   dma_tile<NCH, QST, NW, SW>(Qb, qss, Sq, Q0, wave, lane, qlo);
   dma_tile<NCH, QST, NW, SW>(Ob, oss, Sq, O0, wave, lane, olo);
 
-  // this lane's key (column l16 of the 16x16 tiles): K and V as B fragments, d = 32 ks + 8 g + i
-  const int64_t key = kb * 64 + kg * 16 + l16;
-  const bool kv = key < Sk;
-  const HK_G uint16_t* Kr = gcptr<uint16_t>(p.k) + b * p.k_sb + hh * p.k_sh + key * p.k_ss;
-  const HK_G uint16_t* Vr = gcptr<uint16_t>(p.v) + b * p.v_sb + hh * p.v_sh + key * p.v_ss;
-  u32x4 kf[DCH], vf[DCH];
-#pragma unroll
-  for (int ks = 0; ks < DCH; ++ks) {
-    kf[ks] = kv ? *reinterpret_cast<const HK_G u32x4*>(Kr + ks * 32 + 8 * g4) : u32x4{0, 0, 0, 0};
-    vf[ks] = kv ? *reinterpret_cast<const HK_G u32x4*>(Vr + ks * 32 + 8 * g4) : u32x4{0, 0, 0, 0};
-  }
-
-  // lse and delta of this lane's 8 queries of a stage: tile t, rows 32 qh + 16 t + 4 g + i (i = 0..3, four
-  // consecutive floats: one 16-byte load each when A4, i.e. Sq % 4 == 0 and 16-byte aligned arrays)
+  // lse and delta of this lane's 8 queries of a half: tile t, rows 64 half + 32 qh + 16 t + 4 g + i of the
+  // stage (i = 0..3, four consecutive floats: one 16-byte load each when A4, i.e. Sq % 4 == 0 and 16-byte
+  // aligned arrays)
   const HK_G float* lseb = gcptr<float>(p.lse) + bh * Sq;
   const HK_G float* dltb = gcptr<float>(p.delta) + bh * Sq;
   f32x4 nl[2], dl[2];  // lse, delta
   // Stage st's tile starts at query row origin(st) (stage_origin when there is more than one stage); its
   // rows outside [st QST, Sq) get lse = +inf, so P = dS = 0 for them.
-  auto fetch = [&](int st, f32x4* lo, f32x4* dlo) {
+  auto fetch = [&](int st, int half, f32x4* lo, f32x4* dlo) {
     const int64_t org = nst > 1 ? stage_origin<QST>(st, nst, Sq) : 0;
-    const int r0 = (int)org + qh * 32 + 4 * g4;
+    const int r0 = (int)org + half * QHALF + qh * 32 + 4 * g4;
     if (A4 && st * QST + QST <= Sq) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -697,11 +739,11 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
         }
     }
   };
-  fetch(0, nl, dl);
+  fetch(0, 0, nl, dl);
 
-  // per-lane byte offsets: A-operand rows (query 32 qh + 16 t + l16, chunk 4 ks + g; t adds 16 rows, which
-  // keeps the swizzle) and B-operand column reads (rows 32 qh + 4 g + (l16 >> 2) (+16 for the second read),
-  // columns 16 dt + 4 (l16 & 3))
+  // per-lane byte offsets: A-operand rows (query 32 qh + 16 t + l16, chunk 4 ks + g; t adds 16 rows and the
+  // half 64 rows, which keeps the swizzle) and B-operand column reads (rows 32 qh + 4 g + (l16 >> 2) (+16
+  // for the second read), columns 16 dt + 4 (l16 & 3))
   int roff[DCH], coff[NDT];
 #pragma unroll
   for (int ks = 0; ks < DCH; ++ks) roff[ks] = tile_off<NCH, SW>(qh * 32 + l16, 4 * ks + g4);
@@ -714,19 +756,32 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   for (int dt = 0; dt < NDT; ++dt) dk[dt] = dv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float sl2 = p.scale * kLog2e;
 
-  __syncthreads();
-  // COPY: stage st + 1 is copied while stage st computes, the copies placed between the MFMAs of S / dP;
-  // with more than one stage they are branch-free (stage_origin, as in the other attention kernels).
+  // K and V rows landed (stage 0 of Q / dO may still be in flight); this lane's key (column l16 of the
+  // 16x16 tiles): K and V as B fragments, d = 32 ks + 8 g + i
+  barrier_keep_vm<2 * (QST * NCH / 64 / NW)>();
+  u32x4 kf[DCH], vf[DCH];
+#pragma unroll
+  for (int ks = 0; ks < DCH; ++ks) {
+    kf[ks] = *reinterpret_cast<const HK_L u32x4*>(Q1 + tile_off<NCH, SW>(kg * 16 + l16, 4 * ks + g4));
+    vf[ks] = *reinterpret_cast<const HK_L u32x4*>(O1 + tile_off<NCH, SW>(kg * 16 + l16, 4 * ks + g4));
+  }
+  __syncthreads();  // stage 0 landed; every wave holds its K / V fragments before stage 1 is copied over them
+  // COPY: stage st + 1 is copied while stage st computes (its Q rows during the first half, its dO rows
+  // during the second), the copies placed between the MFMAs of S / dP; with more than one stage they are
+  // branch-free (stage_origin, as in the other attention kernels).
   constexpr int IPW = QST * NCH / 64 / NW;
-  auto stage = [&](auto bc, auto cc, int st) {
+  static_assert(IPW <= 2 * DCH, "a half's copies fit between its S / dP products");
+  auto half_stage = [&](auto bc, auto hc, auto cc, int st) {
     constexpr int BUF = decltype(bc)::value;
+    constexpr int HALF = decltype(hc)::value;
     constexpr bool COPY = decltype(cc)::value;
-    const HK_G uint8_t* qsrc = Qb + stage_origin<QST>(st + 1, nst, Sq) * qss;
-    const HK_G uint8_t* osrc = Ob + stage_origin<QST>(st + 1, nst, Sq) * oss;
+    const HK_G uint8_t* src = HALF ? Ob + stage_origin<QST>(st + 1, nst, Sq) * oss
+                                   : Qb + stage_origin<QST>(st + 1, nst, Sq) * qss;
+    const bool more = HALF == 0 || st + 1 < nst;
     f32x4 nn[2], dn[2];
-    if (st + 1 < nst) fetch(st + 1, nn, dn);
-    const HK_L uint8_t* Qt = BUF ? Q1 : Q0;
-    const HK_L uint8_t* Ot = BUF ? O1 : O0;
+    if (more) fetch(HALF ? st + 1 : st, HALF ^ 1, nn, dn);
+    const HK_L uint8_t* Qt = (BUF ? Q1 : Q0) + HALF * QHALF * ROWB;
+    const HK_L uint8_t* Ot = (BUF ? O1 : O0) + HALF * QHALF * ROWB;
     f32x4 s[2], dp[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -737,8 +792,8 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
         dp[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Ot + roff[ks] + t * 16 * ROWB), vf[ks], dp[t]);
         if constexpr (COPY) {
           const int c = t * DCH + ks;
-          if (c < IPW) dma_tile_part<NCH, QST, NW>(qsrc, qss, BUF ? Q0 : Q1, wave, qlo, c);
-          else if (c < 2 * IPW) dma_tile_part<NCH, QST, NW>(osrc, oss, BUF ? O0 : O1, wave, olo, c - IPW);
+          if (c < IPW) dma_tile_part<NCH, QST, NW>(src, HALF ? oss : qss, HALF ? (BUF ? O0 : O1) : (BUF ? Q0 : Q1),
+                                                   wave, HALF ? olo : qlo, c);
         }
       }
     }
@@ -760,65 +815,69 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
       const u32x2 b0 = lds_tr4(Qt + coff[dt]), b1 = lds_tr4(Qt + coff[dt] + 16 * ROWB);
       dk[dt] = Mfma<T>::mac(da, u32x4{b0.x, b0.y, b1.x, b1.y}, dk[dt]);
     }
-    if (st + 1 < nst) {
+    if (more) {
       nl[0] = nn[0], nl[1] = nn[1], dl[0] = dn[0], dl[1] = dn[1];
     }
-    __syncthreads();
+    if constexpr (HALF == 1 && COPY) __syncthreads();
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
   if (nst == 1) {
-    stage(std::integral_constant<int, 0>(), std::false_type(), 0);
+    half_stage(I0(), I0(), std::false_type(), 0);
+    if (Sq > QHALF) half_stage(I0(), I1(), std::false_type(), 0);
+    __syncthreads();
   } else {
     for (int st = 0; st < nst; st += 2) {
-      stage(std::integral_constant<int, 0>(), std::true_type(), st);
-      if (st + 1 < nst) stage(std::integral_constant<int, 1>(), std::true_type(), st + 1);
+      half_stage(I0(), I0(), std::true_type(), st);
+      half_stage(I0(), I1(), std::true_type(), st);
+      if (st + 1 < nst) {
+        half_stage(I1(), I0(), std::true_type(), st + 1);
+        half_stage(I1(), I1(), std::true_type(), st + 1);
+      }
     }
   }
 
-  // ---- sum the two query halves: wave (k, 1) hands its partials to wave (k, 0) through tile k's area, which
-  // wave (k, 0) then reuses to transpose the results into [key][d] rows for coalesced stores
+  // ---- sum the two query halves through tile k's area: slot 0 takes wave (k, 1)'s dK partials, slot 1 wave
+  // (k, 0)'s dV partials (16 bytes per lane and d tile); each wave then reuses its own slot to transpose its
+  // result into [key][d] rows for coalesced stores.
   float* const area = reinterpret_cast<float*>(kg == 0 ? q0_raw : kg == 1 ? q1_raw : kg == 2 ? o0_raw : o1_raw);
-  static_assert(2 * NDT * 4 * 64 * 4 <= TILE, "partials fit a tile");
-  if (qh == 1) {
+  constexpr int SLOT = NDT * 64 * 4;  // floats per slot
+  static_assert(2 * SLOT * 4 <= TILE && 16 * DCH * 32 == SLOT, "both slots fit a tile; a slot holds 16 rows of D");
+  f32x4* const give = reinterpret_cast<f32x4*>(area + (qh == 1 ? 0 : SLOT));
+  const f32x4* const take = reinterpret_cast<const f32x4*>(area + (qh == 1 ? SLOT : 0));
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        area[((0 * NDT + dt) * 4 + i) * 64 + lane] = dk[dt][i];
-        area[((1 * NDT + dt) * 4 + i) * 64 + lane] = dv[dt][i];
-      }
-  }
+  for (int dt = 0; dt < NDT; ++dt) give[dt * 64 + lane] = qh == 1 ? dk[dt] : dv[dt];
   __syncthreads();
-  if (qh == 1) return;
+  f32x4 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = take[dt * 64 + lane];  // all reads issued before the first use
+  const float mul = qh == 0 ? p.scale : 1.f;                          // dK is scaled, dV not (x * 1 == x)
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      dk[dt][i] = (dk[dt][i] + area[((0 * NDT + dt) * 4 + i) * 64 + lane]) * p.scale;
-      dv[dt][i] += area[((1 * NDT + dt) * 4 + i) * 64 + lane];
-    }
-  // accumulator element i of d tile dt: key 4 g + i, d = 16 dt + l16.  Transposed through the area into
-  // [key][d] rows of DP + 4 floats (conflict-free writes), dK then dV, and stored 8 d per lane.
-  constexpr int RS = DCH * 32 + 4;
+    for (int i = 0; i < 4; ++i) acc[dt][i] = ((qh == 0 ? dk[dt][i] : dv[dt][i]) + acc[dt][i]) * mul;
+  // accumulator element i of d tile dt: key 4 g + i, d = 16 dt + l16.  Transposed through this wave's slot
+  // (read above, same wavefront, so the reads complete before these writes) into 16 [key][d] rows whose
+  // 16-float groups are XOR-permuted by (row / 4) % 4 (conflict-free writes), then stored 8 d per lane.
+  constexpr int DP = DCH * 32;
   constexpr int LPR = DCH * 4;  // lanes per row
-  static_assert(16 * RS * 4 <= TILE, "transposed results fit a tile");
-  auto emit = [&](const f32x4* acc, uint64_t dst_base) {
+  float* const tr = reinterpret_cast<float*>(const_cast<f32x4*>(take));
+  auto phys = [](int r, int c) { return r * DP + (c ^ (16 * ((r >> 2) & 3))); };
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) area[(4 * g4 + i) * RS + 16 * dt + l16] = acc[dt][i];
+    for (int i = 0; i < 4; ++i) tr[phys(4 * g4 + i, 16 * dt + l16)] = acc[dt][i];
+  const uint64_t dst_base = qh == 0 ? p.dk : p.dv;
 #pragma unroll
-    for (int ps = 0; ps < 16 * LPR / 64; ++ps) {
-      const int r = ps * (64 / LPR) + lane / LPR, c8 = (lane % LPR) * 8;
-      const f32x4 x = *reinterpret_cast<const f32x4*>(area + r * RS + c8);
-      const f32x4 y = *reinterpret_cast<const f32x4*>(area + r * RS + c8 + 4);
-      const int64_t kk = kb * 64 + kg * 16 + r;
-      if (kk < Sk)
-        *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + ((b * Sk + kk) * p.H + hh) * p.D + c8) =
-            u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
-    }
-  };
-  emit(dk, p.dk);
-  emit(dv, p.dv);  // same wavefront: its LDS reads of dK's rows complete before these writes
+  for (int ps = 0; ps < 16 * LPR / 64; ++ps) {
+    const int r = ps * (64 / LPR) + lane / LPR, c8 = (lane % LPR) * 8;
+    const f32x4 x = *reinterpret_cast<const f32x4*>(tr + phys(r, c8));
+    const f32x4 y = *reinterpret_cast<const f32x4*>(tr + phys(r, c8) + 4);
+    const int64_t kk = kb * 64 + kg * 16 + r;
+    if (kk < Sk)
+      *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + ((b * Sk + kk) * p.H + hh) * p.D + c8) =
+          u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+  }
 }
 
 // The direct-to-LDS paths need D = 64 or 128, 16-byte aligned rows (q, k, v, dout) and per-stage row

@@ -263,16 +263,18 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 
   const int j0 = wave * (KST * NCH / 64 / NW);
   const DmaLanes klo = dma_lane_offsets<NCH>(kss, lane, j0), vlo = dma_lane_offsets<NCH>(vss, lane, j0);
-  // Q^T operand fragments of this lane's query (needed first), then K(0), V(0) and K(1): K streams one
-  // stage ahead of V
-  const HK_G uint16_t* Q = gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh;
+  // The block's 64 Q rows go to V(1)'s buffer (free until stage 0 copies V(1)), copied once for the four
+  // wavefronts that share them; then K(0), V(0) and K(1): K streams one stage ahead of V
+  const uint32_t qss = (uint32_t)(p.q_ss * 2);
+  const HK_G uint8_t* Qblk = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh) +
+                             qb * 64 * (int64_t)qss;
   const int64_t q = qb * 64 + g * 32 + ql;
-  u32x4 qf[2 * DCH];
-#pragma unroll
-  for (int ks = 0; ks < 2 * DCH; ++ks)
-    qf[ks] = q < Sq ? *reinterpret_cast<const HK_G u32x4*>(Q + q * p.q_ss + ks * 16 + 8 * hl) : u32x4{0, 0, 0, 0};
+  u32x4 qf[2 * DCH];  // Q^T operand fragments of this lane's query, read from LDS after the first barrier
+  dma_tile<NCH, 64, NW>(Qblk, qss, (int)(Sq - qb * 64), V1, wave, lane,
+                        dma_lane_offsets<NCH>(qss, lane, wave * (64 * NCH / 64 / NW)));
   dma_tile<NCH, KST, NW>(Kb, kss, Sk, K0, wave, lane, klo);
   dma_tile<NCH, KST, NW>(Vb, vss, Sk, V0, wave, lane, vlo);
+  issue_order_fence();  // the first barrier counts on K(1) being the last copy issued
   if (nst > 1) dma_tile<NCH, KST, NW>(Kb + stage_origin<KST>(1, nst, Sk) * kss, kss, KST, K1, wave, lane, klo);
 
   // per-lane byte offsets of the A-operand fragments inside a tile
@@ -396,10 +398,16 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
     if (COPY && st + 1 < nst) mask_and_max(sn, st + 1);
     __syncthreads();  // waits for this wave's copies, then for every wave
   };
-  __syncthreads();
+  // Q, K(0), V(0) landed (K(1), issued last, may still be in flight)
+  if (nst > 1) barrier_keep_vm<KST * NCH / 64 / NW>();
+  else __syncthreads();
+  // (rows past Sq hold copies of the last row; their results are never stored)
+#pragma unroll
+  for (int ks = 0; ks < 2 * DCH; ++ks)
+    qf[ks] = *reinterpret_cast<const HK_L u32x4*>(V1 + tile_off<NCH>(g * 32 + ql, 2 * ks + hl));
   f32x16 sa = qk(K0), sb;
   mask_and_max(sa, 0);
-  __syncthreads();  // every wave is done with K(0) before it is copied over
+  __syncthreads();  // every wave is done with K(0) and Q before they are copied over
   if (nst == 1) {
     stage(std::integral_constant<int, 0>(), std::false_type(), 0, sa, sb);
   } else {
@@ -489,7 +497,7 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 bool fwd_dma_ok(const hrt_attn_args& a) {
   if (!(a.D == 64 || a.D == 128) || !attn_vec_ok(a, false)) return false;
   const int64_t lim = (int64_t)1 << 31;
-  return a.k_ss * 2 * (KST + 1) < lim && a.v_ss * 2 * (KST + 1) < lim;
+  return a.k_ss * 2 * (KST + 1) < lim && a.v_ss * 2 * (KST + 1) < lim && a.q_ss * 2 * (64 + 1) < lim;
 }
 
 template <typename T>
