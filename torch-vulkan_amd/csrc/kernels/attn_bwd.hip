@@ -606,9 +606,10 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
   for (int n = 0; n < DCH; ++n) {
     if (n == kq) continue;
     const int pc = g * DCH + n;
-    float* dst = tile_f(pc / PPT) + (pc % PPT) * PIECE + ((kq - n - 1) & 3) * 16 * 64 + lane;
+    // [4][64 lanes] 16-byte pieces: acc[n][4 c .. 4 c + 3] of lane l at 4 c * 64 + 4 l (conflict-free)
+    f32x4* dst = reinterpret_cast<f32x4*>(tile_f(pc / PPT) + (pc % PPT) * PIECE + ((kq - n - 1) & 3) * 16 * 64) + lane;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) dst[e * 64] = acc[n][e];
+    for (int c = 0; c < 4; ++c) dst[c * 64] = f32x4{acc[n][4 * c], acc[n][4 * c + 1], acc[n][4 * c + 2], acc[n][4 * c + 3]};
   }
   __syncthreads();
   auto finish = [&](auto nc) {
@@ -619,7 +620,11 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
 #pragma unroll
     for (int sl = 0; sl < 3; ++sl)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) r[e] += area[(sl * 16 + e) * 64 + lane];
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 x = reinterpret_cast<const f32x4*>(area + sl * 16 * 64)[c * 64 + lane];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) r[4 * c + w] += x[w];
+      }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       *reinterpret_cast<f32x4*>(area + ql * 36 + 8 * j + 4 * hl) =

@@ -430,9 +430,10 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
   for (int n = 0; n < DCH; ++n) {
     if (n == kq) continue;
     const int pc = g * DCH + n;
-    float* dst = tile_f(pc / PPT) + (pc % PPT) * PIECE + ((kq - n - 1) & 3) * 16 * 64 + lane;
+    // [4][64 lanes] 16-byte pieces: o[n][4 c .. 4 c + 3] of lane l at 4 c * 64 + 4 l (conflict-free)
+    f32x4* dst = reinterpret_cast<f32x4*>(tile_f(pc / PPT) + (pc % PPT) * PIECE + ((kq - n - 1) & 3) * 16 * 64) + lane;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) dst[e * 64] = o[n][e];
+    for (int c = 0; c < 4; ++c) dst[c * 64] = f32x4{o[n][4 * c], o[n][4 * c + 1], o[n][4 * c + 2], o[n][4 * c + 3]};
   }
   __syncthreads();
 
@@ -461,8 +462,13 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       if (k == N) continue;
+      const f32x4* src = reinterpret_cast<const f32x4*>(area + ((k - N - 1) & 3) * 16 * 64) + lane;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = fmaf(aw[k], area[(((k - N - 1) & 3) * 16 + e) * 64 + lane], acc[e]);
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 x = src[c * 64];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[4 * c + r] = fmaf(aw[k], x[r], acc[4 * c + r]);
+      }
     }
     // transpose the 32 x 32 block through the same area (rows of 36 floats: conflict-free 16-byte writes),
     // so that 8 lanes store one query's 32 d contiguously (128 bytes of o32, 64 of o) instead of every lane
