@@ -37,8 +37,8 @@ PEAK_GBS = 8000.0  # MI355X HBM3E
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
@@ -192,7 +192,14 @@ class Bench:
         ms = rt.elapsed_ms(0, 1) / args.steps
         gid = rt.graph(step)
         try:
-            self.graph_step_ms = self.time_graph(lambda i: rt.graph_launch(gid), 1, launches=args.steps)
+            rt.graph_launch(gid)
+            rt.synchronize()
+            rt.event_record(0)
+            for _ in range(args.steps):
+                rt.graph_launch(gid)
+            rt.event_record(1)
+            rt.synchronize()
+            self.graph_step_ms = rt.elapsed_ms(0, 1) / args.steps
         finally:
             rt.graph_destroy(gid)
         # per-kernel average launch durations (20 back-to-back launches each)
