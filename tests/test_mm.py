@@ -192,6 +192,23 @@ def test_small_tile_fast_path_layouts_and_bias(ta, tb, m, k, n):
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,k,n", [(4096, 192, 4096), (2048, 320, 8192)])
+def test_large_tile_fast_path_layouts_and_bias(ta, tb, m, k, n):
+    """Problems with at least 256 tiles of 256 x 256 take the 256 x 256-tile kernel with a two-buffer ring (odd
+    K step counts: the loop's last step runs alone)."""
+    dt = torch.bfloat16
+    a = randn((k, m) if ta else (m, k), dt, 33)
+    b = randn((n, k) if tb else (k, n), dt, 34)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), dt, 35)
+    out = torch.addmm(bias.to(dev), A, B, alpha=1.5, beta=0.5)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 1.5, 0.5)
+    check(out, ref, dt, k)
+    assert oracle.rel_l2(f64(out), ref) <= 1e-2
+
+
 def test_tile_aligned_fast_path_batched_and_full_bias():
     bt, m, k, n = 2, 1024, 128, 6144
     a, b = randn((bt, m, k), torch.bfloat16, 16), randn((bt, k, n), torch.bfloat16, 17)

@@ -306,10 +306,11 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 // the MFMAs then read exactly as a copied B tile.  The step barrier also waits for these LDS writes.
 constexpr int GBK = 64;
 
-template <typename T, int BM, int BN, int WM, int WN, bool ATR, bool BTR, bool DQ8>
+template <typename T, int BM, int BN, int WM, int WN, bool ATR, bool BTR, bool DQ8, int RING = 3>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args p, int tiles_m, int tiles_n,
                                                                    uint64_t dq_scale, int64_t dq_nblocks) {
   static_assert(!DQ8 || !BTR, "int8 B is staged as [n][k] rows");
+  static_assert(RING == 3 || (RING == 2 && !DQ8), "three-buffer ring, or two buffers for the plain GEMM");
   constexpr int WNN = BN / WN;         // wavefronts along n
   constexpr int NW = (BM / WM) * WNN;  // wavefronts
   constexpr int FM = WM / 32, FN = WN / 32;  // 32 x 32 accumulators per wavefront along m, n
@@ -330,9 +331,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   constexpr int Q_TILE = DQ8 ? BN * GBK : 16, IPQ = DQ8 ? BN * 4 / 64 / NW : 1, CPT = DQ8 ? BN * 8 / (NW * 64) : 1;
   static_assert(!DQ8 || (IPQ >= 1 && IPA + IPQ <= 16 && CPT * NW * 64 == BN * 8), "int8 copy split");
   // separate LDS objects per buffer, so that reads of one are known not to alias copies into another
-  __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], a2_raw[A_TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], a2_raw[RING == 3 ? A_TILE : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t b0_raw[B_TILE], b1_raw[B_TILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t b2_raw[DQ8 ? Q_TILE : B_TILE];  // DQ8: int8 tile 0
+  __shared__ __attribute__((aligned(1024))) uint8_t b2_raw[DQ8 ? Q_TILE : RING == 3 ? B_TILE : 16];  // DQ8: int8 tile 0
   __shared__ __attribute__((aligned(DQ8 ? 1024 : 16))) uint8_t q1_raw[Q_TILE], q2_raw[Q_TILE];
   HK_L uint8_t* const A0 = (HK_L uint8_t*)a0_raw;
   HK_L uint8_t* const A1 = (HK_L uint8_t*)a1_raw;
@@ -448,7 +449,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   };
   const int k1 = nk > 1 ? 1 : 0, k2 = nk > 2 ? 2 : nk - 1;
   float svq[CPT];  // DQ8: scales of the int8 tile that the next step converts (loaded a step ahead)
-  if constexpr (!DQ8) {
+  if constexpr (!DQ8 && RING == 2) {
+    // step 0; each step then copies the next one into the other buffer and waits for it at its end
+#pragma unroll
+    for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
+#pragma unroll
+    for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
+    __syncthreads();
+  } else if constexpr (!DQ8) {
     // steps 0 and 1 (step min(1, nk - 1): a single-step K re-copies step 0 into a buffer nobody reads)
 #pragma unroll
     for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
@@ -491,9 +499,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   // tile (kt + 1) % 2 (last read in step kt - 1); steps past the end convert a repeat nobody reads.
   auto step = [&](auto bc, auto bq, int kt) {
     constexpr int BUF = decltype(bc)::value;
-    constexpr int NXT = (BUF + 2) % 3;
+    constexpr int NXT = RING == 3 ? (BUF + 2) % 3 : (BUF + 1) % 2;
     constexpr int BB = decltype(bq)::value;  // DQ8: B tile kt % 2
-    const int kn = kt + 2 < nk ? kt + 2 : nk - 1;
+    constexpr int AHEAD = RING - 1;          // steps between a copy and its use
+    const int kn = kt + AHEAD < nk ? kt + AHEAD : nk - 1;
     const HK_G uint8_t* an = Ab + kn * astep;
     const HK_L uint8_t* At = abuf(bc);
     const HK_L uint8_t* Bt = DQ8 ? bbuf(bq) : bbuf(bc);
@@ -533,12 +542,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
       }
     }
     if constexpr (DQ8) barrier_keep_vm_lds<IPA + IPQ>();
-    else barrier_keep_vm<IPA + IPB>();
+    else if constexpr (RING == 3) barrier_keep_vm<IPA + IPB>();
+    else __syncthreads();  // the next step's copies, issued in this one, have landed everywhere
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
-  if constexpr (!DQ8) {
+  if constexpr (!DQ8 && RING == 2) {
+    int kt = 0;
+    for (; kt + 2 <= nk; kt += 2) {
+      step(I0(), I0(), kt);
+      step(I1(), I0(), kt + 1);
+    }
+    if (kt < nk) step(I0(), I0(), kt);
+  } else if constexpr (!DQ8) {
     int kt = 0;
     for (; kt + 3 <= nk; kt += 3) {
       step(I0(), I0(), kt);
@@ -626,17 +643,17 @@ bool mm_dma_ok(const hrt_mm_args& a, int BM, int BN, bool& atr, bool& btr) {
   return (atr ? a.a_sk : a.a_sm) * 2 * (arows + 1) < lim && (btr ? a.b_sk : a.b_sn) * 2 * (brows + 1) < lim;
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN, int RING = 3>
 bool queue_dma(const hrt_mm_args& a, hipStream_t s) {
   bool atr = false, btr = false;
   if (!mm_dma_ok(a, BM, BN, atr, btr)) return false;
   const int tm = (int)(a.M / BM), tn = (int)(a.N / BN);
   const dim3 g((uint32_t)((int64_t)tm * tn * a.batch)), blk((BM / WM) * (BN / WN) * 64);
   const uint64_t ns = 0;
-  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false, false>), g, blk, 0, s, a, tm, tn, ns, 0);
-  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, true, false>), g, blk, 0, s, a, tm, tn, ns, 0);
-  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false, false>), g, blk, 0, s, a, tm, tn, ns, 0);
-  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, true, false>), g, blk, 0, s, a, tm, tn, ns, 0);
+  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, true, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, true, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
   return true;
 }
 
@@ -709,7 +726,12 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int64_t med = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
   const int64_t small = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
   if (small > 0x7fffffffLL) return ctx.fail("GEMM grid too large");
-  // fast path: the largest tile that still gives enough workgroups
+  // fast path: the largest tile that still gives enough workgroups.  256 x 256 tiles (two-buffer ring) copy a
+  // third fewer bytes per flop than 128 x 256 (the copies, not the MFMAs, bound these kernels once the grid
+  // fills the chip) but wait a whole step for each copy: measured 3% faster at K = 2048 (M = 2048, 4096 and
+  // N = 8192), 5% slower at 8192^3
+  if (a.K <= 4096 && a.batch * (a.M / 256) * (a.N / 256) >= 256 && queue_dma<T, 256, 256, 64, 128, 2>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256, 64, 64>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128, 64, 64>(a, ctx.stream))
