@@ -280,6 +280,84 @@ class Bench:
         return {"shape": f"{M}x{K}x{N}", "layout": layout, "bias": bias, "avg_us": round(t * 1e3, 2),
                 "tflops": round(fl / (t * 1e-3) / 1e12, 2), "frac_of_bf16_peak": round(fl / (t * 1e-3) / 1e12 / 2500.0, 4)}
 
+    def mm_ops(self, A, B, C, bias=None, alpha=1.0, beta=0.0, ws=None):
+        """Argument blocks for C = alpha * A @ B + beta * bias on 2-D views (any strides), the way the shim
+        queues them (csrc/shim/ops_mm.cpp: try_gemm): one "mm_mfma_bf16" launch, or, for products too narrow
+        to fill the GPU with 64 x 64 tiles, the split-K pair "mm_mfma_bf16" (fp32 partials into ws) +
+        "mm_reduce_bf16" with the shim's split rule."""
+        abi = self.abi
+        M, K = A.shape
+        N = B.shape[1]
+        m = abi.MmArgs()
+        m.a, m.b, m.c = A.data_ptr(), B.data_ptr(), C.data_ptr()
+        m.M, m.N, m.K, m.batch = M, N, K, 1
+        m.a_sm, m.a_sk, m.b_sk, m.b_sn = A.stride(0), A.stride(1), B.stride(0), B.stride(1)
+        m.c_sm, m.c_sn = C.stride(0), C.stride(1)
+        m.alpha, m.beta = alpha, beta
+        bsm = bsn = 0
+        if bias is not None and beta != 0.0:
+            bsm, bsn = (0, bias.stride(0)) if bias.dim() == 1 else (bias.stride(0), bias.stride(1))
+            m.bias, m.bias_sm, m.bias_sn, m.has_bias = bias.data_ptr(), bsm, bsn, 1
+        tiles = -(-M // 64) * -(-N // 64)
+        S = 1
+        while K % 64 == 0 and min(M, N) <= 64 and tiles * S * 2 <= 256 and (K // 64) % (S * 2) == 0 and K // (S * 2) >= 128:
+            S *= 2
+        if S == 1:
+            return [("mm_mfma_bf16", m)]
+        assert ws is not None and ws.numel() >= S * M * N, "split-K workspace too small"
+        r = abi.MmReduceArgs()
+        r.ws, r.c, r.bias = ws.data_ptr(), m.c, m.bias
+        r.M, r.N, r.splits, r.c_sm, r.c_sn, r.bias_sm, r.bias_sn = M, N, S, m.c_sm, m.c_sn, bsm, bsn
+        r.alpha, r.beta, r.has_bias = alpha, beta, m.has_bias
+        m.K, m.batch = K // S, S
+        m.a_sb, m.b_sb = m.K * m.a_sk, m.K * m.b_sk
+        m.c, m.c_sb, m.c_sm, m.c_sn = ws.data_ptr(), M * N, N, 1
+        m.bias = m.has_bias = m.bias_sm = m.bias_sn = 0
+        m.alpha, m.beta, m.flags = 1.0, 0.0, abi.MM_F32_OUT
+        return [("mm_mfma_bf16", m), ("mm_reduce_bf16", r)]
+
+    def dit_lora_stack(self):
+        """BASELINE C4: the DiT-block linear stack (QKV 2048->6144, out-proj 2048->2048, MLP 2048->8192->2048)
+        at M = 1024 tokens, bf16, frozen base weights with bias and rank-16 LoRA factors.  One step = per layer
+        y = x W^T + b, h = x A^T, y += h B^T (forward) and dx = g W, dB = g^T h, dh = g B, dA = dh^T x,
+        dx += dh A (backward: dX for the base, the four LoRA products), every product queued as the shim
+        queues it.  TFLOP/s counts the base GEMMs (2 x 1.0308e11) plus the LoRA products."""
+        torch = self.torch
+        bf, M, r = torch.bfloat16, 1024, 16
+        layers = [(2048, 6144), (2048, 2048), (2048, 8192), (8192, 2048)]
+        ws = torch.empty(8 * 8192 * 16 * 2, dtype=torch.float32, device=self.dev)  # >= S * M * N of every split product
+        ops, base_ops, keep, flops, base_flops = [], [], [], 0.0, 0.0
+        for li, (fin, fout) in enumerate(layers):
+            x = self.randn((M, fin), bf, 100 + li)
+            W = self.randn((fout, fin), bf, 110 + li, 0.02)
+            b = self.randn((fout,), bf, 120 + li, 0.02)
+            A = self.randn((r, fin), bf, 130 + li, 0.02)
+            Bl = self.randn((fout, r), bf, 140 + li, 0.01)
+            g = self.randn((M, fout), bf, 150 + li)
+            y = torch.empty((M, fout), dtype=bf, device=self.dev)
+            h = torch.empty((M, r), dtype=bf, device=self.dev)
+            dx = torch.empty((M, fin), dtype=bf, device=self.dev)
+            dB = torch.empty((fout, r), dtype=bf, device=self.dev)
+            dh = torch.empty((M, r), dtype=bf, device=self.dev)
+            dA = torch.empty((r, fin), dtype=bf, device=self.dev)
+            keep += [x, W, b, A, Bl, g, y, h, dx, dB, dh, dA]
+            base = [self.mm_ops(x, W.t(), y, b, 1.0, 1.0), self.mm_ops(g, W, dx)]
+            lora = [self.mm_ops(x, A.t(), h, ws=ws), self.mm_ops(h, Bl.t(), y, y, 1.0, 1.0),
+                    self.mm_ops(g.t(), h, dB, ws=ws), self.mm_ops(g, Bl, dh, ws=ws), self.mm_ops(dh.t(), x, dA, ws=ws),
+                    self.mm_ops(dh, A, dx, dx, 1.0, 1.0)]
+            ops += base[0] + lora[0] + lora[1] + base[1] + lora[2] + lora[3] + lora[4] + lora[5]
+            base_ops += base[0] + base[1]
+            base_flops += 2 * (2.0 * M * fin * fout)
+            flops += 2 * (2.0 * M * fin * fout) + 2.0 * M * r * fin * 3 + 2.0 * M * r * fout * 3
+        run = lambda seq: [self.rt.dispatch(n, a) for n, a in seq]  # noqa: E731
+        t = self.time_graph(lambda i: run(ops), 3)
+        tb = self.time_graph(lambda i: run(base_ops), 3)
+        del keep
+        return {"ms": round(t, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 2),
+                "frac_of_bf16_peak": round(flops / (t * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4),
+                "flop": flops, "base_gemms_ms": round(tb, 4), "lora_ms": round(t - tb, 4),
+                "launches": len(ops)}
+
     def dq8_linear(self, M):
         torch, abi = self.torch, self.abi
         N, K = 8192, 2048
@@ -505,6 +583,8 @@ def main():
                         bench.gemm(1024, 1024, 1024, "nn", bias=True)]
         print(f"[bench] gemm {line['gemm']}", file=sys.stderr, flush=True)
         line["dq8_linear"] = [bench.dq8_linear(1024), bench.dq8_linear(4096)]
+        line["dit_lora_stack"] = bench.dit_lora_stack()
+        print(f"[bench] DiT LoRA stack {line['dit_lora_stack']}", file=sys.stderr, flush=True)
         line["softmax_f32_16384x1024"] = bench.softmax()
         line["layer_norm_bf16_1024x2048"] = bench.layer_norm()
         line["dequant_int8_8192x2048_bf16"] = bench.dequant()

@@ -77,6 +77,23 @@ typedef struct hrt_mm_args {
   float alpha, beta;
   uint32_t has_bias, flags;
 } hrt_mm_args;
+/* flags bit for "mm_mfma_{bf16,f16}": c is fp32 and receives alpha * acc + beta * bias unrounded (no
+ * counterpart in the reference: the split-K partial products of "mm_reduce_*"). */
+#define HRT_MM_F32_OUT 1u
+
+/* "mm_reduce_{bf16,f16}" — the second half of a split-K product (no counterpart in the reference, whose
+ * small-N / small-M products run on one workgroup per 64 x 64 tile; composes csrc/ops_mm.cpp:61-175):
+ *   c[m, n] = round(alpha * sum_{s < splits} ws[s, m, n] + beta * bias[m, n])     (bias only if has_bias)
+ * ws: fp32 [splits, M, N] contiguous (the partial products over disjoint K ranges, from "mm_mfma_*" with
+ * HRT_MM_F32_OUT); the splits are summed in order s = 0, 1, ..., so the result is deterministic.  c: strides
+ * (c_sm, c_sn); bias broadcasts through stride 0 like hrt_mm_args. */
+typedef struct hrt_mm_reduce_args {
+  uint64_t ws, c, bias;
+  int64_t M, N, splits;
+  int64_t c_sm, c_sn, bias_sm, bias_sn;
+  float alpha, beta;
+  uint32_t has_bias, pad;
+} hrt_mm_reduce_args;
 
 /* "mm_dq8_{bf16,f16}" — fused int8 weight-only linear (no reference counterpart; composes
  * csrc/ops_quant.cpp:34-59 with csrc/ops_mm.cpp:61-175):

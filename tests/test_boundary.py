@@ -63,6 +63,7 @@ KERNELS = (
     + [f"attn_{op}_mfma_{k}" for op in ("fwd", "dkdv", "dq") for k in ("bf16", "f16")]
     + [f"attn_delta_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_dq8_{k}" for k in ("bf16", "f16")]
+    + [f"mm_reduce_{k}" for k in ("bf16", "f16")]
 )
 
 
@@ -108,7 +109,8 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
 
     structs = {
         "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs,
-        "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_attn_args": abi.AttnArgs,
+        "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_mm_reduce_args": abi.MmReduceArgs,
+        "hrt_attn_args": abi.AttnArgs,
         "hrt_softmax_args": abi.SoftmaxArgs, "hrt_ln_args": abi.LnArgs, "hrt_dq8_args": abi.Dq8Args,
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "hrt_ops.h"', "int main(void) {"]

@@ -209,6 +209,39 @@ def test_large_tile_fast_path_layouts_and_bias(ta, tb, m, k, n):
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
 
 
+# rank-16 LoRA factors of the DiT stack: (M, K, N) with the layouts autograd produces for
+# h = x A^T, y = h B^T, dB = g^T h, dh = g B, dA = dh^T x, dx = dh A (ta / tb: operand given transposed)
+SKINNY = [
+    (1024, 2048, 16, False, True), (1024, 8192, 16, False, True),   # x A^T
+    (1024, 16, 6144, False, True),                                   # h B^T (K = 16: no split)
+    (6144, 1024, 16, True, False), (2048, 1024, 16, True, False),    # g^T h
+    (1024, 8192, 16, False, False), (1024, 2048, 16, False, False),  # g B
+    (16, 1024, 2048, True, False), (16, 1024, 8192, True, False),    # dh^T x
+    (1024, 16, 2048, False, False),                                  # dh A
+    (512, 4096, 512, False, False),                                  # 64 tiles, not one wide: no split
+]
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb", SKINNY)
+def test_skinny_products_split_k(m, k, n, ta, tb):
+    """Products one 64-wide tile across split K over fp32 partials and a second, in-order reduction kernel;
+    checked against the oracle (with addmm's bias, alpha and beta) and for run-to-run identity."""
+    dt = torch.bfloat16
+    a = randn((k, m) if ta else (m, k), dt, 41)
+    b = randn((n, k) if tb else (k, n), dt, 42)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), dt, 43)
+    out = torch.addmm(bias.to(dev), A, B, alpha=0.75, beta=1.25)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.75, 1.25)
+    check(out, ref, dt, k)
+    assert oracle.rel_l2(f64(out), ref) <= 1e-2
+    out2 = torch.addmm(bias.to(dev), A, B, alpha=0.75, beta=1.25)
+    assert torch.equal(out.cpu(), out2.cpu())
+    plain = torch.mm(A, B)
+    assert oracle.rel_l2(f64(plain), oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), None, 1.0, 0.0)) <= 1e-2
+
+
 def test_tile_aligned_fast_path_batched_and_full_bias():
     bt, m, k, n = 2, 1024, 128, 6144
     a, b = randn((bt, m, k), torch.bfloat16, 16), randn((bt, k, n), torch.bfloat16, 17)

@@ -95,7 +95,7 @@ bool mm_check_operands(const hrt_mm_args& a, uint64_t elem, hrt::LaunchCtx& ctx)
   const int64_t sc[3] = {a.batch, a.M, a.N}, tc[3] = {a.c_sb, a.c_sm, a.c_sn};
   const int64_t tbias[3] = {a.bias_sb, a.bias_sm, a.bias_sn};
   if (!ctx.check(a.a, hrt::span_bytes(3, sa, ta, elem), "a") || !ctx.check(a.b, hrt::span_bytes(3, sb, tb, elem), "b") ||
-      !ctx.check(a.c, hrt::span_bytes(3, sc, tc, elem), "c") ||
+      !ctx.check(a.c, hrt::span_bytes(3, sc, tc, (a.flags & HRT_MM_F32_OUT) ? 4 : elem), "c") ||
       (a.has_bias && !ctx.check(a.bias, hrt::span_bytes(3, sc, tbias, elem), "bias")))
     return false;
   return true;
@@ -106,6 +106,7 @@ namespace {
 template <typename T>
 bool launch_mm_fma(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_mm_args*>(p);
+  if (a.flags != 0) return ctx.fail("the FMA GEMM takes no flags");
   if (!mm_check_operands(a, sizeof(typename T::storage), ctx)) return false;
   if (cdiv(a.M, BM) > 65535) return ctx.fail("M too large for the FMA kernel grid");
   const dim3 grid((uint32_t)cdiv(a.N, BN), (uint32_t)cdiv(a.M, BM), (uint32_t)a.batch);

@@ -213,29 +213,75 @@ __device__ __forceinline__ void gemm_mainloop(LA& la, LB& lb, int64_t K, uint16_
 
 // Epilogue: c = alpha * acc + beta * bias, one rounding; lane holds rows 4*(lane/16)+r, column lane%16
 // of every 16x16 tile.
+// Epilogue: alpha * acc + beta * bias, one rounding (f32out: C is fp32 and takes the unrounded value, the
+// split-K partials of HRT_MM_F32_OUT).  Each wavefront's WTM x WTN block goes through LDS in 32-column
+// chunks so that a lane writes 8 consecutive outputs of a row (one 16-byte store when C's row is contiguous
+// and aligned) instead of 2-byte stores scattered over 4 rows.
+constexpr int EPI_RS = 36;  // floats per LDS row of a chunk (conflict-free writes, 16-byte aligned rows)
 template <typename T, int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void gemm_epilogue(const f32x4 (&acc)[BM / WM / 16][BN / WN / 16], HK_G uint16_t* C, int64_t c_sm,
                                               int64_t c_sn, const HK_G uint16_t* bias, int64_t bias_sm, int64_t bias_sn,
                                               bool has_bias, float alpha, float beta, int64_t m0, int64_t n0, int64_t M,
-                                              int64_t N) {
+                                              int64_t N, uint16_t (*lds)[(BM + BN) * LDK], bool f32out = false) {
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 16, TN = WTN / 16;
+  static_assert(WTN % 32 == 0 && WM * WN * WTM * EPI_RS * 4 <= 2 * (BM + BN) * LDK * 2, "epilogue chunks fit the tiles");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int fr = lane & 15;
+  float* const area = reinterpret_cast<float*>(&lds[0][0]) + wave * WTM * EPI_RS;
+  __syncthreads();  // every wavefront is done with the K loop's tiles
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  for (int jc = 0; jc < WTN / 32; ++jc) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t gn = n0 + wn * WTN + j * 16 + fr;
-      if (gn >= N) continue;
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t gm = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
-        if (gm >= M) continue;
-        float o = alpha * acc[i][j][r];
-        if (has_bias) o += beta * T::to_f32(bias[gm * bias_sm + gn * bias_sn]);
-        C[gm * c_sm + gn * c_sn] = T::from_f32(o);
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          area[(i * 16 + (lane >> 4) * 4 + r) * EPI_RS + jj * 16 + (lane & 15)] = acc[i][2 * jc + jj][r];
+    // WTM rows x 4 pieces of 8 columns; LDS reads and writes of one wavefront complete in order
+#pragma unroll
+    for (int ps = 0; ps < WTM / 16; ++ps) {
+      const int q = ps * 64 + lane, row = q >> 2, c8 = (q & 3) * 8;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(area + row * EPI_RS + c8);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(area + row * EPI_RS + c8 + 4);
+      const int64_t gm = m0 + wm * WTM + row, gn = n0 + wn * WTN + jc * 32 + c8;
+      if (gm >= M || gn >= N) continue;
+      float o[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+      const bool full = gn + 8 <= N;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= alpha;
+      if (has_bias) {
+        const HK_G uint16_t* bp = bias + gm * bias_sm + gn * bias_sn;
+        if (full && bias_sn == 1 && ((uint64_t)bp & 15) == 0) {  // one 16-byte load of the bias row
+          const u32x4 bv = *reinterpret_cast<const HK_G u32x4*>(bp);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) o[2 * w] += beta * lo16<T>(bv[w]), o[2 * w + 1] += beta * hi16<T>(bv[w]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (full || gn + e < N) o[e] += beta * T::to_f32(bp[e * bias_sn]);
+        }
+      }
+      if (f32out) {
+        HK_G float* c = reinterpret_cast<HK_G float*>(C) + gm * c_sm + gn * c_sn;
+        if (full && c_sn == 1 && ((uint64_t)c & 15) == 0) {
+          *reinterpret_cast<HK_G f32x4*>(c) = f32x4{o[0], o[1], o[2], o[3]};
+          *reinterpret_cast<HK_G f32x4*>(c + 4) = f32x4{o[4], o[5], o[6], o[7]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gn + e < N) c[e * c_sn] = o[e];
+        }
+      } else {
+        HK_G uint16_t* c = C + gm * c_sm + gn * c_sn;
+        if (full && c_sn == 1 && ((uint64_t)c & 15) == 0) {
+          *reinterpret_cast<HK_G u32x4*>(c) = u32x4{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3]), pack2<T>(o[4], o[5]), pack2<T>(o[6], o[7])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gn + e < N) c[e * c_sn] = T::from_f32(o[e]);
+        }
       }
     }
   }
@@ -257,9 +303,11 @@ __global__ __launch_bounds__(256) void mm_mfma(hrt_mm_args p, int64_t tiles_m, i
   lb.s_r = p.b_sn, lb.s_k = p.b_sk, lb.r0 = n0, lb.nrows = p.N, lb.nk = p.K;
   f32x4 acc[BM / WM / 16][BN / WN / 16];
   gemm_mainloop<T, BM, BN, WM, WN>(la, lb, p.K, lds, acc);
-  gemm_epilogue<T, BM, BN, WM, WN>(acc, gptr<uint16_t>(p.c) + bz * p.c_sb, p.c_sm, p.c_sn,
-                                   gcptr<uint16_t>(p.bias) + bz * p.bias_sb, p.bias_sm, p.bias_sn,
-                                   p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N);
+  const bool f32out = (p.flags & HRT_MM_F32_OUT) != 0;
+  HK_G uint16_t* const C = f32out ? reinterpret_cast<HK_G uint16_t*>(gptr<float>(p.c) + bz * p.c_sb)
+                                  : gptr<uint16_t>(p.c) + bz * p.c_sb;
+  gemm_epilogue<T, BM, BN, WM, WN>(acc, C, p.c_sm, p.c_sn, gcptr<uint16_t>(p.bias) + bz * p.bias_sb, p.bias_sm,
+                                   p.bias_sn, p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N, lds, f32out);
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int AMODE>
@@ -278,7 +326,7 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
   f32x4 acc[BM / WM / 16][BN / WN / 16];
   gemm_mainloop<T, BM, BN, WM, WN>(la, lb, p.K, lds, acc);
   gemm_epilogue<T, BM, BN, WM, WN>(acc, gptr<uint16_t>(p.y), p.N, 1, gcptr<uint16_t>(p.bias), 0,
-                                   1, p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N);
+                                   1, p.has_bias != 0, p.alpha, p.beta, m0, n0, p.M, p.N, lds);
 }
 
 // ---- fast path: tile-aligned GEMMs, operands copied global -> LDS directly ------------------------------------
@@ -720,6 +768,8 @@ template <typename T>
 bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_mm_args*>(pp);
   if (!mm_check_operands(a, 2, ctx)) return false;
+  if (a.flags & ~HRT_MM_F32_OUT) return ctx.fail("unknown GEMM flags");
+  const bool f32out = (a.flags & HRT_MM_F32_OUT) != 0;
   const int am = pick_mode(a.a, a.a_sb, a.a_sm, a.a_sk, a.M, a.K, a.batch);
   const int bm = pick_mode(a.b, a.b_sb, a.b_sn, a.b_sk, a.N, a.K, a.batch);
   const int64_t big = cdiv(a.M, 128) * cdiv(a.N, 256) * a.batch;
@@ -730,13 +780,14 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   // third fewer bytes per flop than 128 x 256 (the copies, not the MFMAs, bound these kernels once the grid
   // fills the chip) but wait a whole step for each copy: measured 3% faster at K = 2048 (M = 2048, 4096 and
   // N = 8192), 5% slower at 8192^3
-  if (a.K <= 4096 && a.batch * (a.M / 256) * (a.N / 256) >= 256 && queue_dma<T, 256, 256, 64, 128, 2>(a, ctx.stream))
+  if (!f32out && a.K <= 4096 && a.batch * (a.M / 256) * (a.N / 256) >= 256 &&
+      queue_dma<T, 256, 256, 64, 128, 2>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
-  if (a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256, 64, 64>(a, ctx.stream))
+  if (!f32out && a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256, 64, 64>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
-  if (a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128, 64, 64>(a, ctx.stream))
+  if (!f32out && a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128, 64, 64>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
-  if (a.batch * (a.M / 64) * (a.N / 64) >= 128 && queue_dma<T, 64, 64, 32, 32>(a, ctx.stream))
+  if (!f32out && a.batch * (a.M / 64) * (a.N / 64) >= 128 && queue_dma<T, 64, 64, 32, 32>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (am == GATHER || bm == GATHER) {
     dispatch_gather<T>(a, am, bm, ctx.stream);
@@ -815,7 +866,62 @@ bool launch_mm_dq8(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   return hrt::launch_ok(hipGetLastError(), ctx, "mm_dq8");
 }
 
+// ---- split-K reduction: c = round(alpha * sum_s ws[s] + beta * bias), splits summed in order ---------------
+// Four consecutive outputs (of the flattened [M, N]) per thread, read as 16-byte pieces of each split when
+// M N is a multiple of 4; the loads of eight splits are in flight together.
+template <typename T>
+__global__ __launch_bounds__(256) void mm_reduce(hrt_mm_reduce_args p) {
+  const int64_t total = p.M * p.N;
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i0 >= total) return;
+  const HK_G float* w = gcptr<float>(p.ws);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  if (total % 4 == 0) {
+    int64_t k = 0;
+    for (; k + 8 <= p.splits; k += 8) {
+      f32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const HK_G f32x4*>(w + (k + u) * total + i0);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; k < p.splits; ++k) s += *reinterpret_cast<const HK_G f32x4*>(w + k * total + i0);
+  } else {
+    for (int64_t k = 0; k < p.splits; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i0 + e < total) s[e] += w[k * total + i0 + e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t i = i0 + e;
+    if (i >= total) break;
+    const int64_t m = i / p.N, n = i % p.N;
+    float o = p.alpha * s[e];
+    if (p.has_bias) o += p.beta * T::to_f32(gcptr<uint16_t>(p.bias)[m * p.bias_sm + n * p.bias_sn]);
+    gptr<uint16_t>(p.c)[m * p.c_sm + n * p.c_sn] = T::from_f32(o);
+  }
+}
+
+template <typename T>
+bool launch_mm_reduce(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_mm_reduce_args*>(pp);
+  if (a.M <= 0 || a.N <= 0 || a.splits <= 0) return ctx.fail("empty split-K reduction");
+  if (a.c_sm < 0 || a.c_sn < 0 || a.bias_sm < 0 || a.bias_sn < 0) return ctx.fail("negative stride");
+  const int64_t total = a.M * a.N;
+  if (cdiv(total, 1024) > 0x7fffffffLL) return ctx.fail("reduction grid too large");
+  const int64_t sw[3] = {a.splits, a.M, a.N}, tw[3] = {a.M * a.N, a.N, 1};
+  const int64_t sc[2] = {a.M, a.N}, tc[2] = {a.c_sm, a.c_sn}, tb[2] = {a.bias_sm, a.bias_sn};
+  if (!ctx.check(a.ws, hrt::span_bytes(3, sw, tw, 4), "ws") || !ctx.check(a.c, hrt::span_bytes(2, sc, tc, 2), "c") ||
+      (a.has_bias && !ctx.check(a.bias, hrt::span_bytes(2, sc, tb, 2), "bias")))
+    return false;
+  hipLaunchKernelGGL(mm_reduce<T>, dim3((uint32_t)cdiv(total, 1024)), dim3(256), 0, ctx.stream, a);
+  return hrt::launch_ok(hipGetLastError(), ctx, "mm_reduce");
+}
+
 HRT_REGISTER("mm_mfma_bf16", hrt_mm_args, launch_mm_mfma<BF16>);
+HRT_REGISTER("mm_reduce_bf16", hrt_mm_reduce_args, launch_mm_reduce<BF16>);
+HRT_REGISTER("mm_reduce_f16", hrt_mm_reduce_args, launch_mm_reduce<F16>);
 HRT_REGISTER("mm_mfma_f16", hrt_mm_args, launch_mm_mfma<F16>);
 HRT_REGISTER("mm_dq8_bf16", hrt_mm_dq8_args, launch_mm_dq8<BF16>);
 HRT_REGISTER("mm_dq8_f16", hrt_mm_dq8_args, launch_mm_dq8<F16>);

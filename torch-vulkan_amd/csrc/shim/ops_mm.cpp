@@ -95,6 +95,52 @@ std::optional<at::Tensor> try_gemm(const at::Tensor& a, const at::Tensor& b, con
       use_mfma = idx >= g_coop_lo.load() && idx < g_coop_hi.load();
     }
   }
+  // Split-K for products one 64-wide tile across (the rank-16 LoRA factors: M or N = 16 with K = 1024 .. 8192
+  // run on 16 - 128 workgroups otherwise; wider products keep one K order, so that e.g. the fused int8 linear
+  // stays bit-identical to dequant + mm): the K range is split over the batch
+  // dimension of the matrix-core kernel, which writes fp32 partial products into a workspace, and
+  // "mm_reduce_*" sums the splits in order (deterministic), applies alpha / beta * bias and rounds once.
+  if (use_mfma && !batched && K % 64 == 0 && std::min(M, N) <= 64) {
+    const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
+    const int64_t kblocks = K / 64;
+    int64_t S = 1;
+    // up to one workgroup per CU, K slices of at least 128 (more splits measured slower: every split adds a
+    // workgroup prologue and an fp32 partial of the output)
+    while (tiles * S * 2 <= 256 && kblocks % (S * 2) == 0 && K / (S * 2) >= 128) S *= 2;
+    if (S >= 2) {
+      at::Tensor ws = at::empty({S, M, N}, a.options().dtype(at::kFloat));
+      hrt_mm_reduce_args R{};
+      R.ws = addr_of(ws);
+      R.c = P.c;
+      R.bias = P.bias;
+      R.M = M;
+      R.N = N;
+      R.splits = S;
+      R.c_sm = N;
+      R.c_sn = 1;
+      R.bias_sm = P.bias_sm;
+      R.bias_sn = P.bias_sn;
+      R.alpha = P.alpha;
+      R.beta = P.beta;
+      R.has_bias = P.has_bias;
+      P.K = K / S;
+      P.batch = S;
+      P.a_sb = P.K * P.a_sk;
+      P.b_sb = P.K * P.b_sk;
+      P.c = R.ws;
+      P.c_sb = M * N;
+      P.has_bias = 0;
+      P.bias = 0;
+      P.bias_sm = P.bias_sn = 0;
+      P.alpha = 1.f;
+      P.beta = 0.f;
+      P.flags = HRT_MM_F32_OUT;
+      launch(std::string("mm_mfma_") + kind, P);
+      launch(std::string("mm_reduce_") + kind, R);
+      count_kernel(aten_name);
+      return out;
+    }
+  }
   launch(std::string(use_mfma ? "mm_mfma_" : "mm_") + kind, P);
   count_kernel(aten_name);
   return out;

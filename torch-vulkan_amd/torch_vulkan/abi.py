@@ -14,6 +14,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhrt.so"
 MAX_DIMS = 8
 F32, BF16, F16, RAW8, RAW16, RAW32, RAW64 = range(7)
 ATTN_O_F32 = 1
+MM_F32_OUT = 1  # hrt_mm_args.flags: fp32 output (split-K partials)
 ATTN_DQ_DELTA = 2
 
 u64, i64, i32, u32, f32 = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float
@@ -38,6 +39,12 @@ class MmArgs(ctypes.Structure):
                 ("a_sb", i64), ("a_sm", i64), ("a_sk", i64), ("b_sb", i64), ("b_sk", i64), ("b_sn", i64),
                 ("c_sb", i64), ("c_sm", i64), ("c_sn", i64), ("bias_sb", i64), ("bias_sm", i64), ("bias_sn", i64),
                 ("alpha", f32), ("beta", f32), ("has_bias", u32), ("flags", u32)]
+
+
+class MmReduceArgs(ctypes.Structure):
+    _fields_ = [("ws", u64), ("c", u64), ("bias", u64), ("M", i64), ("N", i64), ("splits", i64), ("c_sm", i64),
+                ("c_sn", i64), ("bias_sm", i64), ("bias_sn", i64), ("alpha", f32), ("beta", f32), ("has_bias", u32),
+                ("pad", u32)]
 
 
 class MmDq8Args(ctypes.Structure):
