@@ -91,6 +91,14 @@ int hrt_kernel_index(const char* name);
  * Replaces `vkrt_dispatch` (csrc/vkrt.h:22). */
 int hrt_dispatch(uint32_t kernel, const void* args, uint32_t len, uint32_t gx, uint32_t gy, uint32_t gz);
 
+/* Queue n operator kernels in order, each exactly as hrt_dispatch(kernels[i], args[i], lens[i], 0, 0, 0).
+ * Returns 0 when all are queued; at the first rejected one it stops and returns -(i + 1) with the error
+ * set (the ones before it stay queued).  No counterpart function in the reference, whose runtime records
+ * its dispatches into command buffers and submits them together (vkrt/src/lib.rs:542-561): this is the
+ * batched launch for HIP, one call for a sequence of launches, so that the caller's per-call cost (a
+ * Python binding, for instance) does not stall the stream between short kernels. */
+int hrt_dispatch_batch(const uint32_t* kernels, const void* const* args, const uint32_t* lens, uint32_t n);
+
 /* Wait until all queued work has finished.  Replaces `vkrt_synchronize` (csrc/vkrt.h:23). */
 int hrt_synchronize(void);
 

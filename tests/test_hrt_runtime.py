@@ -129,6 +129,45 @@ def test_out_of_range_operands_are_rejected_before_launch(hrt):
     assert hrt.hrt_free(a) == -1
 
 
+def test_dispatch_batch_queues_in_order_and_stops_at_a_rejected_launch(hrt):
+    """hrt_dispatch_batch: every launch as hrt_dispatch; the first rejected one stops the batch with
+    -(index + 1) and the launches before it stay queued."""
+    u32, vp = ctypes.c_uint32, ctypes.c_void_p
+    hrt.hrt_dispatch_batch.argtypes = [ctypes.POINTER(u32), ctypes.POINTER(vp), ctypes.POINTER(u32), u32]
+    q = hrt.hrt_alloc(64)
+    sc = hrt.hrt_alloc(2)
+    outs = [hrt.hrt_alloc(128) for _ in range(2)]
+    small = hrt.hrt_alloc(64)
+    qv = np.arange(-32, 32, dtype=np.int8)
+    assert hrt.hrt_upload(q, qv.ctypes.data, 64) == 0
+    one = np.array([0x3F80], dtype=np.uint16)  # bf16 1.0
+    assert hrt.hrt_upload(sc, one.ctypes.data, 2) == 0
+    kd = hrt.hrt_kernel_index(b"dq8_bf16")
+    blocks = [np.array([q, sc, o, 1, 64, 1], dtype=np.int64) for o in outs + [small]]
+    ids = (u32 * 3)(kd, kd, kd)
+    ptrs = (vp * 3)(*[b.ctypes.data for b in blocks])
+    lens = (u32 * 3)(48, 48, 48)
+    assert hrt.hrt_dispatch_batch(ids, ptrs, lens, 2) == 0, err(hrt)
+    assert hrt.hrt_synchronize() == 0
+    for o in outs:
+        got = np.zeros(64, np.uint16)
+        assert hrt.hrt_download(got.ctypes.data, o, 128) == 0
+        f = (got.astype(np.uint32) << 16).view(np.float32)
+        assert np.array_equal(f, qv.astype(np.float32))
+    # third block writes 128 bytes into a 64-byte block: rejected, batch stops at index 2
+    zero = np.zeros(64, np.uint16)
+    assert hrt.hrt_upload(outs[0], zero.ctypes.data, 128) == 0
+    ids2 = (u32 * 3)(kd, kd, kd)
+    ptrs2 = (vp * 3)(blocks[0].ctypes.data, blocks[2].ctypes.data, blocks[1].ctypes.data)
+    assert hrt.hrt_dispatch_batch(ids2, ptrs2, lens, 3) == -2 and "out" in err(hrt)
+    assert hrt.hrt_synchronize() == 0
+    got = np.zeros(64, np.uint16)
+    assert hrt.hrt_download(got.ctypes.data, outs[0], 128) == 0
+    assert np.array_equal((got.astype(np.uint32) << 16).view(np.float32), qv.astype(np.float32))
+    for p in [q, sc, small] + outs:
+        assert hrt.hrt_free(p) == 0
+
+
 def test_allocation_above_device_limit_fails(hrt):
     assert hrt.hrt_alloc(hrt.hrt_max_alloc() + 1) == 0
 

@@ -392,6 +392,16 @@ int hrt_dispatch(uint32_t kernel, const void* args, uint32_t len, uint32_t gx, u
   return 0;
 }
 
+int hrt_dispatch_batch(const uint32_t* kernels, const void* const* args, const uint32_t* lens, uint32_t n) {
+  if (n && (!kernels || !args || !lens)) {
+    set_error("hrt_dispatch_batch: null array");
+    return -1;
+  }
+  for (uint32_t i = 0; i < n; ++i)
+    if (hrt_dispatch(kernels[i], args[i], lens[i], 0, 0, 0) != 0) return -(int)(i + 1);
+  return 0;
+}
+
 int hrt_synchronize(void) {
   Runtime* rt = rt_or_error();
   if (!rt) return -1;

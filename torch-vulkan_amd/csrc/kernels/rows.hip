@@ -66,7 +66,7 @@ __device__ __forceinline__ float ld(const typename T::storage* p, int64_t i) {
 }
 
 // ================================ softmax ================================================================
-template <typename T, int NV>
+template <typename T, int NV, bool FULL>
 __global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage* __restrict__ x,
                                                        typename T::storage* __restrict__ y, int64_t rows, int64_t R,
                                                        uint32_t safe) {
@@ -81,12 +81,12 @@ __global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < R) raw[c] = rd_nt(xr + col);  // every load in flight before the first use
+    if ((FULL || col < R)) raw[c] = rd_nt(xr + col);  // every load in flight before the first use
   }
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < R) {
+    if ((FULL || col < R)) {
       Vec<T>::unpack(raw[c], v[c]);
 #pragma unroll
       for (int e = 0; e < V; ++e) m = fmaxf(m, v[c][e]);
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < R) {
+    if ((FULL || col < R)) {
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         v[c][e] = __builtin_amdgcn_exp2f(fmaf(v[c][e], kL2e, nm));
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < R) {
+    if ((FULL || col < R)) {
 #pragma unroll
       for (int e = 0; e < V; ++e) v[c][e] = zero ? 0.f : v[c][e] * inv;
       wr_nt(yr + col, Vec<T>::pack(v[c]));
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void softmax_fwd_reg(const typename T::storage
   }
 }
 
-template <typename T, int NV>
+template <typename T, int NV, bool FULL>
 __global__ __launch_bounds__(256) void softmax_bwd_reg(const typename T::storage* __restrict__ y,
                                                        const typename T::storage* __restrict__ g,
                                                        typename T::storage* __restrict__ dx, int64_t rows, int64_t R) {
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void softmax_bwd_reg(const typename T::storage
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < R) {
+    if ((FULL || col < R)) {
       ry[c] = rd_nt(y + row * R + col);
       rg[c] = rd_nt(g + row * R + col);
     }
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void softmax_bwd_reg(const typename T::storage
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < R) {
+    if ((FULL || col < R)) {
       Vec<T>::unpack(ry[c], yv[c]);
       Vec<T>::unpack(rg[c], gv[c]);
 #pragma unroll
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void softmax_bwd_reg(const typename T::storage
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < R) {
+    if ((FULL || col < R)) {
 #pragma unroll
       for (int e = 0; e < V; ++e) yv[c][e] = yv[c][e] * (gv[c][e] - d);
       wr_nt(dx + row * R + col, Vec<T>::pack(yv[c]));
@@ -266,12 +266,13 @@ bool launch_softmax_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   S* y = (S*)a.y;
   if (a.inner == 1) {
     const int nv = reg_nv<T>(a.R, {a.x, a.y});
+  const auto full_row = [&](int v) { return a.R == (int64_t)v * 64 * Vec<T>::N; };  // rows fill every chunk: no column guards
     const dim3 g((uint32_t)cdiv(a.outer, 4));
     switch (nv) {
-      case 1: hipLaunchKernelGGL((softmax_fwd_reg<T, 1>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
-      case 2: hipLaunchKernelGGL((softmax_fwd_reg<T, 2>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
-      case 4: hipLaunchKernelGGL((softmax_fwd_reg<T, 4>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
-      case 8: hipLaunchKernelGGL((softmax_fwd_reg<T, 8>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      case 1: if (full_row(1)) hipLaunchKernelGGL((softmax_fwd_reg<T, 1, true>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); else hipLaunchKernelGGL((softmax_fwd_reg<T, 1, false>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      case 2: if (full_row(2)) hipLaunchKernelGGL((softmax_fwd_reg<T, 2, true>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); else hipLaunchKernelGGL((softmax_fwd_reg<T, 2, false>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      case 4: if (full_row(4)) hipLaunchKernelGGL((softmax_fwd_reg<T, 4, true>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); else hipLaunchKernelGGL((softmax_fwd_reg<T, 4, false>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
+      case 8: if (full_row(8)) hipLaunchKernelGGL((softmax_fwd_reg<T, 8, true>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); else hipLaunchKernelGGL((softmax_fwd_reg<T, 8, false>), g, dim3(256), 0, ctx.stream, x, y, a.outer, a.R, a.safe); break;
       default:
         hipLaunchKernelGGL(softmax_fwd_row<T>, dim3((uint32_t)a.outer), dim3(256), 0, ctx.stream, x, y, a.R, a.safe);
     }
@@ -294,12 +295,13 @@ bool launch_softmax_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const S *y = (const S*)a.y, *g = (const S*)a.g;
   S* dx = (S*)a.dx;
   const int nv = a.inner == 1 ? reg_nv<T>(a.R, {a.y, a.g, a.dx}) : 0;
+  const auto full_row = [&](int v) { return a.R == (int64_t)v * 64 * Vec<T>::N; };  // rows fill every chunk: no column guards
   const dim3 g4((uint32_t)cdiv(a.outer, 4));
   switch (nv) {
-    case 1: hipLaunchKernelGGL((softmax_bwd_reg<T, 1>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
-    case 2: hipLaunchKernelGGL((softmax_bwd_reg<T, 2>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
-    case 4: hipLaunchKernelGGL((softmax_bwd_reg<T, 4>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
-    case 8: hipLaunchKernelGGL((softmax_bwd_reg<T, 8>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    case 1: if (full_row(1)) hipLaunchKernelGGL((softmax_bwd_reg<T, 1, true>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); else hipLaunchKernelGGL((softmax_bwd_reg<T, 1, false>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    case 2: if (full_row(2)) hipLaunchKernelGGL((softmax_bwd_reg<T, 2, true>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); else hipLaunchKernelGGL((softmax_bwd_reg<T, 2, false>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    case 4: if (full_row(4)) hipLaunchKernelGGL((softmax_bwd_reg<T, 4, true>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); else hipLaunchKernelGGL((softmax_bwd_reg<T, 4, false>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
+    case 8: if (full_row(8)) hipLaunchKernelGGL((softmax_bwd_reg<T, 8, true>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); else hipLaunchKernelGGL((softmax_bwd_reg<T, 8, false>), g4, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R); break;
     default: {
       const dim3 grid(a.inner == 1 ? (uint32_t)a.outer : (uint32_t)cdiv(a.outer * a.inner, 256));
       hipLaunchKernelGGL(softmax_bwd_generic<T>, grid, dim3(256), 0, ctx.stream, y, g, dx, a.outer, a.R, a.inner);
@@ -309,7 +311,7 @@ bool launch_softmax_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
 }
 
 // ================================ layer_norm ============================================================
-template <typename T, int NV>
+template <typename T, int NV, bool FULL>
 __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __restrict__ x,
                                                   typename T::storage* __restrict__ y, float* __restrict__ mean_out,
                                                   float* __restrict__ rstd_out, const typename T::storage* __restrict__ w,
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < D) {
+    if ((FULL || col < D)) {
       rx[c] = rd_nt(x + row * D + col);
       if (w) rw[c] = rd(w + col);
       if (b) rb[c] = rd(b + col);
@@ -335,7 +337,7 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < D) {
+    if ((FULL || col < D)) {
       Vec<T>::unpack(rx[c], v[c]);
 #pragma unroll
       for (int e = 0; e < V; ++e) s += v[c][e];
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < D) {
+    if ((FULL || col < D)) {
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         const float d = v[c][e] - mean;
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (col < D) {
+    if ((FULL || col < D)) {
       float wv[V], bv[V];
       if (w) Vec<T>::unpack(rw[c], wv);
       if (b) Vec<T>::unpack(rb[c], bv);
@@ -411,7 +413,7 @@ __global__ __launch_bounds__(256) void ln_fwd_row(const typename T::storage* __r
 // Backward, register path: workgroup = one chunk of 4 rows, one wavefront per row.  dx per row; the
 // per-column partial sums of g*xhat and g of the 4 rows are combined through LDS (every wavefront stores
 // its row, then each thread sums the 4 rows of its columns) and written as one ws row pair per chunk.
-template <typename T, int NV>
+template <typename T, int NV, bool FULL>
 __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __restrict__ x,
                                                   const typename T::storage* __restrict__ g,
                                                   const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (live && col < D) {
+    if (live && (FULL || col < D)) {
       rx[c] = rd_nt(x + row * D + col);
       rg[c] = rd_nt(g + row * D + col);
       if (w) rw[c] = rd(w + col);
@@ -442,7 +444,7 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (live && col < D) {
+    if (live && (FULL || col < D)) {
       float wv[V];
       Vec<T>::unpack(rx[c], xh[c]);
       Vec<T>::unpack(rg[c], gv[c]);
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
       const int64_t col = (int64_t)(c * 64 + lane) * V;
-      if (col < D) {
+      if ((FULL || col < D)) {
         float wv[V], o[V];
         if (w) Vec<T>::unpack(rw[c], wv);
 #pragma unroll
@@ -486,7 +488,7 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
       const int64_t col = (int64_t)(c * 64 + lane) * V;
-      if (col < D) {
+      if ((FULL || col < D)) {
         float o[V];
 #pragma unroll
         for (int e = 0; e < V; ++e) o[e] = qn ? gv[c][e] : gv[c][e] * xh[c][e];
@@ -591,12 +593,13 @@ bool launch_ln_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   S* y = (S*)a.y;
   float *mu = (float*)a.mean, *rs = (float*)a.rstd;
   const int nv = reg_nv<T>(a.D, {a.x, a.y, a.w, a.b});
+  const auto full_row = [&](int v) { return a.D == (int64_t)v * 64 * Vec<T>::N; };  // rows fill every chunk: no column guards
   const dim3 g4((uint32_t)cdiv(a.rows, 4));
   switch (nv) {
-    case 1: hipLaunchKernelGGL((ln_fwd_reg<T, 1>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
-    case 2: hipLaunchKernelGGL((ln_fwd_reg<T, 2>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
-    case 4: hipLaunchKernelGGL((ln_fwd_reg<T, 4>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
-    case 8: hipLaunchKernelGGL((ln_fwd_reg<T, 8>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 1: if (full_row(1)) hipLaunchKernelGGL((ln_fwd_reg<T, 1, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 1, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 2: if (full_row(2)) hipLaunchKernelGGL((ln_fwd_reg<T, 2, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 2, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 4: if (full_row(4)) hipLaunchKernelGGL((ln_fwd_reg<T, 4, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 4, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 8: if (full_row(8)) hipLaunchKernelGGL((ln_fwd_reg<T, 8, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 8, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
     default:
       hipLaunchKernelGGL(ln_fwd_row<T>, dim3((uint32_t)a.rows), dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.D, a.eps);
   }
@@ -621,14 +624,15 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   float* ws = (float*)a.ws;
   const float *mu = (const float*)a.mean, *rs = (const float*)a.rstd;
   int nv = reg_nv<T>(a.D, {a.x, a.g, a.w, a.dx});
+  const auto full_row = [&](int v) { return a.D == (int64_t)v * 64 * Vec<T>::N; };  // rows fill every chunk: no column guards
   const size_t lds = ws ? (size_t)(4 * a.D) * 4 : 0;
   if (lds > 64 * 1024 || a.D % 4) nv = 0;
   const dim3 grid((uint32_t)chunks);
   switch (nv) {
-    case 1: hipLaunchKernelGGL((ln_bwd_reg<T, 1>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
-    case 2: hipLaunchKernelGGL((ln_bwd_reg<T, 2>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
-    case 4: hipLaunchKernelGGL((ln_bwd_reg<T, 4>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
-    case 8: hipLaunchKernelGGL((ln_bwd_reg<T, 8>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 1: if (full_row(1)) hipLaunchKernelGGL((ln_bwd_reg<T, 1, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 1, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 2: if (full_row(2)) hipLaunchKernelGGL((ln_bwd_reg<T, 2, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 2, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 4: if (full_row(4)) hipLaunchKernelGGL((ln_bwd_reg<T, 4, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 4, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 8: if (full_row(8)) hipLaunchKernelGGL((ln_bwd_reg<T, 8, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 8, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
     default: hipLaunchKernelGGL(ln_bwd_row<T>, grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
   }
   return hrt::launch_ok(hipGetLastError(), ctx, "ln_bwd");

@@ -103,6 +103,7 @@ class Runtime:
             "hrt_copy_d2d": (ctypes.c_int, [u64, u64, u64]),
             "hrt_kernel_index": (ctypes.c_int, [cp]),
             "hrt_dispatch": (ctypes.c_int, [u32, vp, u32, u32, u32, u32]),
+            "hrt_dispatch_batch": (ctypes.c_int, [ctypes.POINTER(u32), ctypes.POINTER(vp), ctypes.POINTER(u32), u32]),
             "hrt_synchronize": (ctypes.c_int, []),
             "hrt_empty_cache": (sz, []),
             "hrt_reserved_bytes": (u64, []),
@@ -148,6 +149,21 @@ class Runtime:
     def dispatch(self, name, args):
         """Queue operator kernel `name` with a Structure argument block (the kernel sizes its own grid)."""
         self.check(self.lib.hrt_dispatch(self.kernel(name), ctypes.byref(args), ctypes.sizeof(args), 0, 0, 0), name)
+
+    def batch(self, pairs):
+        """A prepared sequence of (kernel name, Structure) launches for run_batch (keeps the blocks alive)."""
+        n = len(pairs)
+        vp = ctypes.c_void_p
+        ids = (u32 * n)(*[self.kernel(k) for k, _ in pairs])
+        ptrs = (vp * n)(*[ctypes.addressof(a) for _, a in pairs])
+        lens = (u32 * n)(*[ctypes.sizeof(a) for _, a in pairs])
+        return (ids, ptrs, lens, n, [a for _, a in pairs])
+
+    def run_batch(self, b):
+        """Queue a prepared sequence with one hrt_dispatch_batch call."""
+        rc = self.lib.hrt_dispatch_batch(b[0], b[1], b[2], b[3])
+        if rc != 0:
+            raise RuntimeError(f"hrt_dispatch_batch failed at launch {-rc - 1}: {self.last_error()}")
 
     def synchronize(self):
         self.check(self.lib.hrt_synchronize(), "hrt_synchronize")
