@@ -14,7 +14,7 @@ step time, and the CPU baseline: the oracle's float64 restatement of the same fw
 (plus, for reference, torch's CPU aten SDPA, which is what the reference runs on CPU).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--skip-cpu] [--only-attn]
-       python bench.py --profile {fwd,dq,dkdv,copy,gemm,gemm1024,dq8,softmax,ln,dequant} [--steps K]
+       python bench.py --profile {fwd,dq,dkdv,copy,gemm,gemm1024,dq8,softmax,ln,dequant,dit} [--steps K]
                                                                    (launches only that workload, for rocprofv3)
        python bench.py --pmc-summary DIR [DIR ...]                 (per-kernel counters of rocprofv3 --pmc runs)
 """
@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
-    ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy", "gemm", "gemm1024", "dq8", "softmax", "ln", "dequant"],
+    ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy", "gemm", "gemm1024", "dq8", "softmax", "ln", "dequant",
+                                          "dit"],
                     help="launch one kernel (or one benchmark workload) --steps times, untimed")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR", help="summarise rocprofv3 --pmc output directories")
     return ap.parse_args()
@@ -495,7 +496,7 @@ class Bench:
         torch = self.torch
         workloads = {"gemm": lambda: self.gemm(1024, 2048, 8192, "nt"), "gemm1024": lambda: self.gemm(1024, 1024, 1024, "nn", True),
                      "dq8": lambda: self.dq8_linear(1024), "softmax": self.softmax, "ln": self.layer_norm,
-                     "dequant": self.dequant}
+                     "dequant": self.dequant, "dit": self.dit_lora_stack}
         if which in workloads:
             self.profile_n = n
             workloads[which]()

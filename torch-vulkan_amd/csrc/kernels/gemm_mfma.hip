@@ -868,7 +868,8 @@ bool launch_mm_dq8(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
 
 // ---- split-K reduction: c = round(alpha * sum_s ws[s] + beta * bias), splits summed in order ---------------
 // Four consecutive outputs (of the flattened [M, N]) per thread, read as 16-byte pieces of each split when
-// M N is a multiple of 4; the loads of eight splits are in flight together.
+// M N is a multiple of 4; the loads of up to 16 splits are in flight together (the outputs are small: one
+// memory round trip per 16 splits bounds the kernel), then summed in split order.
 template <typename T>
 __global__ __launch_bounds__(256) void mm_reduce(hrt_mm_reduce_args p) {
   const int64_t total = p.M * p.N;
@@ -877,15 +878,15 @@ __global__ __launch_bounds__(256) void mm_reduce(hrt_mm_reduce_args p) {
   const HK_G float* w = gcptr<float>(p.ws);
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   if (total % 4 == 0) {
-    int64_t k = 0;
-    for (; k + 8 <= p.splits; k += 8) {
-      f32x4 v[8];
+    for (int64_t k = 0; k < p.splits; k += 16) {
+      f32x4 v[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const HK_G f32x4*>(w + (k + u) * total + i0);
+      for (int u = 0; u < 16; ++u)  // splits past the end re-read the last one (in range) and are not added
+        v[u] = *reinterpret_cast<const HK_G f32x4*>(w + (k + u < p.splits ? k + u : p.splits - 1) * total + i0);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) s += v[u];
+      for (int u = 0; u < 16; ++u)
+        if (k + u < p.splits) s += v[u];
     }
-    for (; k < p.splits; ++k) s += *reinterpret_cast<const HK_G f32x4*>(w + k * total + i0);
   } else {
     for (int64_t k = 0; k < p.splits; ++k)
 #pragma unroll
