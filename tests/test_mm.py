@@ -222,11 +222,11 @@ SKINNY = [
 ]
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,k,n,ta,tb", SKINNY)
-def test_skinny_products_split_k(m, k, n, ta, tb):
+def test_skinny_products_split_k(m, k, n, ta, tb, dt):
     """Products one 64-wide tile across split K over fp32 partials and a second, in-order reduction kernel;
     checked against the oracle (with addmm's bias, alpha and beta) and for run-to-run identity."""
-    dt = torch.bfloat16
     a = randn((k, m) if ta else (m, k), dt, 41)
     b = randn((n, k) if tb else (k, n), dt, 42)
     A = a.to(dev).t() if ta else a.to(dev)
