@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
     ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy", "gemm", "gemm1024", "dq8", "softmax", "ln", "dequant",
-                                          "dit"],
+                                          "dit", "ew"],
                     help="launch one kernel (or one benchmark workload) --steps times, untimed")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR", help="summarise rocprofv3 --pmc output directories")
     return ap.parse_args()
@@ -413,8 +413,11 @@ class Bench:
 
     # ---- bandwidth kernels: rotate over > 512 MB so the 256 MB MALL cannot serve them ------------
     def bw(self, name, nbytes, sets, make_args, kernels):
+        """Average time of one launch rotating over `sets` input sets; at least 64 launches per timed round so
+        that the start-up latency of a round stays out of the average for long kernels too."""
         args = [make_args(i) for i in range(sets)]
-        t, how = self.time_best(lambda i: [self.rt.dispatch(k, args[i % sets][j]) for j, k in enumerate(kernels)], 2 * sets)
+        reps = -(-max(2 * sets, 64) // sets) * sets
+        t, how = self.time_best(lambda i: [self.rt.dispatch(k, args[i % sets][j]) for j, k in enumerate(kernels)], reps)
         return {"avg_us": round(t * 1e3, 3), "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
                 "frac_of_hbm_peak": round(nbytes / (t * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": nbytes, "timing": how}
 
@@ -489,6 +492,63 @@ class Bench:
 
         return self.bw("dq8", R * C + R * (C // 64) * 2 + R * C * 2, sets, mk, ["dq8_bf16"])
 
+    def elementwise(self):
+        """ew_map at the shapes of the LoRA/DiT training step: the MLP activation forward and backward
+        ([1024, 8192] bf16, tanh GELU), a bias add broadcast over rows, an optimizer moment update (lerp_ on
+        16 M fp32 parameters) and a large flat bf16 add.  Every case rotates over enough buffers to exceed
+        the 256 MB last-level cache; bytes are the compulsory HBM traffic (each operand read once, the
+        output written once)."""
+        torch, abi = self.torch, self.abi
+        bf, f32 = torch.bfloat16, torch.float32
+        dt = {bf: abi.BF16, f32: abi.F32}
+
+        def ew(op, out, a, b=None, s0=0.0, bstrides=None):
+            A = abi.EwArgs()
+            A.op, A.out, A.a, A.out_dtype, A.a_dtype, A.s0 = abi.EW_OPS[op], out.data_ptr(), a.data_ptr(), dt[out.dtype], dt[a.dtype], s0
+            A.ndim = out.dim()
+            for i in range(out.dim()):
+                A.sizes[i], A.out_strides[i], A.a_strides[i] = out.shape[i], out.stride(i), a.stride(i)
+            if b is not None:
+                A.b, A.b_dtype = b.data_ptr(), dt[b.dtype]
+                for i, st in enumerate(bstrides or b.stride()):
+                    A.b_strides[i] = st
+            return A
+
+        def case(name, shape, dtype, op, sets, nin, s0=0.0, bshape=None):
+            n = 1
+            for d in shape:
+                n *= d
+            es = torch.tensor([], dtype=dtype).element_size()
+            xs = [[self.randn(shape if j == 0 or bshape is None else bshape, dtype, 40 + 10 * i + j) for j in range(nin)]
+                  for i in range(sets)]
+            outs = [torch.empty(shape, dtype=dtype, device=self.dev) for _ in range(sets)]
+
+            def mk(i):
+                a = xs[i][0]
+                if nin == 1:
+                    return [ew(op, outs[i], a, s0=s0)]
+                b = xs[i][1]
+                lead = len(shape) - b.dim()  # b broadcasts right-aligned over the leading dimensions
+                bst = [0 if k < lead or b.shape[k - lead] == 1 else b.stride(k - lead) for k in range(len(shape))]
+                return [ew(op, outs[i], a, b, s0=s0, bstrides=bst)]
+
+            bbytes = n * es if bshape is None else (xs[0][1].numel() * es if nin > 1 else 0)
+            nbytes = n * es * 2 + (bbytes if nin > 1 else 0)
+            r = self.bw("ew_map", nbytes, sets, mk, ["ew_map"])
+            r["op"] = op
+            r["shape"] = list(shape)
+            r["dtype"] = str(dtype).replace("torch.", "")
+            return name, r
+
+        cases = [
+            case("gelu_tanh_fwd", (1024, 8192), bf, "gelu_tanh", 16, 1),
+            case("gelu_tanh_bwd", (1024, 8192), bf, "gelu_tanh_bwd", 12, 2),
+            case("bias_add_rows", (1024, 8192), bf, "add", 16, 2, s0=1.0, bshape=(8192,)),
+            case("lerp_f32_16M", (16 * 1024 * 1024,), f32, "lerp_s", 3, 2, s0=0.1),
+            case("add_bf16_64M", (8192, 8192), bf, "add", 2, 2, s0=1.0),
+        ]
+        return dict(cases)
+
     # ---- CPU baseline: the reference's CPU path (torch CPU aten) -------------------------------------
     def profile(self, which, n):
         """Launch one kernel of the headline step (or a 64 MiB device copy) n times and return: the workload
@@ -496,7 +556,7 @@ class Bench:
         torch = self.torch
         workloads = {"gemm": lambda: self.gemm(1024, 2048, 8192, "nt"), "gemm1024": lambda: self.gemm(1024, 1024, 1024, "nn", True),
                      "dq8": lambda: self.dq8_linear(1024), "softmax": self.softmax, "ln": self.layer_norm,
-                     "dequant": self.dequant, "dit": self.dit_lora_stack}
+                     "dequant": self.dequant, "dit": self.dit_lora_stack, "ew": self.elementwise}
         if which in workloads:
             self.profile_n = n
             workloads[which]()
@@ -621,6 +681,7 @@ def main():
         line["softmax_f32_16384x1024"] = bench.softmax()
         line["layer_norm_bf16_1024x2048"] = bench.layer_norm()
         line["dequant_int8_8192x2048_bf16"] = bench.dequant()
+        line["elementwise"] = bench.elementwise()
         print("[bench] bandwidth kernels done", file=sys.stderr, flush=True)
     if not args.skip_cpu:
         line["cpu_baseline"] = bench.cpu_baseline()

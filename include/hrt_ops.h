@@ -62,6 +62,66 @@ typedef struct hrt_fill_args {
   int64_t strides[HRT_MAX_DIMS];
 } hrt_fill_args;
 
+/* "ew_map" — out[i] = f(a[i], b[i], c[i]; s0, s1) over an ndim-dimensional index space (ndim <= 8):
+ * every operand has its own element strides (stride 0 = broadcast along that dimension), a, b, c are
+ * read as HRT_F32/BF16/F16 (c as HRT_RAW8 bytes for HRT_EW_WHERE), converted to fp32, f is evaluated in
+ * fp32 and rounded once to out_dtype.  Operands an op does not read must have address 0.  Additions and
+ * products are evaluated in the written order without fused multiply-add, so the arithmetic ops give
+ * the same bits as PyTorch's CPU kernels.  Replaces the generated `ew_<op>_<kinds>` kernel family
+ * (vkrt/shaders/ew.comp.in:115-257, op table tools/gen_shaders.py:53-120) driven by `ew_prepare` /
+ * `ew_run` (csrc/ops_ew.cpp:76-139); the op code is an argument instead of part of the kernel name. */
+enum hrt_ew_op {
+  /* (a, b) */
+  HRT_EW_ADD = 0,      /* a + s0 * b                 add.Tensor (alpha = s0)          ops_ew.cpp:146-190 */
+  HRT_EW_SUB = 1,      /* a - s0 * b                 sub.Tensor                                         */
+  HRT_EW_MUL = 2,      /* a * b                                                                         */
+  HRT_EW_DIV = 3,      /* a / b                                                                         */
+  /* (a) with host scalars */
+  HRT_EW_ADD_S = 4,    /* a + s0                     add/sub with a scalar, s0 = +-(alpha * value)     */
+  HRT_EW_MUL_S = 5,    /* a * s0                                                                        */
+  HRT_EW_DIV_S = 6,    /* a / s0                                                                        */
+  HRT_EW_AXPB = 7,     /* s1 + s0 * a                scalar on the left of add/sub (ops_ew.cpp:222-229) */
+  HRT_EW_RDIV_S = 8,   /* s0 / a                     scalar on the left of div                          */
+  HRT_EW_POW_S = 9,    /* pow(a, s0)                 pow.Tensor_Scalar                                  */
+  /* (a) unary (ops_ew.cpp:283-334) */
+  HRT_EW_NEG = 10,
+  HRT_EW_RSQRT = 11,
+  HRT_EW_RECIP = 12,
+  HRT_EW_EXP = 13,
+  HRT_EW_SIN = 14,
+  HRT_EW_COS = 15,
+  HRT_EW_SQRT = 16,
+  HRT_EW_TANH = 17,
+  HRT_EW_SIGMOID = 18,
+  HRT_EW_RELU = 19,
+  HRT_EW_SILU = 20,
+  HRT_EW_GELU_ERF = 21,
+  HRT_EW_GELU_TANH = 22,
+  /* (a = grad, b = input) activation backward (ops_ew.cpp:336-372) */
+  HRT_EW_SILU_BWD = 23,
+  HRT_EW_GELU_ERF_BWD = 24,
+  HRT_EW_GELU_TANH_BWD = 25,
+  /* optimizer forms (ops_ew.cpp:394-455) */
+  HRT_EW_ADDCMUL = 26, /* a + s0 * b * c                                                                */
+  HRT_EW_ADDCDIV = 27, /* a + s0 * b / c                                                                */
+  HRT_EW_LERP_S = 28,  /* a + s0 * (b - a), as b - (b - a) * (1 - s0) when |s0| >= 0.5                  */
+  /* (a, b, c = bool) */
+  HRT_EW_WHERE = 29,   /* c != 0 ? a : b             where.self (ops_ew.cpp:374-392)                    */
+  HRT_EW_OP_COUNT = 30
+};
+
+typedef struct hrt_ew_args {
+  uint64_t out, a, b, c;
+  int32_t op, ndim;
+  int32_t out_dtype, a_dtype, b_dtype, c_dtype;
+  float s0, s1;
+  int64_t sizes[HRT_MAX_DIMS];
+  int64_t out_strides[HRT_MAX_DIMS];
+  int64_t a_strides[HRT_MAX_DIMS];
+  int64_t b_strides[HRT_MAX_DIMS];
+  int64_t c_strides[HRT_MAX_DIMS];
+} hrt_ew_args;
+
 /* "mm_{f32,bf16,f16}" (portable FMA kernel) and "mm_mfma_{bf16,f16}" (gfx950 matrix cores):
  *   c[b, m, n] = alpha * sum_k a[b, m, k] * b[b, k, n] + beta * bias[b, m, n]     (bias only if has_bias)
  * a, b, bias: any non-negative strides (transposed / sliced views are read in place; bias broadcasts

@@ -230,3 +230,139 @@ def rel_l2(got, ref):
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     return float(np.linalg.norm(got - ref) / (np.linalg.norm(ref) + 1e-300))
+
+
+# ---------------------------------------------------------------------------------------------------------
+# Elementwise — vkrt/shaders/ew.comp.in:115-257 (op expressions tools/gen_shaders.py:53-92), adapters
+# csrc/ops_ew.cpp:146-455
+# ---------------------------------------------------------------------------------------------------------
+
+# Ops whose float32 evaluation the restatement reproduces bit for bit: sums, products, quotients and
+# square roots rounded one at a time in the written order (numpy never fuses a multiply-add).  The
+# others contain exp / erf / tanh / sin / cos / pow, whose float32 library results differ between
+# implementations in the last bits; for them the restatement evaluates the same formula in float64.
+EW_EXACT = frozenset({
+    "add", "sub", "mul", "div", "add_s", "mul_s", "div_s", "axpb", "rdiv_s", "neg", "rsqrt", "recip", "sqrt",
+    "relu", "addcmul", "addcdiv", "lerp_s", "where",
+})
+EW_POW_EXACT = (2.0, 3.0, 0.5, -0.5, -1.0, -2.0)  # exponents evaluated by products / sqrt / reciprocal
+
+_SQRT_HALF = 0.70710678118654752440
+_INV_SQRT_2PI = 0.39894228040143267794
+_SQRT_2_OVER_PI = 0.79788456080286535588
+_KAPPA = 0.044715
+
+
+def _erf(x):
+    try:
+        from scipy.special import erf
+    except ImportError:  # pragma: no cover - scipy is part of the image
+        import math
+
+        erf = np.vectorize(math.erf, otypes=[np.float64])
+    return erf(x)
+
+
+def _ew_formula(op, x, y, z, s0, s1, f):
+    """The formula of `op` with every constant and intermediate in the float type f (np.float32 for the
+    exact ops, np.float64 for the rest)."""
+    s0, s1 = f(s0), f(s1)
+    one, half = f(1.0), f(0.5)
+    if op == "add":
+        return x + s0 * y
+    if op == "sub":
+        return x - s0 * y
+    if op == "mul":
+        return x * y
+    if op == "div":
+        return x / y
+    if op == "add_s":
+        return x + s0
+    if op == "mul_s":
+        return x * s0
+    if op == "div_s":
+        return x / s0
+    if op == "axpb":
+        return s1 + s0 * x
+    if op == "rdiv_s":
+        return s0 / x
+    if op == "pow_s":
+        e = float(s0)
+        if e == 2.0:
+            return x * x
+        if e == 3.0:
+            return x * x * x
+        if e == 0.5:
+            return np.sqrt(x)
+        if e == -0.5:
+            return one / np.sqrt(x)
+        if e == -1.0:
+            return one / x
+        if e == -2.0:
+            return one / (x * x)
+        return np.power(x, s0)
+    if op == "neg":
+        return -x
+    if op == "rsqrt":
+        return one / np.sqrt(x)
+    if op == "recip":
+        return one / x
+    if op == "exp":
+        return np.exp(x)
+    if op == "sin":
+        return np.sin(x)
+    if op == "cos":
+        return np.cos(x)
+    if op == "sqrt":
+        return np.sqrt(x)
+    if op == "tanh":
+        return np.tanh(x)
+    if op == "sigmoid":
+        return one / (one + np.exp(-x))
+    if op == "relu":
+        return np.where(x < 0, f(0.0), x)
+    if op == "silu":
+        return x / (one + np.exp(-x))
+    if op == "gelu_erf":
+        return half * x * (one + _erf(x * f(_SQRT_HALF)))
+    if op == "gelu_tanh":
+        return half * x * (one + np.tanh(f(_SQRT_2_OVER_PI) * (x + f(_KAPPA) * x * x * x)))
+    if op == "silu_bwd":  # x = grad, y = input
+        s = one / (one + np.exp(-y))
+        return x * s * (one + y * (one - s))
+    if op == "gelu_erf_bwd":
+        cdf = half * (one + _erf(y * f(_SQRT_HALF)))
+        pdf = f(_INV_SQRT_2PI) * np.exp(-half * y * y)
+        return x * (cdf + y * pdf)
+    if op == "gelu_tanh_bwd":
+        y2 = y * y
+        t = np.tanh(f(_SQRT_2_OVER_PI) * (y + f(_KAPPA) * y2 * y))
+        dright = half * y * (one - t * t) * f(_SQRT_2_OVER_PI) * (one + f(3.0) * f(_KAPPA) * y2)
+        return x * (half * (one + t) + dright)
+    if op == "addcmul":
+        return x + s0 * y * z
+    if op == "addcdiv":
+        return x + s0 * y / z
+    if op == "lerp_s":
+        return x + s0 * (y - x) if abs(float(s0)) < 0.5 else y - (y - x) * (one - s0)
+    if op == "where":
+        return np.where(z != 0, x, y)
+    raise ValueError(op)
+
+
+def ew_map(op, a, b=None, c=None, s0=0.0, s1=0.0, out_kind="f32"):
+    """out = f(a, b, c; s0, s1) as the device computes it: inputs (float arrays holding values of their
+    storage type, broadcast numpy-style) widened to float32, the formula in float32, one store rounding
+    to out_kind.  Ops outside EW_EXACT (and pow_s with another exponent) evaluate the formula in float64
+    from the same float32 inputs and round that to float32 first: the correctly rounded result the
+    device's float32 evaluation approximates.  Returns (stored value as float32, stored bits)."""
+    exact = op in EW_EXACT or (op == "pow_s" and float(s0) in EW_POW_EXACT)
+    f = np.float32 if exact else np.float64
+    arrs = [np.asarray(t, dtype=np.float32) for t in (a, b, c) if t is not None]
+    shape = np.broadcast_shapes(*[t.shape for t in arrs])
+    x, y, z = (np.broadcast_to(np.asarray(t, dtype=np.float32), shape).astype(f) if t is not None else None
+               for t in (a, b, c))
+    with np.errstate(all="ignore"):
+        r = _ew_formula(op, x, y, z, s0, s1, f)
+        r32 = np.asarray(r, dtype=np.float64).astype(np.float32).reshape(shape)
+    return _round_to(r32, out_kind)

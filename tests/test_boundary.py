@@ -53,7 +53,7 @@ def test_runtime_reports_errors_without_a_device():
 
 
 KERNELS = (
-    ["add_f32", "ew_copy", "ew_fill"]
+    ["add_f32", "ew_copy", "ew_fill", "ew_map"]
     + [f"dq8_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_mfma_{k}" for k in ("bf16", "f16")]
@@ -85,6 +85,13 @@ def test_shim_registers_the_reference_operator_surface():
         "aten::native_layer_norm", "aten::native_layer_norm_backward",
         "aten::empty.memory_format", "aten::empty_strided", "aten::_copy_from", "aten::_copy_from_and_resize",
         "aten::view", "aten::as_strided", "aten::_reshape_alias", "aten::resize_", "aten::fill_.Scalar", "aten::zero_",
+    ] + [  # elementwise (csrc/ops_ew.cpp:510-550)
+        f"aten::{n}" for n in (
+            "add.Tensor", "add_.Tensor", "sub.Tensor", "sub_.Tensor", "mul.Tensor", "mul_.Tensor", "div.Tensor",
+            "div_.Tensor", "neg", "rsqrt", "reciprocal", "exp", "sin", "cos", "sqrt", "tanh", "sigmoid", "relu",
+            "silu", "pow.Tensor_Scalar", "gelu", "silu_backward", "gelu_backward", "where.self", "addcmul_",
+            "addcdiv_", "addcmul", "addcdiv", "lerp_.Scalar", "lerp.Scalar", "add.Scalar", "add_.Scalar",
+            "sub.Scalar", "sub_.Scalar", "mul.Scalar", "mul_.Scalar", "div.Scalar", "div_.Scalar")
     ]
     missing = [o for o in ops if not torch._C._dispatch_has_kernel_for_dispatch_key(o, "PrivateUse1")]
     assert not missing, missing
@@ -108,7 +115,7 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
     from torch_vulkan import abi
 
     structs = {
-        "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs,
+        "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs, "hrt_ew_args": abi.EwArgs,
         "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_mm_reduce_args": abi.MmReduceArgs,
         "hrt_attn_args": abi.AttnArgs,
         "hrt_softmax_args": abi.SoftmaxArgs, "hrt_ln_args": abi.LnArgs, "hrt_dq8_args": abi.Dq8Args,
@@ -130,3 +137,21 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
         for fname, _ in py._fields_:
             assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
     assert abi.ln_chunks(1024) == 256 and abi.ln_chunks(5) == 2
+
+
+def test_python_ew_op_codes_match_the_c_header(tmp_path):
+    """abi.EW_OPS names the hrt_ew_op codes of include/hrt_ops.h in order."""
+    from torch_vulkan import abi
+
+    enum = {n: "HRT_EW_" + n.upper() for n in abi.EW_OPS}
+    lines = ['#include <stdio.h>', '#include "hrt_ops.h"', "int main(void) {"]
+    lines += [f'  printf("{n} %d\\n", (int){c});' for n, c in enum.items()]
+    lines += ['  printf("count %d\\n", (int)HRT_EW_OP_COUNT);', "  return 0; }"]
+    src = tmp_path / "ew_ops.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "ew_ops"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True, check=True).stdout.split()
+    got = dict(zip(out[::2], map(int, out[1::2])))
+    assert got.pop("count") == len(abi.EW_OPS)
+    assert got == abi.EW_OPS

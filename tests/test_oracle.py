@@ -296,3 +296,153 @@ def test_planted_rounding_truncation_is_caught():
     ref = torch_bits(torch.from_numpy(x.copy()).to(torch.bfloat16))
     nan = np.isnan(x)
     assert not np.array_equal(truncated[~nan], ref[~nan])
+
+
+# ---- elementwise (oracle.ew_map) -------------------------------------------------------------------------------
+# The reference's own checks compare each op with CPU PyTorch at these tolerances (tests/test_ops_ew.py:17)
+EW_TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (2e-2, 1e-3), torch.float16: (4e-3, 1e-4)}
+EW_KIND = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+_gelu_bwd = torch.ops.aten.gelu_backward
+# op -> (torch CPU form, input range (lo, hi) of every operand, scalars s0, s1, tolerance scale)
+EW_CASES = {
+    "add": (lambda x, y, z, s0, s1: torch.add(x, y, alpha=s0), (-3, 3), 2.0, 0.0, 1.0),
+    "sub": (lambda x, y, z, s0, s1: torch.sub(x, y, alpha=s0), (-3, 3), 0.5, 0.0, 1.0),
+    "mul": (lambda x, y, z, s0, s1: torch.mul(x, y), (-3, 3), 0.0, 0.0, 1.0),
+    "div": (lambda x, y, z, s0, s1: torch.div(x, y), (0.5, 3), 0.0, 0.0, 1.0),
+    "add_s": (lambda x, y, z, s0, s1: torch.add(x, s0), (-3, 3), 2.5, 0.0, 1.0),
+    "mul_s": (lambda x, y, z, s0, s1: torch.mul(x, s0), (-3, 3), 0.999, 0.0, 1.0),
+    "div_s": (lambda x, y, z, s0, s1: torch.div(x, s0), (-3, 3), 3.0, 0.0, 1.0),
+    "axpb": (lambda x, y, z, s0, s1: torch.add(s1, x, alpha=s0), (-3, 3), 2.0, 2.0, 2.0),
+    "rdiv_s": (lambda x, y, z, s0, s1: torch.div(torch.full_like(x, s0), x), (0.5, 3), 2.0, 0.0, 1.0),
+    "pow_s": (lambda x, y, z, s0, s1: torch.pow(x, s0), (0.3, 3), 2.5, 0.0, 4.0),
+    "neg": (lambda x, y, z, s0, s1: torch.neg(x), (-3, 3), 0.0, 0.0, 1.0),
+    "rsqrt": (lambda x, y, z, s0, s1: torch.rsqrt(x), (0.1, 5), 0.0, 0.0, 1.0),
+    "recip": (lambda x, y, z, s0, s1: torch.reciprocal(x), (0.2, 5), 0.0, 0.0, 1.0),
+    "exp": (lambda x, y, z, s0, s1: torch.exp(x), (-4, 4), 0.0, 0.0, 2.0),
+    "sin": (lambda x, y, z, s0, s1: torch.sin(x), (-8, 8), 0.0, 0.0, 1.0),
+    "cos": (lambda x, y, z, s0, s1: torch.cos(x), (-8, 8), 0.0, 0.0, 1.0),
+    "sqrt": (lambda x, y, z, s0, s1: torch.sqrt(x), (0.0, 6), 0.0, 0.0, 1.0),
+    "tanh": (lambda x, y, z, s0, s1: torch.tanh(x), (-4, 4), 0.0, 0.0, 1.0),
+    "sigmoid": (lambda x, y, z, s0, s1: torch.sigmoid(x), (-6, 6), 0.0, 0.0, 1.0),
+    "relu": (lambda x, y, z, s0, s1: torch.relu(x), (-3, 3), 0.0, 0.0, 1.0),
+    "silu": (lambda x, y, z, s0, s1: F.silu(x), (-6, 6), 0.0, 0.0, 1.0),
+    "gelu_erf": (lambda x, y, z, s0, s1: F.gelu(x), (-6, 6), 0.0, 0.0, 2.0),
+    "gelu_tanh": (lambda x, y, z, s0, s1: F.gelu(x, approximate="tanh"), (-6, 6), 0.0, 0.0, 2.0),
+    "silu_bwd": (lambda x, y, z, s0, s1: torch.ops.aten.silu_backward(x, y), (-5, 5), 0.0, 0.0, 3.0),
+    "gelu_erf_bwd": (lambda x, y, z, s0, s1: _gelu_bwd(x, y, approximate="none"), (-5, 5), 0.0, 0.0, 3.0),
+    "gelu_tanh_bwd": (lambda x, y, z, s0, s1: _gelu_bwd(x, y, approximate="tanh"), (-5, 5), 0.0, 0.0, 3.0),
+    "addcmul": (lambda x, y, z, s0, s1: torch.addcmul(x, y, z, value=s0), (0.5, 3), 0.3, 0.0, 2.0),
+    "addcdiv": (lambda x, y, z, s0, s1: torch.addcdiv(x, y, z, value=s0), (0.5, 3), -0.7, 0.0, 2.0),
+    "lerp_s": (lambda x, y, z, s0, s1: torch.lerp(x, y, s0), (-3, 3), 0.75, 0.0, 2.0),
+    "where": (lambda x, y, z, s0, s1: torch.where(z != 0, x, y), (-3, 3), 0.0, 0.0, 1.0),
+}
+EW_ARITY = {"add": 2, "sub": 2, "mul": 2, "div": 2, "silu_bwd": 2, "gelu_erf_bwd": 2, "gelu_tanh_bwd": 2,
+            "lerp_s": 2, "addcmul": 3, "addcdiv": 3, "where": 3}
+
+
+def ew_inputs(op, dtype, shape=(37, 53), seed=0):
+    lo, hi = EW_CASES[op][1]
+    g = torch.Generator().manual_seed(seed)
+    ts = [(torch.rand(shape, generator=g) * (hi - lo) + lo).to(dtype) for _ in range(EW_ARITY.get(op, 1))]
+    if op == "where":
+        ts[2] = (torch.rand(shape, generator=g) > 0.5).to(dtype)
+    while len(ts) < 3:
+        ts.append(None)
+    return ts
+
+
+def ew_oracle(op, ts, s0, s1, dtype):
+    arr = [None if t is None else t.float().numpy() for t in ts]
+    return oracle.ew_map(op, *arr, s0=s0, s1=s1, out_kind=EW_KIND[dtype])
+
+
+@pytest.mark.parametrize("dtype", list(EW_KIND))
+@pytest.mark.parametrize("op", list(EW_CASES))
+def test_ew_oracle_matches_torch_cpu(op, dtype):
+    """Every op against CPU PyTorch, the reference tests' own oracle, at their tolerances."""
+    fn, _, s0, s1, scale = EW_CASES[op]
+    ts = ew_inputs(op, dtype)
+    ref = fn(*ts, s0, s1).float().numpy()
+    got, _ = ew_oracle(op, ts, s0, s1, dtype)
+    rtol, atol = EW_TOL[dtype]
+    np.testing.assert_allclose(got, ref, rtol=rtol * scale, atol=atol * scale)
+
+
+# The CPU kernels round these ops once from a float32 evaluation in the same order, so the restatement must
+# give PyTorch's bits exactly (add/sub with alpha 1, where fused and separate multiply-add agree).  Not
+# in the list: sqrt and rsqrt, whose CPU float32 kernels are not correctly rounded in the last bit.
+EW_BIT_EXACT = ["mul", "div", "add_s", "neg", "recip", "relu", "where"]
+
+
+@pytest.mark.parametrize("dtype", list(EW_KIND))
+@pytest.mark.parametrize("op", ["add", "sub"] + EW_BIT_EXACT)
+def test_ew_oracle_bits_equal_torch_where_rounding_is_fixed(op, dtype):
+    fn, _, s0, s1, _ = EW_CASES[op]
+    if op in ("add", "sub"):
+        s0 = 1.0
+    ts = ew_inputs(op, dtype, seed=7)
+    ref = fn(*ts, s0, s1).contiguous()
+    _, got = ew_oracle(op, ts, s0, s1, dtype)
+    np.testing.assert_array_equal(got, torch_bits(ref))
+
+
+def _fd_error(fwd, bwd, x):
+    """max |bwd(g=1, x) - central difference of fwd| in float64."""
+    h = 1e-5
+    one = np.ones_like(x)
+    num = (fwd(x + h) - fwd(x - h)) / (2 * h)
+    return float(np.max(np.abs(bwd(one, x) - num)))
+
+
+def _f64(op):
+    from oracle.ops import _ew_formula
+
+    return lambda *a: _ew_formula(op, *(list(a) + [None] * (3 - len(a))), 0.0, 0.0, np.float64)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu_erf", "gelu_tanh"])
+def test_ew_oracle_backward_is_the_derivative(act):
+    """silu_bwd / gelu_*_bwd equal the finite-difference derivative of the forward formulas."""
+    x = np.linspace(-7, 7, 2001)
+    assert _fd_error(_f64(act), _f64(act + "_bwd"), x) < 1e-7
+
+
+def test_planted_gelu_backward_dropped_factor_is_caught():
+    """A tanh-GELU backward without the 3 of d/dx x^3 fails the derivative pin."""
+    from oracle.ops import _SQRT_2_OVER_PI, _KAPPA
+
+    def planted(g, y):
+        t = np.tanh(_SQRT_2_OVER_PI * (y + _KAPPA * y ** 3))
+        return g * (0.5 * (1 + t) + 0.5 * y * (1 - t * t) * _SQRT_2_OVER_PI * (1 + _KAPPA * y * y))
+
+    x = np.linspace(-7, 7, 2001)
+    assert _fd_error(_f64("gelu_tanh"), planted, x) > 1e-3
+
+
+def test_ew_oracle_identities():
+    g = np.random.default_rng(3)
+    a = g.uniform(-3, 3, 1000).astype(np.float32)
+    b = g.uniform(-3, 3, 1000).astype(np.float32)
+    # lerp's two-sided form returns its end points exactly
+    assert np.array_equal(oracle.ew_map("lerp_s", a, b, s0=0.0)[0], a)
+    assert np.array_equal(oracle.ew_map("lerp_s", a, b, s0=1.0)[0], b)
+    m = (g.uniform(size=1000) > 0.5).astype(np.float32)
+    assert np.array_equal(oracle.ew_map("where", a, b, m)[0], np.where(m != 0, a, b))
+    assert np.array_equal(oracle.ew_map("addcmul", a, b, b, s0=0.0)[0], a)
+    assert np.array_equal(oracle.ew_map("pow_s", a, s0=2.0)[1], oracle.ew_map("mul", a, a)[1])
+    assert np.array_equal(oracle.ew_map("sub", a, a, s0=1.0)[0], np.zeros_like(a))
+    assert np.array_equal(oracle.ew_map("relu", a)[0], np.maximum(a, 0))
+    # silu = x * sigmoid(x); the tanh GELU stays within 5e-4 of the erf GELU (its published accuracy)
+    s = oracle.ew_map("sigmoid", a)[0].astype(np.float64)
+    np.testing.assert_allclose(oracle.ew_map("silu", a)[0], a * s, rtol=1e-6, atol=1e-7)
+    assert np.max(np.abs(oracle.ew_map("gelu_tanh", a)[0] - oracle.ew_map("gelu_erf", a)[0])) < 5e-4
+    # broadcasting and the bf16 store rounding
+    r, bits = oracle.ew_map("add", a.reshape(10, 100), b[:100], s0=1.0, out_kind="bf16")
+    assert r.shape == (10, 100) and np.array_equal(bits, oracle.round_bf16(a.reshape(10, 100) + b[:100]))
+
+
+def test_ew_oracle_large_argument_sin_cos():
+    """RoPE-like arguments up to ~1500 (the reference's range-reduction case)."""
+    x = torch.arange(0, 4000, dtype=torch.float32) * 0.37
+    for op, fn in (("sin", torch.sin), ("cos", torch.cos)):
+        np.testing.assert_allclose(oracle.ew_map(op, x.numpy())[0], fn(x).numpy(), rtol=4e-4, atol=4e-5)

@@ -35,6 +35,7 @@ HIP_FLAGS = [
 HRT_SOURCES = [
     "hrt/runtime.cpp",
     "kernels/ew.hip",
+    "kernels/ew_map.hip",
     "kernels/dq8.hip",
     "kernels/gemm.hip",
     "kernels/gemm_mfma.hip",

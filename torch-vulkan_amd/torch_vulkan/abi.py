@@ -34,6 +34,20 @@ class FillArgs(ctypes.Structure):
                 ("sizes", i64 * MAX_DIMS), ("strides", i64 * MAX_DIMS)]
 
 
+class EwArgs(ctypes.Structure):
+    _fields_ = [("out", u64), ("a", u64), ("b", u64), ("c", u64), ("op", i32), ("ndim", i32), ("out_dtype", i32),
+                ("a_dtype", i32), ("b_dtype", i32), ("c_dtype", i32), ("s0", f32), ("s1", f32),
+                ("sizes", i64 * MAX_DIMS), ("out_strides", i64 * MAX_DIMS), ("a_strides", i64 * MAX_DIMS),
+                ("b_strides", i64 * MAX_DIMS), ("c_strides", i64 * MAX_DIMS)]
+
+
+# hrt_ew_op codes (include/hrt_ops.h), by the oracle's op names
+EW_OPS = {n: i for i, n in enumerate((
+    "add", "sub", "mul", "div", "add_s", "mul_s", "div_s", "axpb", "rdiv_s", "pow_s", "neg", "rsqrt", "recip", "exp",
+    "sin", "cos", "sqrt", "tanh", "sigmoid", "relu", "silu", "gelu_erf", "gelu_tanh", "silu_bwd", "gelu_erf_bwd",
+    "gelu_tanh_bwd", "addcmul", "addcdiv", "lerp_s", "where"))}
+
+
 class MmArgs(ctypes.Structure):
     _fields_ = [("a", u64), ("b", u64), ("c", u64), ("bias", u64), ("M", i64), ("N", i64), ("K", i64), ("batch", i64),
                 ("a_sb", i64), ("a_sm", i64), ("a_sk", i64), ("b_sb", i64), ("b_sk", i64), ("b_sn", i64),
