@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
     ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy", "gemm", "gemm1024", "dq8", "softmax", "ln", "dequant",
-                                          "dit", "ew"],
+                                          "dit", "ew", "reduce"],
                     help="launch one kernel (or one benchmark workload) --steps times, untimed")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR", help="summarise rocprofv3 --pmc output directories")
     return ap.parse_args()
@@ -549,6 +549,65 @@ class Bench:
         ]
         return dict(cases)
 
+    def reductions(self):
+        """reduce_sum at the step's shapes: the bias gradient of the DiT MLP up-projection (sum over 1024
+        rows of [1024, 8192] bf16), row sums of the softmax benchmark's [16384, 1024] fp32, a full sum of
+        64 M fp32; and cat of three [1024, 2048] bf16 parts along the last dimension (three ew_copy launches
+        into the slices).  Bytes: input read once + output written once."""
+        import ctypes
+
+        torch, abi = self.torch, self.abi
+        dt = {torch.bfloat16: abi.BF16, torch.float32: abi.F32}
+
+        def case(shape, dtype, mask, sets, seed):
+            xs = [self.randn(shape, dtype, seed + i) for i in range(sets)]
+            kept = [n for d, n in enumerate(shape) if not (mask >> d) & 1]
+            n_out = 1
+            for n in kept:
+                n_out *= n
+            outs = [torch.empty(kept, dtype=dtype, device=self.dev) for _ in range(sets)]
+
+            def args(i):
+                a = abi.ReduceArgs()
+                a.x, a.out, a.ndim, a.x_dtype, a.out_dtype, a.reduce_mask, a.div = (
+                    xs[i].data_ptr(), outs[i].data_ptr(), len(shape), dt[dtype], dt[dtype], mask, 1.0)
+                for d, n in enumerate(shape):
+                    a.sizes[d], a.strides[d] = n, xs[i].stride(d)
+                return a
+
+            wsn = self.rt.lib.hrt_reduce_workspace(ctypes.byref(args(0)))
+            ws = torch.empty(max(wsn, 1), dtype=torch.float32, device=self.dev)
+
+            def mk(i):
+                a = args(i)
+                a.ws = ws.data_ptr() if wsn > 0 else 0
+                return [a]
+
+            es = xs[0].element_size()
+            r = self.bw("reduce_sum", xs[0].numel() * es + n_out * es, sets, mk, ["reduce_sum"])
+            r["shape"], r["reduce_mask"], r["dtype"], r["workspace_floats"] = list(shape), mask, str(dtype)[6:], wsn
+            return r
+
+        R, C = 1024, 2048
+        parts = [[self.randn((R, C), torch.bfloat16, 90 + 3 * i + j) for j in range(3)] for i in range(8)]
+        cats = [torch.empty((R, 3 * C), dtype=torch.bfloat16, device=self.dev) for _ in range(8)]
+
+        def cat_args(i):
+            out = []
+            for j in range(3):
+                a = abi.CopyArgs()
+                a.dst, a.src, a.ndim, a.dst_dtype, a.src_dtype = cats[i].data_ptr() + j * C * 2, parts[i][j].data_ptr(), 2, 1, 1
+                a.sizes[0], a.sizes[1], a.dst_strides[0], a.dst_strides[1], a.src_strides[0], a.src_strides[1] = R, C, 3 * C, 1, C, 1
+                out.append(a)
+            return out
+
+        cat = self.bw("ew_copy", 2 * 3 * R * C * 2, 8, cat_args, ["ew_copy", "ew_copy", "ew_copy"])
+        cat["launches"] = 3
+        return {"bias_grad_sum0_bf16_1024x8192": case((1024, 8192), torch.bfloat16, 0b01, 16, 300),
+                "row_sum_f32_16384x1024": case((16384, 1024), torch.float32, 0b10, 5, 320),
+                "full_sum_f32_64M": case((64 * 1024 * 1024,), torch.float32, 0b1, 2, 340),
+                "cat_bf16_3x1024x2048_dim1": cat}
+
     # ---- CPU baseline: the reference's CPU path (torch CPU aten) -------------------------------------
     def profile(self, which, n):
         """Launch one kernel of the headline step (or a 64 MiB device copy) n times and return: the workload
@@ -556,7 +615,8 @@ class Bench:
         torch = self.torch
         workloads = {"gemm": lambda: self.gemm(1024, 2048, 8192, "nt"), "gemm1024": lambda: self.gemm(1024, 1024, 1024, "nn", True),
                      "dq8": lambda: self.dq8_linear(1024), "softmax": self.softmax, "ln": self.layer_norm,
-                     "dequant": self.dequant, "dit": self.dit_lora_stack, "ew": self.elementwise}
+                     "dequant": self.dequant, "dit": self.dit_lora_stack, "ew": self.elementwise,
+                     "reduce": self.reductions}
         if which in workloads:
             self.profile_n = n
             workloads[which]()
@@ -682,6 +742,7 @@ def main():
         line["layer_norm_bf16_1024x2048"] = bench.layer_norm()
         line["dequant_int8_8192x2048_bf16"] = bench.dequant()
         line["elementwise"] = bench.elementwise()
+        line["reductions"] = bench.reductions()
         print("[bench] bandwidth kernels done", file=sys.stderr, flush=True)
     if not args.skip_cpu:
         line["cpu_baseline"] = bench.cpu_baseline()

@@ -66,8 +66,9 @@ typedef struct hrt_fill_args {
  * every operand has its own element strides (stride 0 = broadcast along that dimension), a, b, c are
  * read as HRT_F32/BF16/F16 (c as HRT_RAW8 bytes for HRT_EW_WHERE), converted to fp32, f is evaluated in
  * fp32 and rounded once to out_dtype.  Operands an op does not read must have address 0.  Additions and
- * products are evaluated in the written order without fused multiply-add, so the arithmetic ops give
- * the same bits as PyTorch's CPU kernels.  Replaces the generated `ew_<op>_<kinds>` kernel family
+ * products are evaluated in the written order without fused multiply-add (division and square root
+ * correctly rounded), so the arithmetic ops equal a float32 evaluation of the same formula bit for bit;
+ * the activations are within a few float32 ulps.  Replaces the generated `ew_<op>_<kinds>` kernel family
  * (vkrt/shaders/ew.comp.in:115-257, op table tools/gen_shaders.py:53-120) driven by `ew_prepare` /
  * `ew_run` (csrc/ops_ew.cpp:76-139); the op code is an argument instead of part of the kernel name. */
 enum hrt_ew_op {
@@ -247,6 +248,28 @@ typedef struct hrt_dq8_args {
   uint64_t q, scale, out;
   int64_t rows, cols, nblocks;
 } hrt_dq8_args;
+
+/* "reduce_sum" — out[k] = (sum over the reduced coordinates r of x[k, r]) / div, accumulated in fp32 and
+ * rounded once to out_dtype.  x: an ndim-dimensional strided view (ndim <= 8, non-negative strides) of
+ * HRT_F32/BF16/F16; bit d of reduce_mask marks dimension d as summed; out: the kept dimensions, in order,
+ * contiguous (what sum/mean with or without keepdim return); div: 1 for sum, the reduced element count
+ * for mean.  When the reduced range is split across workgroups the fp32 partial sums go to ws and a
+ * second pass adds them in order (deterministic); ws must then hold hrt_reduce_workspace(&args) floats,
+ * otherwise it may be 0.  Replaces `try_reduce` / "reduce_{dt}" (csrc/ops_rows.cpp:183-270,
+ * vkrt/shaders/reduce.comp.in:1-45), which took 4 kept and 2 reduced dimensions and one workgroup per
+ * output. */
+typedef struct hrt_reduce_args {
+  uint64_t x, out, ws;
+  int32_t ndim, x_dtype, out_dtype;
+  uint32_t reduce_mask;
+  float div;
+  uint32_t pad;
+  int64_t sizes[HRT_MAX_DIMS];
+  int64_t strides[HRT_MAX_DIMS];
+} hrt_reduce_args;
+
+/* fp32 elements of workspace "reduce_sum" needs for these arguments (0: none, -1: invalid arguments). */
+int64_t hrt_reduce_workspace(const hrt_reduce_args* args);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,8 @@ bit-exact parts in oracle/csrc/oracle.c):
   layer_norm_fwd / _bwd  vkrt/shaders/ln.comp.in:27-81                          torch float64 layer_norm + autograd, moments
   attention_fwd / _bwd   vkrt/shaders/attn.comp.in:210-395,                     torch float64 math SDPA + autograd, Sk=1,
   attention_delta        attn_coop.comp.in:158-301, csrc/ops_attn.cpp:240-248   identical keys, zero dO, lse closed form
+  reduce_sum             csrc/ops_rows.cpp:183-270, reduce.comp.in:27-44       torch float64 sum/mean on strided views, arange
+                                                                                closed forms, empty reductions
   ew_map                 vkrt/shaders/ew.comp.in:115-257,                       torch CPU ops at the reference tests' tolerances,
                          tools/gen_shaders.py:53-92, csrc/ops_ew.cpp:146-455    bit equality where CPU rounding is fixed,
                                                                                 finite differences of the backward formulas,
@@ -37,6 +39,7 @@ from .ops import (  # noqa: F401
     gemm,
     layer_norm_bwd,
     layer_norm_fwd,
+    reduce_sum,
     rel_l2,
     round_bf16,
     round_f16,

@@ -15,11 +15,12 @@ import numpy as np
 def round_bf16(x):
     """float32 -> bf16 bit pattern (uint16): round to nearest even, every NaN -> 0x7FC0.
     types.glsl:45-50 (f2bf)."""
+    shape = np.shape(x)  # ascontiguousarray makes 0-dim arrays 1-dim
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
     r = np.where(nan, 0x7FC0, r)
-    return r.astype(np.uint16)
+    return r.astype(np.uint16).reshape(shape)
 
 
 def bf16_to_f32(bits):
@@ -30,6 +31,7 @@ def bf16_to_f32(bits):
 def round_f16(x):
     """float32 -> IEEE half bit pattern (uint16), round to nearest even including subnormals, overflow
     -> inf, NaN -> quiet NaN with the top payload bits.  types.glsl:18-41 (f2h)."""
+    shape = np.shape(x)
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.int64)
     sign = (u >> 16) & 0x8000
     e = (u >> 23) & 0xFF
@@ -60,7 +62,7 @@ def round_f16(x):
     h = sign | (ne << 10) | hm
     up = (rem > 0x1000) | ((rem == 0x1000) & ((hm & 1) != 0))
     out = np.where(norm, h + up.astype(np.int64), out)
-    return out.astype(np.uint16)
+    return out.astype(np.uint16).reshape(shape)
 
 
 def f16_to_f32(bits):
@@ -365,4 +367,25 @@ def ew_map(op, a, b=None, c=None, s0=0.0, s1=0.0, out_kind="f32"):
     with np.errstate(all="ignore"):
         r = _ew_formula(op, x, y, z, s0, s1, f)
         r32 = np.asarray(r, dtype=np.float64).astype(np.float32).reshape(shape)
+    return _round_to(r32, out_kind)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# sum / mean — csrc/ops_rows.cpp:183-270, vkrt/shaders/reduce.comp.in:27-44
+# ---------------------------------------------------------------------------------------------------------
+
+
+def reduce_sum(x, dims=None, keepdim=False, mean=False, out_kind="f32"):
+    """sum (or mean: the sum divided by the reduced element count) of x over `dims` (every dimension when
+    None or empty), accumulated in float64, then one store rounding to out_kind.  The device accumulates in
+    float32, which the reduction tolerance covers.  Returns (stored value as float32, stored bits)."""
+    x = np.asarray(x, dtype=np.float64)
+    axes = tuple(range(x.ndim)) if not dims else tuple(sorted(d % x.ndim for d in dims))
+    n = 1
+    for d in axes:
+        n *= x.shape[d]
+    s = np.sum(x, axis=axes, keepdims=keepdim)
+    with np.errstate(all="ignore"):
+        r = s / n if mean else s
+        r32 = np.asarray(r, dtype=np.float64).astype(np.float32)
     return _round_to(r32, out_kind)

@@ -17,9 +17,10 @@ LIBHRT = os.path.join(PKG, "torch_vulkan", "libhrt.so")
 
 def declared_functions():
     names = []
-    for h in ("hrt.h",):
+    for h in ("hrt.h", "hrt_ops.h"):
         text = open(os.path.join(REPO, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"static inline[^{]*\{[^}]*\}", "", text)  # header-only helpers are not exported
         names += re.findall(r"\b(hrt_[a-z0-9_]+)\s*\(", text)
     return sorted(set(names))
 
@@ -53,7 +54,7 @@ def test_runtime_reports_errors_without_a_device():
 
 
 KERNELS = (
-    ["add_f32", "ew_copy", "ew_fill", "ew_map"]
+    ["add_f32", "ew_copy", "ew_fill", "ew_map", "reduce_sum"]
     + [f"dq8_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_mfma_{k}" for k in ("bf16", "f16")]
@@ -91,7 +92,8 @@ def test_shim_registers_the_reference_operator_surface():
             "div_.Tensor", "neg", "rsqrt", "reciprocal", "exp", "sin", "cos", "sqrt", "tanh", "sigmoid", "relu",
             "silu", "pow.Tensor_Scalar", "gelu", "silu_backward", "gelu_backward", "where.self", "addcmul_",
             "addcdiv_", "addcmul", "addcdiv", "lerp_.Scalar", "lerp.Scalar", "add.Scalar", "add_.Scalar",
-            "sub.Scalar", "sub_.Scalar", "mul.Scalar", "mul_.Scalar", "div.Scalar", "div_.Scalar")
+            "sub.Scalar", "sub_.Scalar", "mul.Scalar", "mul_.Scalar", "div.Scalar", "div_.Scalar",
+            "sum.dim_IntList", "mean.dim", "sum", "mean", "cat")  # + csrc/ops_rows.cpp:342-346
     ]
     missing = [o for o in ops if not torch._C._dispatch_has_kernel_for_dispatch_key(o, "PrivateUse1")]
     assert not missing, missing
@@ -115,7 +117,7 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
     from torch_vulkan import abi
 
     structs = {
-        "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs, "hrt_ew_args": abi.EwArgs,
+        "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs, "hrt_ew_args": abi.EwArgs, "hrt_reduce_args": abi.ReduceArgs,
         "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_mm_reduce_args": abi.MmReduceArgs,
         "hrt_attn_args": abi.AttnArgs,
         "hrt_softmax_args": abi.SoftmaxArgs, "hrt_ln_args": abi.LnArgs, "hrt_dq8_args": abi.Dq8Args,
@@ -155,3 +157,28 @@ def test_python_ew_op_codes_match_the_c_header(tmp_path):
     got = dict(zip(out[::2], map(int, out[1::2])))
     assert got.pop("count") == len(abi.EW_OPS)
     assert got == abi.EW_OPS
+
+
+def test_reduce_workspace_plan_on_the_host():
+    """hrt_reduce_workspace is a pure host function: the fp32 partial-sum workspace "reduce_sum" needs."""
+    from torch_vulkan import abi
+
+    lib = ctypes.CDLL(LIBHRT)
+    lib.hrt_reduce_workspace.restype = ctypes.c_int64
+    lib.hrt_reduce_workspace.argtypes = [ctypes.c_void_p]
+
+    def ws(sizes, strides, mask, dt=abi.BF16, x=1 << 20):
+        a = abi.ReduceArgs()
+        a.x, a.ndim, a.x_dtype, a.out_dtype, a.reduce_mask, a.div = x, len(sizes), dt, dt, mask, 1.0
+        for i, (s, t) in enumerate(zip(sizes, strides)):
+            a.sizes[i], a.strides[i] = s, t
+        return lib.hrt_reduce_workspace(ctypes.byref(a))
+
+    assert ws([4096, 2048], [2048, 1], 0b10) == 0              # one workgroup per row: no split
+    n = ws([1024, 8192], [8192, 1], 0b01)                       # bias gradient: split over rows
+    assert n > 0 and n % 8192 == 0 and n // 8192 <= 1024
+    assert ws([1 << 20], [1], 0b1) > 0                          # full sum: split, one output
+    assert ws([3, 0], [0, 1], 0b10) == 0                        # empty sums
+    assert ws([5], [1], 0b10) == -1                             # reduce_mask beyond ndim
+    assert ws([5], [-1], 0b1) == -1                             # negative stride
+    assert ws([5], [1], 0b1, dt=abi.RAW8) == -1                 # not a float type

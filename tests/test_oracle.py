@@ -446,3 +446,31 @@ def test_ew_oracle_large_argument_sin_cos():
     x = torch.arange(0, 4000, dtype=torch.float32) * 0.37
     for op, fn in (("sin", torch.sin), ("cos", torch.cos)):
         np.testing.assert_allclose(oracle.ew_map(op, x.numpy())[0], fn(x).numpy(), rtol=4e-4, atol=4e-5)
+
+
+# ---- sum / mean (oracle.reduce_sum) ------------------------------------------------------------------------------
+@pytest.mark.parametrize("dims", [None, (0,), (-1,), (1, 2), (0, 3), (0, 1, 2, 3)])
+@pytest.mark.parametrize("keepdim", [False, True])
+@pytest.mark.parametrize("mean", [False, True])
+def test_reduce_oracle_matches_torch(dims, keepdim, mean):
+    x = torch.randn(3, 5, 4, 6, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    fn = torch.mean if mean else torch.sum
+    ref = fn(x) if dims is None else fn(x, dim=dims, keepdim=keepdim)
+    got, _ = oracle.reduce_sum(x.numpy(), dims, keepdim and dims is not None, mean)
+    assert got.shape == tuple(ref.shape)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-6, atol=1e-6)
+
+
+def test_reduce_oracle_closed_forms():
+    n = 1 << 12
+    a = np.arange(n, dtype=np.float64).reshape(64, 64)
+    assert oracle.reduce_sum(a)[0] == n * (n - 1) / 2
+    assert oracle.reduce_sum(a, mean=True)[0] == (n - 1) / 2
+    np.testing.assert_array_equal(oracle.reduce_sum(a, (0,))[0], 64 * np.arange(64) + 64 * 63 * 64 / 2)
+    np.testing.assert_array_equal(oracle.reduce_sum(a, (1,), keepdim=True)[0][:, 0], 64 * 64 * np.arange(64) + 63 * 64 / 2)
+    e = np.zeros((3, 0))
+    assert np.array_equal(oracle.reduce_sum(e, (1,))[0], np.zeros(3))
+    assert np.all(np.isnan(oracle.reduce_sum(e, (1,), mean=True)[0]))
+    # bf16 store rounding of the float64 result
+    r, b = oracle.reduce_sum(np.full((3, 7), 1.0 / 3.0), (1,), out_kind="bf16")
+    assert np.array_equal(b, oracle.round_bf16(np.full(3, 7.0 / 3.0, dtype=np.float32)))

@@ -36,6 +36,7 @@ HRT_SOURCES = [
     "hrt/runtime.cpp",
     "kernels/ew.hip",
     "kernels/ew_map.hip",
+    "kernels/reduce.hip",
     "kernels/dq8.hip",
     "kernels/gemm.hip",
     "kernels/gemm_mfma.hip",

@@ -125,6 +125,27 @@ __global__ __launch_bounds__(256) void ew_copy_vec16(u32x4* __restrict__ dst, co
   if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
+// Same-type copy whose innermost dimension is contiguous on both sides and whole 16-byte chunks long,
+// with 16-byte aligned rows (a slice of a concatenation, a sliced view made contiguous): one chunk per
+// thread, the row found once per chunk.  Sizes and strides of sh are in bytes here; its last dimension
+// is the row (stride 1 chunk).
+__global__ __launch_bounds__(256) void copy_rows16(uint8_t* dst, const uint8_t* src, Shape sh, int64_t row16,
+                                                   int64_t n16) {
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= n16) return;
+  int64_t q = j / row16;
+  const int64_t c = (j - q * row16) * 16;
+  int64_t od = c, os = c;
+  for (int d = sh.ndim - 2; d >= 0; --d) {
+    const int64_t nq = q / sh.sizes[d];
+    const int64_t r = q - nq * sh.sizes[d];
+    od += r * sh.s0[d];
+    os += r * sh.s1[d];
+    q = nq;
+  }
+  __builtin_nontemporal_store(__builtin_nontemporal_load((const u32x4*)(src + os)), (u32x4*)(dst + od));
+}
+
 template <typename S>
 __global__ __launch_bounds__(256) void raw_nd(void* dst, const void* src, Shape sh, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -172,6 +193,16 @@ void queue_cast(const hrt_copy_args& a, const Shape& sh, int64_t n, bool contig,
     hipLaunchKernelGGL((cast_nd<DC, SC>), dim3(grid_for(n, 1)), dim3(256), 0, s, (void*)a.dst, (const void*)a.src, sh, n);
 }
 
+// Same-type copy with a contiguous innermost dimension of whole 16-byte chunks and 16-byte aligned rows.
+bool rows16_ok(const hrt_copy_args& a, const Shape& sh, uint64_t es, int64_t n) {
+  if (a.dst_dtype != a.src_dtype || a.ndim < 2) return false;
+  const int in = a.ndim - 1;
+  if (sh.s0[in] != 1 || sh.s1[in] != 1 || (sh.sizes[in] * (int64_t)es) % 16 || a.dst % 16 || a.src % 16) return false;
+  for (int d = 0; d < in; ++d)
+    if ((sh.s0[d] * (int64_t)es) % 16 || (sh.s1[d] * (int64_t)es) % 16) return false;
+  return cdiv(n * (int64_t)es / 16, 256) < ((int64_t)1 << 31);
+}
+
 bool launch_copy(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_copy_args*>(p);
   if (a.ndim < 0 || a.ndim > HRT_MAX_DIMS) return ctx.fail("ndim out of range");
@@ -212,6 +243,16 @@ bool launch_copy(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
     const int64_t n16 = (int64_t)(n * de) / 16;
     hipLaunchKernelGGL(ew_copy_vec16, dim3((uint32_t)((n16 + 255) / 256)), dim3(256), 0, s, (u32x4*)a.dst,
                        (const u32x4*)a.src, n16);
+  } else if (rows16_ok(a, sh, de, n)) {
+    Shape b = sh;  // byte strides; the row is the last dimension
+    for (int d = 0; d < a.ndim; ++d) {
+      b.s0[d] = sh.s0[d] * (int64_t)de;
+      b.s1[d] = sh.s1[d] * (int64_t)de;
+    }
+    const int64_t row16 = sh.sizes[a.ndim - 1] * (int64_t)de / 16;
+    const int64_t n16 = n * (int64_t)de / 16;
+    hipLaunchKernelGGL(copy_rows16, dim3((uint32_t)cdiv(n16, 256)), dim3(256), 0, s, (uint8_t*)a.dst, (const uint8_t*)a.src,
+                       b, row16, n16);
   } else {
     dim3 g(grid_for(n, 1));
     switch (de) {

@@ -48,6 +48,11 @@ EW_OPS = {n: i for i, n in enumerate((
     "gelu_tanh_bwd", "addcmul", "addcdiv", "lerp_s", "where"))}
 
 
+class ReduceArgs(ctypes.Structure):
+    _fields_ = [("x", u64), ("out", u64), ("ws", u64), ("ndim", i32), ("x_dtype", i32), ("out_dtype", i32),
+                ("reduce_mask", u32), ("div", f32), ("pad", u32), ("sizes", i64 * MAX_DIMS), ("strides", i64 * MAX_DIMS)]
+
+
 class MmArgs(ctypes.Structure):
     _fields_ = [("a", u64), ("b", u64), ("c", u64), ("bias", u64), ("M", i64), ("N", i64), ("K", i64), ("batch", i64),
                 ("a_sb", i64), ("a_sm", i64), ("a_sk", i64), ("b_sb", i64), ("b_sk", i64), ("b_sn", i64),
@@ -133,6 +138,7 @@ class Runtime:
             "hrt_graph_end": (i64, []),
             "hrt_graph_launch": (ctypes.c_int, [i64]),
             "hrt_graph_destroy": (ctypes.c_int, [i64]),
+            "hrt_reduce_workspace": (i64, [vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
