@@ -5,7 +5,7 @@
 // Layout on MI355X.  Reductions are HBM-bound (every input element is read once), so the kernel is chosen
 // by which dimension of x is contiguous, so that a wavefront always reads consecutive memory:
 //   * columns (the contiguous dimension is kept: a bias gradient sum over rows): lanes own consecutive
-//     outputs, V of them each, and walk the reduced coordinates with 16-byte loads, 8 in flight; the
+//     outputs, V of them each, and walk the reduced coordinates with 16-byte loads, 16 in flight; the
 //     four wavefronts of a workgroup take quarters of the coordinates and add up through LDS;
 //   * rows (the contiguous dimension is reduced: row sums, full sums): a wavefront per output for short
 //     rows, else a workgroup per output (and split) streaming 16-byte loads, 4 in flight;
@@ -173,7 +173,8 @@ __device__ __forceinline__ void emit(const RedKArgs& p, int64_t o, float acc) {
 
 // Columns: a workgroup owns 64 * V consecutive outputs (lane l: outputs o0 .. o0 + V - 1); its four
 // wavefronts take consecutive quarters of split blockIdx.y's reduced coordinates and their sums are added
-// through LDS in wavefront order.  Each lane keeps 8 loads in flight.
+// through LDS in wavefront order.  Each lane keeps up to 16 loads in flight (one wavefront per SIMD
+// needs ~64 KB in flight per CU to cover HBM latency).
 template <int XT, int V>
 __global__ __launch_bounds__(256) void red_cols(RedKArgs p) {
   __shared__ float part[3][64 * V];
@@ -198,6 +199,10 @@ __global__ __launch_bounds__(256) void red_cols(RedKArgs p) {
       const int64_t n = min(rsz_in - i, r1 - r);  // elements left in this row and range
       int64_t e = row + i * rin;
       int64_t k = 0;
+      for (; k + 16 <= n; k += 16, e += 16 * rin) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) addv<XT, V>(acc, p.x, e + u * rin);
+      }
       for (; k + 8 <= n; k += 8, e += 8 * rin) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) addv<XT, V>(acc, p.x, e + u * rin);
@@ -309,6 +314,18 @@ __global__ __launch_bounds__(256) void red_finish(RedKArgs p) {
   store_out(p.out, p.odt, o, s / p.div);
 }
 
+// Second pass for few outputs and many splits: a workgroup per output; thread t adds splits t, t + 256,
+// ... in order, then the workgroup's fixed reduction tree combines the threads.
+__global__ __launch_bounds__(256) void red_finish_wide(RedKArgs p) {
+  __shared__ float red[4];
+  const int64_t o = blockIdx.x;
+  const HK_G float* ws = gcptr<float>(p.ws);
+  float a = 0.0f;
+  for (int64_t k = threadIdx.x; k < p.splits; k += 256) a += ws[k * p.n_out + o];
+  a = block_sum<4>(a, red);
+  if (threadIdx.x == 0) store_out(p.out, p.odt, o, a / p.div);
+}
+
 template <int XT>
 void launch_pass1(const RedPlan& P, const RedKArgs& k, hipStream_t s) {
   constexpr int V16 = XT == HRT_F32 ? 4 : 8;
@@ -362,7 +379,9 @@ bool launch_reduce(const void* args, const uint32_t*, hrt::LaunchCtx& ctx) {
     case HRT_BF16: launch_pass1<HRT_BF16>(P, k, ctx.stream); break;
     default: launch_pass1<HRT_F16>(P, k, ctx.stream); break;
   }
-  if (P.splits > 1)
+  if (P.splits > 1 && P.n_out < 256 && P.splits >= 64)
+    hipLaunchKernelGGL(red_finish_wide, dim3((uint32_t)P.n_out), dim3(256), 0, ctx.stream, k);
+  else if (P.splits > 1)
     hipLaunchKernelGGL(red_finish, dim3((uint32_t)cdiv(P.n_out, 256)), dim3(256), 0, ctx.stream, k);
   return hrt::launch_ok(hipGetLastError(), ctx, "reduce_sum");
 }
