@@ -608,6 +608,61 @@ class Bench:
                 "full_sum_f32_64M": case((64 * 1024 * 1024,), torch.float32, 0b1, 2, 340),
                 "cat_bf16_3x1024x2048_dim1": cat}
 
+    def transfers(self):
+        """The block-swap path: host -> device bandwidth for 100 MB (about one DiT block's bf16 weights:
+        QKV 2048x6144, out 2048x2048, MLP 2048x8192 and 8192x2048) from pageable memory (synchronous, what
+        the reference does), from pinned memory synchronously, and asynchronously (hrt_upload_async on the
+        copy stream); then the same asynchronous upload queued beside a run of 1024x2048x8192 bf16 GEMMs
+        that does not touch its destination, against each alone: overlap = (t_gemm + t_upload - t_both) /
+        min(t_gemm, t_upload).  Host wall-clock around a synchronize, median of 5."""
+        import ctypes
+
+        torch, abi, rt, lib = self.torch, self.abi, self.rt, self.rt.lib
+        n = 100 * 1000 * 1000
+        dev = torch.empty(n, dtype=torch.uint8, device=self.dev)
+        pageable = torch.ones(n, dtype=torch.uint8)
+        pin = lib.hrt_host_alloc(n)
+        if not pin:
+            raise RuntimeError("hrt_host_alloc failed: " + rt.last_error())
+        ctypes.memset(pin, 1, n)
+
+        def wall(fn, reps=5):
+            ts = []
+            for _ in range(reps + 1):
+                rt.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                rt.synchronize()
+                ts.append(time.perf_counter() - t0)
+            return statistics.median(ts[1:])
+
+        t_pg = wall(lambda: rt.check(lib.hrt_upload(dev.data_ptr(), pageable.data_ptr(), n), "upload"))
+        t_ps = wall(lambda: rt.check(lib.hrt_upload(dev.data_ptr(), pin, n), "upload"))
+        t_pa = wall(lambda: rt.check(lib.hrt_upload_async(dev.data_ptr(), pin, n), "upload_async"))
+        M, K, N = 1024, 2048, 8192
+        a, w = self.randn((M, K), torch.bfloat16, 1), self.randn((N, K), torch.bfloat16, 2)
+        c = torch.empty((M, N), dtype=torch.bfloat16, device=self.dev)
+        m = abi.MmArgs()
+        m.a, m.b, m.c = a.data_ptr(), w.data_ptr(), c.data_ptr()
+        m.M, m.N, m.K, m.batch = M, N, K, 1
+        m.a_sm, m.a_sk, m.b_sk, m.b_sn, m.c_sm, m.c_sn = K, 1, 1, K, N, 1
+        m.alpha = 1.0
+        reps = max(1, int(t_pa / 40e-6))  # GEMMs (~40 us each) worth about one upload
+        b = rt.batch([("mm_mfma_bf16", m)] * reps)
+        t_gemm = wall(lambda: rt.run_batch(b))
+
+        def both():
+            rt.check(lib.hrt_upload_async(dev.data_ptr(), pin, n), "upload_async")
+            rt.run_batch(b)
+
+        t_both = wall(both)
+        lib.hrt_host_free(pin)
+        gbs = lambda t: round(n / t / 1e9, 2)  # noqa: E731
+        return {"bytes": n, "pageable_sync_gbs": gbs(t_pg), "pinned_sync_gbs": gbs(t_ps), "pinned_async_gbs": gbs(t_pa),
+                "gemm_ms": round(t_gemm * 1e3, 3), "gemms": reps, "upload_async_ms": round(t_pa * 1e3, 3),
+                "both_ms": round(t_both * 1e3, 3),
+                "overlap": round((t_gemm + t_pa - t_both) / min(t_gemm, t_pa), 3)}
+
     # ---- CPU baseline: the reference's CPU path (torch CPU aten) -------------------------------------
     def profile(self, which, n):
         """Launch one kernel of the headline step (or a 64 MiB device copy) n times and return: the workload
@@ -743,6 +798,7 @@ def main():
         line["dequant_int8_8192x2048_bf16"] = bench.dequant()
         line["elementwise"] = bench.elementwise()
         line["reductions"] = bench.reductions()
+        line["block_swap_transfers"] = bench.transfers()
         print("[bench] bandwidth kernels done", file=sys.stderr, flush=True)
     if not args.skip_cpu:
         line["cpu_baseline"] = bench.cpu_baseline()

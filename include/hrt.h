@@ -78,6 +78,26 @@ int hrt_upload(uint64_t dst, const void* src, uint64_t n);
 int hrt_download(void* dst, uint64_t src, uint64_t n);
 int hrt_copy_d2d(uint64_t dst, uint64_t src, uint64_t n);
 
+/* Pinned (page-locked) host memory and asynchronous transfers — the block-swap path (sd-scripts' H2D
+ * block offloader streams frozen weights from host to device every step; the reference serves its
+ * `non_blocking` copies from pageable memory with synchronous transfers, csrc/shim.cpp:195-198, and has
+ * no function of this kind).
+ * hrt_host_alloc: `bytes` of pinned host memory (hipHostMalloc), returned as an address, 0 on failure.
+ * hrt_host_free: releases it; the memory is reused or returned to the driver only after every transfer
+ *   queued before the call has finished, so a buffer may be freed right after an asynchronous copy.
+ * hrt_host_is_pinned: 1 if p lies inside a live block from hrt_host_alloc, else 0.
+ * hrt_upload_async: queues a host -> device copy from pinned memory on the runtime's copy stream and
+ *   returns at once.  The copy starts after all work queued before the call (so it never overwrites data
+ *   earlier kernels still read), and the first later kernel or transfer that touches the destination
+ *   waits for it; work on other memory overlaps the copy.  src must lie in one pinned block (-1 otherwise).
+ * hrt_download_async: queues a device -> host copy into pinned memory in stream order and returns at once;
+ *   the data is valid after hrt_synchronize. */
+uint64_t hrt_host_alloc(uint64_t bytes);
+int hrt_host_free(uint64_t ptr);
+int hrt_host_is_pinned(const void* p);
+int hrt_upload_async(uint64_t dst, const void* src, uint64_t n);
+int hrt_download_async(void* dst, uint64_t src, uint64_t n);
+
 /* Kernel id for a registered kernel name, -1 if unknown.  Names follow the reference's `op_dtype`
  * convention (tools/gen_shaders.py:155-185), e.g. "dq8_bf16", "mm_bf16", "softmax_fwd_f32".
  * The argument block of each kernel is declared in hrt_ops.h.  Replaces `vkrt_kernel_index`

@@ -85,12 +85,70 @@ struct Runtime {
   hipEvent_t prof_ev[2] = {nullptr, nullptr};
   hipEvent_t slots[16] = {};
   std::vector<hipGraphExec_t> graphs;
+  // Asynchronous uploads run on their own stream (default priority) so they overlap kernels.
+  hipStream_t copy_stream = nullptr;
+  hipEvent_t order_ev = nullptr;      // compute-stream position an upload starts after
+  std::vector<hipEvent_t> ev_pool;    // completion events of uploads, reused
+  struct Pending {
+    uint64_t lo, hi;
+    hipEvent_t done;
+  };
+  std::vector<Pending> pending;       // uploads no later device work has waited for yet
+  std::map<uint64_t, uint64_t> pinned;  // live pinned host blocks: base -> bytes
+  struct FreedPinned {
+    uint64_t base, bytes;
+    hipEvent_t after_compute, after_copy;  // reusable once both have completed
+  };
+  std::vector<FreedPinned> pinned_free;
 };
 
 Runtime* g_rt = nullptr;
 std::mutex g_init_mu;
 
-bool in_bounds_locked(uint64_t addr, uint64_t bytes, std::string* err) { return g_rt->alloc->resolve(addr, bytes, err); }
+hipEvent_t take_event(Runtime* rt) {
+  if (!rt->ev_pool.empty()) {
+    hipEvent_t e = rt->ev_pool.back();
+    rt->ev_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return e;
+}
+
+// Make the compute stream wait for every pending upload into [addr, addr + n) (a wait queued on the
+// stream: the host does not block).  After the wait is queued the event may be recorded again.
+void wait_pending(Runtime* rt, uint64_t addr, uint64_t n) {
+  for (size_t i = 0; i < rt->pending.size();) {
+    const Runtime::Pending p = rt->pending[i];
+    if (p.lo < addr + n && addr < p.hi) {
+      (void)hipStreamWaitEvent(rt->stream, p.done, 0);
+      rt->ev_pool.push_back(p.done);
+      rt->pending[i] = rt->pending.back();
+      rt->pending.pop_back();
+    } else {
+      ++i;
+    }
+  }
+}
+
+bool in_bounds_locked(uint64_t addr, uint64_t bytes, std::string* err) {
+  if (!g_rt->alloc->resolve(addr, bytes, err)) return false;
+  if (!g_rt->pending.empty()) wait_pending(g_rt, addr, bytes);
+  return true;
+}
+
+// Pinned block containing [p, p + n), or pinned.end().
+std::map<uint64_t, uint64_t>::const_iterator pinned_of(const Runtime* rt, uint64_t p, uint64_t n) {
+  auto it = rt->pinned.upper_bound(p);
+  if (it == rt->pinned.begin()) return rt->pinned.end();
+  --it;
+  if (p >= it->first + it->second || n > it->first + it->second - p) return rt->pinned.end();
+  return it;
+}
 
 int hip_fail(const char* what, hipError_t e) {
   (void)hipGetLastError();
@@ -135,6 +193,9 @@ int init_runtime() {
   rt->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
   rt->total_mem = prop.totalGlobalMem;
   if ((e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking)) != hipSuccess) return hip_fail("hipStreamCreate", e);
+  if ((e = hipStreamCreateWithFlags(&rt->copy_stream, hipStreamNonBlocking)) != hipSuccess)
+    return hip_fail("hipStreamCreate(copy)", e);
+  if ((e = hipEventCreateWithFlags(&rt->order_ev, hipEventDisableTiming)) != hipSuccess) return hip_fail("hipEventCreate", e);
   rt->backing.stream = rt->stream;
   rt->alloc = std::make_unique<SlabAllocator>(&rt->backing, rt->total_mem);
   const char* pe = std::getenv("HRT_PROFILE");
@@ -166,7 +227,48 @@ bool checked(Runtime* rt, uint64_t addr, uint64_t n) {
     set_error(err);
     return false;
   }
+  if (!rt->pending.empty()) wait_pending(rt, addr, n);
   return true;
+}
+
+// Record where both streams stand when a pinned block is freed (no stream may be recording a graph).
+void mark_freed(Runtime* rt, Runtime::FreedPinned& f) {
+  f.after_compute = take_event(rt);
+  f.after_copy = take_event(rt);
+  if (f.after_compute && f.after_copy) {
+    (void)hipEventRecord(f.after_compute, rt->stream);
+    (void)hipEventRecord(f.after_copy, rt->copy_stream);
+    return;
+  }
+  (void)hipStreamSynchronize(rt->copy_stream);  // no events: wait for the transfers instead
+  (void)hipStreamSynchronize(rt->stream);
+  if (f.after_compute) rt->ev_pool.push_back(f.after_compute);
+  if (f.after_copy) rt->ev_pool.push_back(f.after_copy);
+  f.after_compute = f.after_copy = nullptr;
+  (void)hipHostFree(reinterpret_cast<void*>(f.base));
+  f.base = 0;
+}
+
+// Freed pinned blocks whose transfers have all finished go back to the driver (all: every marked one,
+// after the caller has waited for both streams).  Blocks freed while a graph was being recorded wait to
+// be marked.
+void release_pinned(Runtime* rt, bool all) {
+  for (size_t i = 0; i < rt->pinned_free.size();) {
+    auto& f = rt->pinned_free[i];
+    const bool marked = f.after_compute && f.after_copy;
+    const bool done = f.base == 0 || (marked && (all || (hipEventQuery(f.after_compute) == hipSuccess &&
+                                                         hipEventQuery(f.after_copy) == hipSuccess)));
+    if (done) {
+      if (f.base) (void)hipHostFree(reinterpret_cast<void*>(f.base));
+      if (f.after_compute) rt->ev_pool.push_back(f.after_compute);
+      if (f.after_copy) rt->ev_pool.push_back(f.after_copy);
+      rt->pinned_free[i] = rt->pinned_free.back();
+      rt->pinned_free.pop_back();
+    } else {
+      ++i;
+    }
+  }
+  (void)hipGetLastError();  // hipEventQuery reports hipErrorNotReady through the error state
 }
 
 }  // namespace
@@ -260,6 +362,7 @@ int hrt_free(uint64_t addr) {
   if (!rt) return -1;
   std::lock_guard<std::mutex> l(rt->mu);
   std::string err;
+  if (!rt->pending.empty()) wait_pending(rt, addr, std::max<uint64_t>(rt->alloc->block_bytes(addr), 1));
   if (rt->backing.capturing && !rt->alloc->is_regular_block(addr)) {
     set_error("hrt_free: a dedicated block cannot be released while a graph is being recorded");
     return -1;
@@ -330,6 +433,111 @@ int hrt_copy_d2d(uint64_t dst, uint64_t src, uint64_t n) {
   hipError_t e =
       hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), n, hipMemcpyDeviceToDevice, rt->stream);
   if (e != hipSuccess) return hip_fail("copy_d2d", e);
+  return 0;
+}
+
+uint64_t hrt_host_alloc(uint64_t bytes) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return 0;
+  if (bytes == 0) {
+    set_error("hrt_host_alloc: size 0");
+    return 0;
+  }
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (!rt->pinned_free.empty()) release_pinned(rt, false);
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+  if (e != hipSuccess || !p) {
+    hip_fail("hipHostMalloc", e);
+    return 0;
+  }
+  rt->pinned[reinterpret_cast<uint64_t>(p)] = bytes;
+  return reinterpret_cast<uint64_t>(p);
+}
+
+int hrt_host_free(uint64_t ptr) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  std::lock_guard<std::mutex> l(rt->mu);
+  auto it = rt->pinned.find(ptr);
+  if (it == rt->pinned.end()) {
+    set_error("hrt_host_free: not a pinned block from hrt_host_alloc");
+    return -1;
+  }
+  Runtime::FreedPinned f{ptr, it->second, nullptr, nullptr};
+  rt->pinned.erase(it);
+  if (!rt->backing.capturing) mark_freed(rt, f);  // while recording: marked when the recording ends
+  rt->pinned_free.push_back(f);
+  release_pinned(rt, false);
+  return 0;
+}
+
+int hrt_host_is_pinned(const void* p) {
+  Runtime* rt = g_rt;
+  if (!rt || !p) return 0;
+  std::lock_guard<std::mutex> l(rt->mu);
+  return pinned_of(rt, reinterpret_cast<uint64_t>(p), 1) != rt->pinned.end() ? 1 : 0;
+}
+
+int hrt_upload_async(uint64_t dst, const void* src, uint64_t n) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  if (n == 0) return 0;
+  uint64_t t0 = now_ns();
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (rt->backing.capturing) {
+    set_error("hrt_upload_async: not allowed while a graph is being recorded");
+    return -1;
+  }
+  if (!src || pinned_of(rt, reinterpret_cast<uint64_t>(src), n) == rt->pinned.end()) {
+    set_error("hrt_upload_async: the source is not inside one pinned block from hrt_host_alloc");
+    return -1;
+  }
+  std::string err;
+  if (!rt->alloc->resolve(dst, n, &err)) {
+    g_validation_errors++;
+    set_error(err);
+    return -1;
+  }
+  hipEvent_t done = take_event(rt);
+  if (!done) return hip_fail("hipEventCreate", hipErrorOutOfMemory);
+  // the copy starts after everything queued so far on the compute stream (no overwrite of data that
+  // earlier kernels read) and after earlier uploads (copy stream order)
+  hipError_t e = hipEventRecord(rt->order_ev, rt->stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(rt->copy_stream, rt->order_ev, 0);
+  if (e == hipSuccess) e = hipMemcpyAsync(reinterpret_cast<void*>(dst), src, n, hipMemcpyHostToDevice, rt->copy_stream);
+  if (e == hipSuccess) e = hipEventRecord(done, rt->copy_stream);
+  if (e != hipSuccess) {
+    rt->ev_pool.push_back(done);
+    return hip_fail("upload_async", e);
+  }
+  rt->pending.push_back({dst, dst + n, done});
+  g_stats[2] += now_ns() - t0;
+  g_stats[3]++;
+  g_stats[5] += n;
+  return 0;
+}
+
+int hrt_download_async(void* dst, uint64_t src, uint64_t n) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  if (n == 0) return 0;
+  uint64_t t0 = now_ns();
+  std::lock_guard<std::mutex> l(rt->mu);
+  if (rt->backing.capturing) {
+    set_error("hrt_download_async: not allowed while a graph is being recorded");
+    return -1;
+  }
+  if (!dst || pinned_of(rt, reinterpret_cast<uint64_t>(dst), n) == rt->pinned.end()) {
+    set_error("hrt_download_async: the destination is not inside one pinned block from hrt_host_alloc");
+    return -1;
+  }
+  if (!checked(rt, src, n)) return -1;
+  hipError_t e = hipMemcpyAsync(dst, reinterpret_cast<const void*>(src), n, hipMemcpyDeviceToHost, rt->stream);
+  g_stats[2] += now_ns() - t0;
+  g_stats[3]++;
+  g_stats[6] += n;
+  if (e != hipSuccess) return hip_fail("download_async", e);
   return 0;
 }
 
@@ -411,9 +619,11 @@ int hrt_synchronize(void) {
     return -1;
   }
   uint64_t t0 = now_ns();
-  hipError_t e = hipStreamSynchronize(rt->stream);
+  hipError_t e = hipStreamSynchronize(rt->copy_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
   g_stats[7] += now_ns() - t0;
   if (e != hipSuccess) return hip_fail("synchronize", e);
+  if (!rt->pinned_free.empty()) release_pinned(rt, false);
   return 0;
 }
 
@@ -514,6 +724,7 @@ int hrt_graph_begin(void) {
     set_error("hrt_graph_begin: a graph is already being recorded");
     return -1;
   }
+  if (!rt->pending.empty()) wait_pending(rt, 0, ~0ull);  // earlier uploads: waited for outside the graph
   hipError_t e = hipStreamBeginCapture(rt->stream, hipStreamCaptureModeRelaxed);
   if (e != hipSuccess) return hip_fail("hipStreamBeginCapture", e);
   rt->backing.capturing = true;
@@ -533,6 +744,8 @@ int64_t hrt_graph_end(void) {
   rt->alloc->set_frozen(false);
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(rt->stream, &g);
+  for (auto& f : rt->pinned_free)  // pinned blocks freed during the recording
+    if (f.base && !f.after_compute) mark_freed(rt, f);
   if (e != hipSuccess) return hip_fail("hipStreamEndCapture", e);
   hipGraphExec_t x = nullptr;
   e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);

@@ -189,6 +189,12 @@ class SlabAllocator {
   }
 
   // True when [addr, addr + len) lies inside the requested size of one live block.
+  // Size of the live block starting at base (0 if none).
+  uint64_t block_bytes(uint64_t base) const {
+    auto it = blocks_.find(base);
+    return it == blocks_.end() ? 0 : it->second.size;
+  }
+
   bool resolve(uint64_t addr, uint64_t len, std::string* err) const {
     auto it = blocks_.upper_bound(addr);
     if (it == blocks_.begin()) {

@@ -21,6 +21,7 @@
 
 #include <atomic>
 #include <chrono>
+#include <cstring>
 #include <cstdlib>
 #include <iostream>
 #include <map>
@@ -169,6 +170,25 @@ struct VkAllocator final : public c10::Allocator {
 };
 VkAllocator g_allocator;
 
+// Pinned host memory (tensor.pin_memory(), torch.empty(..., pin_memory=True) with vk as the
+// accelerator): page-locked buffers from the runtime, whose frees wait for in-flight transfers.
+struct VkPinnedAllocator final : public c10::Allocator {
+  static void deleter(void* p) {
+    if (p) hrt_host_free(reinterpret_cast<uint64_t>(p));
+  }
+  c10::DataPtr allocate(size_t n) override {
+    ensure_init();
+    if (n == 0) return {nullptr, nullptr, &deleter, c10::Device(c10::DeviceType::CPU)};
+    uint64_t a = hrt_host_alloc(n);
+    TORCH_CHECK(a != 0, "vk: cannot allocate ", n, " bytes of pinned host memory: ", last_error());
+    void* p = reinterpret_cast<void*>(a);
+    return {p, p, &deleter, c10::Device(c10::DeviceType::CPU)};
+  }
+  c10::DeleterFnPtr raw_deleter() const override { return &deleter; }
+  void copy_data(void* dest, const void* src, std::size_t count) const override { std::memcpy(dest, src, count); }
+};
+VkPinnedAllocator g_pinned_allocator;
+
 // ---- device guard: one device, one stream ----------------------------------------------------------------
 struct VkGuardImpl final : public c10::impl::DeviceGuardImplInterface {
   c10::DeviceType type() const override { return kDev; }
@@ -193,13 +213,14 @@ C10_REGISTER_GUARD_IMPL(PrivateUse1, VkGuardImpl);
 
 // ---- hooks ---------------------------------------------------------------------------------------------------
 struct VkHooks final : public at::PrivateUse1HooksInterface {
+  void init() const override { ensure_init(); }
   bool isBuilt() const override { return true; }
   bool isAvailable() const override { return true; }
   bool hasPrimaryContext(c10::DeviceIndex) const override { return true; }
   at::Device getDeviceFromPtr(void*) const override { return c10::Device(kDev, 0); }
-  bool isPinnedPtr(const void*) const override { return false; }
-  // Transfers are synchronous on return, so pageable host memory serves non_blocking copies as well.
-  at::Allocator* getPinnedMemoryAllocator() const override { return c10::GetCPUAllocator(); }
+  bool isPinnedPtr(const void* p) const override { return hrt_host_is_pinned(p) == 1; }  // 0 before init
+  // non_blocking copies from / to these buffers are asynchronous (hrt_upload_async / hrt_download_async).
+  at::Allocator* getPinnedMemoryAllocator() const override { return &g_pinned_allocator; }
   void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
     auto* impl = storage.unsafeGetStorageImpl();
     const size_t old = impl->nbytes();
@@ -247,12 +268,31 @@ void copy_vk_to_cpu(const at::Tensor& dst, const at::Tensor& src) {
   dst.copy_(host);
 }
 
-void copy_impl(const at::Tensor& dst, const at::Tensor& src) {
+// A non_blocking copy between a dense pinned host tensor and a dense device tensor of the same dtype and
+// shape is queued asynchronously: host -> device on the copy stream (later device work on dst waits for
+// it, other work overlaps it), device -> host in stream order (valid after a synchronize).  Everything
+// else is the synchronous path.
+bool async_ok(const at::Tensor& host, const at::Tensor& dev) {
+  return host.scalar_type() == dev.scalar_type() && host.sizes() == dev.sizes() && host.is_contiguous() &&
+         dev.is_contiguous() && host.numel() > 0 && hrt_host_is_pinned(host.data_ptr()) == 1;
+}
+
+void copy_impl(const at::Tensor& dst, const at::Tensor& src, bool non_blocking = false) {
   if (!is_vk(src) && !is_vk(dst)) {
     dst.copy_(src);
   } else if (!is_vk(src)) {
+    if (non_blocking && async_ok(src, dst)) {
+      hrt_check(hrt_upload_async(addr_of(dst), src.data_ptr(), dst.nbytes()), "upload_async");
+      count_kernel("aten::copy_ (async H2D)");
+      return;
+    }
     copy_cpu_to_vk(dst, src);
   } else if (!is_vk(dst)) {
+    if (non_blocking && async_ok(dst, src)) {
+      hrt_check(hrt_download_async(dst.data_ptr(), addr_of(src), src.nbytes()), "download_async");
+      count_kernel("aten::copy_ (async D2H)");
+      return;
+    }
     copy_vk_to_cpu(dst, src);
   } else if (src.scalar_type() == dst.scalar_type() && src.sizes() == dst.sizes() && src.is_contiguous() &&
              dst.is_contiguous()) {
@@ -268,8 +308,8 @@ void copy_impl(const at::Tensor& dst, const at::Tensor& src) {
   }
 }
 
-at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool /*non_blocking*/) {
-  copy_impl(dst, self);
+at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_blocking) {
+  copy_impl(dst, self, non_blocking);
   return dst;
 }
 
@@ -397,6 +437,20 @@ float event_elapsed(uint32_t a, uint32_t b) {
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("init", [] { ensure_init(); });
+  m.def("empty_pinned", [](std::vector<int64_t> sizes, at::ScalarType dtype) {
+    ensure_init();
+    // torch answers is_pinned() only for accelerators it has initialised itself
+    at::globalContext().lazyInitDevice(kDev);
+    return at::Tensor(at::detail::empty_generic(sizes, &g_pinned_allocator, c10::DispatchKeySet(c10::DispatchKey::CPU),
+                                                dtype, std::nullopt));
+  });
+  m.def("is_pinned", [](const at::Tensor& t) {
+    return t.device().is_cpu() && t.numel() > 0 && hrt_host_is_pinned(t.data_ptr()) == 1;
+  });
+  m.def("stream_stats", [] {
+    ensure_init();
+    return std::vector<uint64_t>{hrt_stat(2), hrt_stat(3), hrt_stat(5), hrt_stat(6)};
+  });
   m.def("dequant_int8", [](const at::Tensor& q, const at::Tensor& scale, at::ScalarType out_dtype) {
     ensure_init();
     return dequant_int8_vk(q, scale, out_dtype);

@@ -198,6 +198,30 @@ def set_coop_enabled(on: bool) -> None:
     _C.set_coop_enabled(bool(on))
 
 
+def empty_pinned(shape, dtype=torch.float32) -> torch.Tensor:
+    """An uninitialised CPU tensor in pinned (page-locked) host memory of the vk runtime.  Copies between it
+    and a dense vk tensor of the same dtype and shape with non_blocking=True are asynchronous: uploads run
+    on the runtime's copy stream and overlap kernels that do not touch their destination (the kernels that
+    do wait for them); downloads are valid after torch_vulkan.synchronize().  The block-swap path:
+    frozen weights kept here and streamed into a ring of device buffers each step."""
+    return _C.empty_pinned(list(shape), dtype)
+
+
+def is_pinned(t: torch.Tensor) -> bool:
+    """True if CPU tensor t lies in vk pinned host memory (what t.is_pinned(device="vk") answers, without
+    PyTorch's deprecation warning for the device argument)."""
+    return bool(_C.is_pinned(t))
+
+
+def pin_memory(t: torch.Tensor) -> torch.Tensor:
+    """A copy of CPU tensor t in vk pinned host memory (see empty_pinned); t itself if it already is."""
+    if is_pinned(t):
+        return t
+    out = _C.empty_pinned(list(t.shape), t.dtype)
+    out.copy_(t)
+    return out
+
+
 def dequant_int8(q, scale, out_dtype=torch.bfloat16):
     """Weight-only int8 dequant: out[r, c] = float(q[r, c]) * float(scale[r, c // 64]) rounded to out_dtype.
 
@@ -268,6 +292,9 @@ def _register():
         "set_memory_limit",
         "peak_live_bytes",
         "reset_peak_live_bytes",
+        "empty_pinned",
+        "pin_memory",
+        "is_pinned",
     ):
         setattr(module, name, globals()[name])
     torch._register_device_module("vk", module)

@@ -120,6 +120,11 @@ class Runtime:
             "hrt_upload": (ctypes.c_int, [u64, vp, u64]),
             "hrt_download": (ctypes.c_int, [vp, u64, u64]),
             "hrt_copy_d2d": (ctypes.c_int, [u64, u64, u64]),
+            "hrt_host_alloc": (u64, [u64]),
+            "hrt_host_free": (ctypes.c_int, [u64]),
+            "hrt_host_is_pinned": (ctypes.c_int, [vp]),
+            "hrt_upload_async": (ctypes.c_int, [u64, vp, u64]),
+            "hrt_download_async": (ctypes.c_int, [vp, u64, u64]),
             "hrt_kernel_index": (ctypes.c_int, [cp]),
             "hrt_dispatch": (ctypes.c_int, [u32, vp, u32, u32, u32, u32]),
             "hrt_dispatch_batch": (ctypes.c_int, [ctypes.POINTER(u32), ctypes.POINTER(vp), ctypes.POINTER(u32), u32]),
