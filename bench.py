@@ -608,6 +608,54 @@ class Bench:
                 "full_sum_f32_64M": case((64 * 1024 * 1024,), torch.float32, 0b1, 2, 340),
                 "cat_bf16_3x1024x2048_dim1": cat}
 
+    def image_ops(self):
+        """VAE-decoder shaped operators through PyTorch on the vk device (the adapters' host work included):
+        conv3x3 512 -> 512 channels at 64x64 bf16 forward and backward (im2col + the MFMA GEMM), group_norm
+        (32 groups) forward / backward on [1, 512, 128, 128] bf16, nearest x2 upsampling of [1, 512, 64, 64]
+        bf16 forward / backward.  GPU time from events around 20 calls after 3 untimed."""
+        torch, rt = self.torch, self.rt
+        import torch.nn.functional as F
+
+        def gpu_ms(fn, n=20):
+            for _ in range(3):
+                fn()
+            rt.synchronize()
+            rt.event_record(2)
+            for _ in range(n):
+                fn()
+            rt.event_record(3)
+            rt.synchronize()
+            return rt.elapsed_ms(2, 3) / n
+
+        bf = torch.bfloat16
+        x = self.randn((1, 512, 64, 64), bf, 60)
+        w = self.randn((512, 512, 3, 3), bf, 61, 0.02)
+        go = self.randn((1, 512, 64, 64), bf, 62)
+        flop = 2.0 * 512 * 512 * 9 * 64 * 64
+        t_conv = gpu_ms(lambda: F.conv2d(x, w, None, padding=1))
+
+        def conv_fb():
+            xx = x.detach().requires_grad_(True)
+            F.conv2d(xx, w, None, padding=1).backward(go)
+
+        t_conv_fb = gpu_ms(conv_fb)  # forward + input gradient (frozen weights)
+        xg = self.randn((1, 512, 128, 128), bf, 63)
+        gw, gb = self.randn((512,), bf, 64), self.randn((512,), bf, 65)
+        gg = self.randn((1, 512, 128, 128), bf, 66)
+        t_gn = gpu_ms(lambda: F.group_norm(xg, 32, gw, gb, 1e-6))
+        _, mean, rstd = torch.native_group_norm(xg, gw, gb, 1, 512, 128 * 128, 32, 1e-6)
+        t_gnb = gpu_ms(lambda: torch.ops.aten.native_group_norm_backward(gg, xg, mean, rstd, gw, 1, 512, 128 * 128, 32,
+                                                                       [True, True, True]))
+        t_up = gpu_ms(lambda: F.interpolate(x, scale_factor=2, mode="nearest"))
+        t_upb = gpu_ms(lambda: torch.ops.aten.upsample_nearest2d_backward(gg, [128, 128], [1, 512, 64, 64]))
+        n_gn = 512 * 128 * 128 * 2
+        return {"conv3x3_512_64x64_fwd": {"ms": round(t_conv, 4), "tflops": round(flop / t_conv / 1e9, 1)},
+                "conv3x3_512_64x64_fwd_dx": {"ms": round(t_conv_fb, 4), "tflops": round(2 * flop / t_conv_fb / 1e9, 1)},
+                "group_norm_fwd_1x512x128x128": {"ms": round(t_gn, 4), "gbs": round(2 * n_gn / t_gn / 1e6, 1)},
+                "group_norm_bwd_1x512x128x128": {"ms": round(t_gnb, 4), "gbs": round(4 * n_gn / t_gnb / 1e6, 1)},
+                "upsample2x_fwd_1x512x64x64": {"ms": round(t_up, 4), "gbs": round(5 * n_gn / 4 / t_up / 1e6, 1)},
+                "upsample2x_bwd_1x512x64x64": {"ms": round(t_upb, 4), "gbs": round(5 * n_gn / 4 / t_upb / 1e6, 1)}}
+
     def transfers(self):
         """The block-swap path: host -> device bandwidth for 100 MB (about one DiT block's bf16 weights:
         QKV 2048x6144, out 2048x2048, MLP 2048x8192 and 8192x2048) from pageable memory (synchronous, what
@@ -799,6 +847,7 @@ def main():
         line["elementwise"] = bench.elementwise()
         line["reductions"] = bench.reductions()
         line["block_swap_transfers"] = bench.transfers()
+        line["image_ops"] = bench.image_ops()
         print("[bench] bandwidth kernels done", file=sys.stderr, flush=True)
     if not args.skip_cpu:
         line["cpu_baseline"] = bench.cpu_baseline()

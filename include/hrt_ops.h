@@ -271,6 +271,53 @@ typedef struct hrt_reduce_args {
 /* fp32 elements of workspace "reduce_sum" needs for these arguments (0: none, -1: invalid arguments). */
 int64_t hrt_reduce_workspace(const hrt_reduce_args* args);
 
+/* "im2col_{f32,bf16,f16}" / "col2im_{f32,bf16,f16}" — the unfolding behind conv2d (NCHW, stride, zero
+ * padding, no dilation) and its adjoint.  im2col: cols[n, (c, kh, kw), (oh, ow)] = x[n, c, oh*SH - PH + kh,
+ * ow*SW - PW + kw] (0 outside x).  col2im: x[n, c, h, w] = sum of the cols entries that im2col takes from
+ * (n, c, h, w), accumulated in fp32 in a fixed order (a gather: no atomics).  x: [N, C, H, W] contiguous,
+ * cols: [N, C*KH*KW, OH*OW] contiguous.  Replaces "im2col_{dt}" / "col2im_{dt}" and Im2colPush
+ * (csrc/ops_conv.cpp:31-35, 78-88, 153-162; vkrt/shaders/im2col.comp.in). */
+typedef struct hrt_im2col_args {
+  uint64_t x, cols;
+  int64_t N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW;
+} hrt_im2col_args;
+
+/* "upsample_nearest_fwd_{dt}" / "upsample_nearest_bwd_{dt}" — nearest-neighbour upsampling of [NC, H, W]
+ * by the integer factors OH / H and OW / W (src index = dst index / factor) and its backward, dst [NC, H, W]
+ * = the sum of each factor block of src [NC, OH, OW] (fp32, fixed order).  Contiguous.  Replaces "up_fwd" /
+ * "up_bwd" and UpPush (csrc/ops_conv.cpp:37-41, 185-221). */
+typedef struct hrt_upsample_args {
+  uint64_t src, dst;
+  int64_t NC, H, W, OH, OW;
+} hrt_upsample_args;
+
+/* "gn_fwd_{dt}": y = (x - mean[n, g]) * rstd[n, g] * w[c] + b[c] over x [N, C, HW] contiguous, G groups of
+ * C / G channels; mean and rstd = 1 / sqrt(var + eps) (biased variance) are written [N, G] in x's dtype,
+ * as PyTorch's CPU kernel returns them; w, b optional (0).  Statistics: fp32 Welford partials over chunks
+ * of each group, merged in a fixed order.  ws: fp32 [hrt_gn_workspace(N, C, HW, G)].
+ * "gn_bwd_{dt}": from g = dL/dy, x, mean, rstd (x's dtype) and optional w: dx (if nonzero) =
+ * rstd*w*g + c2*x + c3 per (n, g) with c2 = (db_g*mean - ds_g)*rstd^3/M, c3 = -c2*mean - db_g*rstd/M,
+ * ds_g = sum over the group of w[c]*sum_hw(g*x), db_g = sum of w[c]*sum_hw(g), M = HW*C/G; dw[c] (if
+ * nonzero) = sum_n (sum_hw(g*x) - sum_hw(g)*mean)*rstd; db[c] = sum_n sum_hw(g).  ws as for the forward.
+ * Replaces "gn_fwd" / "gn_bwd" / "gn_wgrad" and GnPush (csrc/ops_norm.cpp:27-33, 67-142). */
+typedef struct hrt_gn_args {
+  uint64_t x, y, g, mean, rstd, w, b, dx, dw, db, ws;
+  int64_t N, C, HW, G;
+  float eps;
+  uint32_t pad;
+} hrt_gn_args;
+
+/* Workspace of "gn_fwd_*" / "gn_bwd_*": fp32 elements (group-statistics partials, per-channel sums). */
+static inline int64_t hrt_gn_chunks(int64_t C, int64_t HW, int64_t G) {
+  const int64_t m = (C / G) * HW; /* elements per group */
+  int64_t k = (m + 16383) / 16384;
+  return k < 1 ? 1 : (k > 256 ? 256 : k);
+}
+static inline int64_t hrt_gn_workspace(int64_t N, int64_t C, int64_t HW, int64_t G) {
+  const int64_t fwd = N * G * hrt_gn_chunks(C, HW, G) * 3, bwd = 2 * N * C + 2 * N * G;
+  return fwd > bwd ? fwd : bwd;
+}
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,11 @@ bit-exact parts in oracle/csrc/oracle.c):
   layer_norm_fwd / _bwd  vkrt/shaders/ln.comp.in:27-81                          torch float64 layer_norm + autograd, moments
   attention_fwd / _bwd   vkrt/shaders/attn.comp.in:210-395,                     torch float64 math SDPA + autograd, Sk=1,
   attention_delta        attn_coop.comp.in:158-301, csrc/ops_attn.cpp:240-248   identical keys, zero dO, lse closed form
+  conv2d / _backward     csrc/ops_conv.cpp:60-178, im2col.comp.in              torch float64 conv2d + autograd, delta kernels,
+                                                                                adjointness <conv x, g> = <x, conv^T g>
+  upsample_nearest / bwd csrc/ops_conv.cpp:185-221, upsample.comp.in            torch F.interpolate + autograd, block sums
+  group_norm_fwd / _bwd  csrc/ops_norm.cpp:67-142, gn.comp.in                   torch float64 group_norm + autograd, moments,
+                                                                                finite differences
   reduce_sum             csrc/ops_rows.cpp:183-270, reduce.comp.in:27-44       torch float64 sum/mean on strided views, arange
                                                                                 closed forms, empty reductions
   ew_map                 vkrt/shaders/ew.comp.in:115-257,                       torch CPU ops at the reference tests' tolerances,
@@ -32,11 +37,15 @@ from .ops import (  # noqa: F401
     attention_delta,
     attention_fwd,
     bf16_to_f32,
+    conv2d,
+    conv2d_backward,
     dequant_int8,
     ew_map,
     EW_EXACT,
     f16_to_f32,
     gemm,
+    group_norm_bwd,
+    group_norm_fwd,
     layer_norm_bwd,
     layer_norm_fwd,
     reduce_sum,
@@ -45,4 +54,6 @@ from .ops import (  # noqa: F401
     round_f16,
     softmax_bwd,
     softmax_fwd,
+    upsample_nearest,
+    upsample_nearest_backward,
 )

@@ -389,3 +389,104 @@ def reduce_sum(x, dims=None, keepdim=False, mean=False, out_kind="f32"):
         r = s / n if mean else s
         r32 = np.asarray(r, dtype=np.float64).astype(np.float32)
     return _round_to(r32, out_kind)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# conv2d, nearest upsampling, group_norm — csrc/ops_conv.cpp:60-221, vkrt/shaders/im2col.comp.in,
+# upsample.comp.in; csrc/ops_norm.cpp:67-142, vkrt/shaders/gn.comp.in
+# ---------------------------------------------------------------------------------------------------------
+
+
+def _taps(x, KH, KW, stride, padding):
+    """(kh, kw, patch) for every kernel tap: patch[n, c, oh, ow] = zero-padded x at (oh*sh + kh, ow*sw + kw)."""
+    (sh, sw), (ph, pw) = stride, padding
+    N, C, H, W = x.shape
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)))
+    for kh in range(KH):
+        for kw in range(KW):
+            yield kh, kw, xp[:, :, kh:kh + sh * (OH - 1) + 1:sh, kw:kw + sw * (OW - 1) + 1:sw]
+
+
+def conv2d(x, w, b=None, stride=(1, 1), padding=(0, 0)):
+    """NCHW cross-correlation in float64: out[n, o, oh, ow] = sum_{c, kh, kw} w[o, c, kh, kw] * x[n, c,
+    oh*sh - ph + kh, ow*sw - pw + kw] (0 outside x) + b[o].  ops_conv.cpp:91-97 (im2col + product)."""
+    x, w = np.asarray(x, np.float64), np.asarray(w, np.float64)
+    out = None
+    for kh, kw, patch in _taps(x, w.shape[2], w.shape[3], stride, padding):
+        t = np.einsum("nchw,oc->nohw", patch, w[:, :, kh, kw])
+        out = t if out is None else out + t
+    if b is not None:
+        out = out + np.asarray(b, np.float64)[None, :, None, None]
+    return out
+
+
+def conv2d_backward(x, w, gout, stride=(1, 1), padding=(0, 0)):
+    """(dx, dw, db) of conv2d for the output gradient gout, float64: dw[o, c, kh, kw] = sum gout * tap,
+    dx = the adjoint scatter of every tap, db = gout summed over n, h, w.  ops_conv.cpp:126-178."""
+    x, w, gout = (np.asarray(t, np.float64) for t in (x, w, gout))
+    (sh, sw), (ph, pw) = stride, padding
+    N, C, H, W = x.shape
+    KH, KW = w.shape[2], w.shape[3]
+    OH, OW = gout.shape[2], gout.shape[3]
+    gxp = np.zeros((N, C, H + 2 * ph, W + 2 * pw))
+    dw = np.zeros_like(w)
+    for kh, kw, patch in _taps(x, KH, KW, stride, padding):
+        dw[:, :, kh, kw] = np.einsum("nohw,nchw->oc", gout, patch)
+        gxp[:, :, kh:kh + sh * (OH - 1) + 1:sh, kw:kw + sw * (OW - 1) + 1:sw] += np.einsum("nohw,oc->nchw", gout, w[:, :, kh, kw])
+    return gxp[:, :, ph:ph + H, pw:pw + W], dw, gout.sum(axis=(0, 2, 3))
+
+
+def upsample_nearest(x, OH, OW):
+    """Nearest upsampling by integer factors: out[..., oh, ow] = x[..., oh // fh, ow // fw].  upsample.comp.in."""
+    x = np.asarray(x, np.float64)
+    H, W = x.shape[-2:]
+    return x[..., np.arange(OH) // (OH // H), :][..., np.arange(OW) // (OW // W)]
+
+
+def upsample_nearest_backward(g, H, W):
+    """Adjoint of upsample_nearest: the sum of each fh x fw block of g."""
+    g = np.asarray(g, np.float64)
+    *lead, OH, OW = g.shape
+    return g.reshape(*lead, H, OH // H, W, OW // W).sum(axis=(-3, -1))
+
+
+def group_norm_fwd(x, G, w=None, b=None, eps=1e-5):
+    """(y, mean, rstd) of group_norm over x [N, C, *], float64: statistics over the C / G channels of each
+    group and all spatial positions (biased variance), rstd = 1 / sqrt(var + eps), y = (x - mean) * rstd *
+    w[c] + b[c].  ops_norm.cpp:67-95, gn.comp.in."""
+    x = np.asarray(x, np.float64)
+    N, C = x.shape[:2]
+    xg = x.reshape(N, G, -1)
+    mean, var = xg.mean(-1), xg.var(-1)
+    rstd = 1.0 / np.sqrt(var + eps)
+    y = ((xg - mean[..., None]) * rstd[..., None]).reshape(x.shape)
+    shape = (1, C) + (1,) * (x.ndim - 2)
+    if w is not None:
+        y = y * np.asarray(w, np.float64).reshape(shape)
+    if b is not None:
+        y = y + np.asarray(b, np.float64).reshape(shape)
+    return y, mean, rstd
+
+
+def group_norm_bwd(g, x, mean, rstd, G, w=None):
+    """(dx, dw, db) of group_norm, float64, from per-(n, c) sums ds = sum_hw g*x and db = sum_hw g:
+    ds_g, db_g = sums over a group's channels weighted by w; dx = rstd*w*g + c2*x + c3 with
+    c2 = (db_g*mean - ds_g)*rstd^3/M, c3 = -c2*mean - db_g*rstd/M (M = elements per group);
+    dw[c] = sum_n (ds - db*mean)*rstd, db[c] = sum_n db.  ops_norm.cpp:97-142, gn.comp.in."""
+    g, x = np.asarray(g, np.float64), np.asarray(x, np.float64)
+    mean, rstd = np.asarray(mean, np.float64), np.asarray(rstd, np.float64)
+    N, C = x.shape[:2]
+    Cg = C // G
+    gf, xf = g.reshape(N, C, -1), x.reshape(N, C, -1)
+    M = Cg * gf.shape[-1]
+    ds, dbs = (gf * xf).sum(-1), gf.sum(-1)
+    wv = np.ones(C) if w is None else np.asarray(w, np.float64)
+    dsg = (ds * wv).reshape(N, G, Cg).sum(-1)
+    dbg = (dbs * wv).reshape(N, G, Cg).sum(-1)
+    c2 = (dbg * mean - dsg) * rstd ** 3 / M
+    c3 = -c2 * mean - dbg * rstd / M
+    rep = lambda t: np.repeat(t, Cg, axis=1)[..., None]  # noqa: E731  [N, G] -> [N, C, 1]
+    dx = (rep(rstd) * wv[None, :, None] * gf + rep(c2) * xf + rep(c3)).reshape(x.shape)
+    dw = ((ds - dbs * np.repeat(mean, Cg, axis=1)) * np.repeat(rstd, Cg, axis=1)).sum(0)
+    return dx, dw, dbs.sum(0)

@@ -55,6 +55,8 @@ def test_runtime_reports_errors_without_a_device():
 
 KERNELS = (
     ["add_f32", "ew_copy", "ew_fill", "ew_map", "reduce_sum"]
+    + [f"{op}_{k}" for op in ("im2col", "col2im", "upsample_nearest_fwd", "upsample_nearest_bwd", "gn_fwd", "gn_bwd")
+       for k in ("f32", "bf16", "f16")]
     + [f"dq8_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_mfma_{k}" for k in ("bf16", "f16")]
@@ -93,7 +95,9 @@ def test_shim_registers_the_reference_operator_surface():
             "silu", "pow.Tensor_Scalar", "gelu", "silu_backward", "gelu_backward", "where.self", "addcmul_",
             "addcdiv_", "addcmul", "addcdiv", "lerp_.Scalar", "lerp.Scalar", "add.Scalar", "add_.Scalar",
             "sub.Scalar", "sub_.Scalar", "mul.Scalar", "mul_.Scalar", "div.Scalar", "div_.Scalar",
-            "sum.dim_IntList", "mean.dim", "sum", "mean", "cat")  # + csrc/ops_rows.cpp:342-346
+            "sum.dim_IntList", "mean.dim", "sum", "mean", "cat",  # + csrc/ops_rows.cpp:342-346
+            "convolution_overrideable", "convolution_backward_overrideable", "upsample_nearest2d",
+            "upsample_nearest2d_backward", "native_group_norm", "native_group_norm_backward")  # ops_conv/ops_norm
     ]
     missing = [o for o in ops if not torch._C._dispatch_has_kernel_for_dispatch_key(o, "PrivateUse1")]
     assert not missing, missing
@@ -118,6 +122,7 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
 
     structs = {
         "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs, "hrt_ew_args": abi.EwArgs, "hrt_reduce_args": abi.ReduceArgs,
+        "hrt_im2col_args": abi.Im2colArgs, "hrt_upsample_args": abi.UpsampleArgs, "hrt_gn_args": abi.GnArgs,
         "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_mm_reduce_args": abi.MmReduceArgs,
         "hrt_attn_args": abi.AttnArgs,
         "hrt_softmax_args": abi.SoftmaxArgs, "hrt_ln_args": abi.LnArgs, "hrt_dq8_args": abi.Dq8Args,
@@ -182,3 +187,18 @@ def test_reduce_workspace_plan_on_the_host():
     assert ws([5], [1], 0b10) == -1                             # reduce_mask beyond ndim
     assert ws([5], [-1], 0b1) == -1                             # negative stride
     assert ws([5], [1], 0b1, dt=abi.RAW8) == -1                 # not a float type
+
+
+def test_group_norm_workspace_formula_matches_the_header(tmp_path):
+    from torch_vulkan import abi
+
+    cases = [(1, 64, 262144, 32), (2, 8, 25, 4), (3, 2560, 256, 32), (1, 6, 1, 3)]
+    lines = ['#include <stdio.h>', '#include "hrt_ops.h"', "int main(void) {"]
+    lines += [f'  printf("%lld\\n", (long long)hrt_gn_workspace({n}, {c}, {hw}, {g}));' for n, c, hw, g in cases]
+    lines += ["  return 0; }"]
+    src = tmp_path / "gn.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "gn"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True, check=True).stdout.split()]
+    assert got == [abi.gn_workspace(*c) for c in cases]

@@ -1,0 +1,285 @@
+"""conv2d (forward, input/weight/bias gradients), nearest upsampling and group_norm on the vk device.
+
+Mirrors the reference's tests/test_conv.py (its rel-norm tolerances :19, inputs :28-30, cases :46-54) and
+tests/test_group_norm.py (its tolerance rule :15, :38-43, shapes :17-24); every result is also compared
+with the oracle (float64 restatements).  On top: a VAE-decoder sized conv + group_norm + upsample chain,
+group_norm statistics over chunked groups (up to 262144 elements per group), and the kernels' argument
+checks through the C ABI.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+import torch_vulkan  # noqa: E402
+from torch_vulkan import abi  # noqa: E402
+
+dev = torch.device("vk")
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+REL = {torch.float32: 2e-5, torch.bfloat16: 2e-2, torch.float16: 4e-3}
+GN_TOL = {torch.float32: 5e-5, torch.bfloat16: 2.5e-2, torch.float16: 4e-3}
+
+
+@pytest.fixture(autouse=True)
+def _reset():
+    torch_vulkan.reset_fallback_counts()
+    yield
+
+
+def rnd(shape, dtype=torch.float32, seed=0, scale=1.0):
+    """tests/test_conv.py:28-30 of the reference: uniform[-1, 1) * scale."""
+    g = torch.Generator().manual_seed(seed)
+    return ((torch.rand(shape, generator=g) * 2 - 1) * scale).to(dtype)
+
+
+def f64(t):
+    return t.detach().cpu().double().numpy()
+
+
+def rel_close(gpu, ref, dt, what=""):
+    g, c = torch.as_tensor(f64(gpu)), torch.as_tensor(np.asarray(ref, dtype=np.float64))
+    assert g.shape == c.shape, (what, g.shape, c.shape)
+    err = (g - c).norm() / max(c.norm().item(), 1e-12)
+    assert err < REL[dt], f"{what}: rel-L2 {err.item():.3g}"
+
+
+def gn_close(out, ref, dt, what="", mult=1.0):
+    o, r = f64(out), np.asarray(ref, dtype=np.float64)
+    assert o.shape == r.shape, (what, o.shape, r.shape)
+    scale = max(np.abs(r).max(), 1.0)
+    err = np.abs(o - r).max()
+    assert err <= GN_TOL[dt] * scale * mult, f"{what}: max err {err} (scale {scale})"
+
+
+def no_fallback(*names):
+    fb = torch_vulkan.fallback_counts()
+    bad = {n: fb[n] for n in names if n in fb}
+    assert not bad, f"CPU fallback: {bad}"
+
+
+# ---- conv2d (reference tests/test_conv.py:46-105) -----------------------------------------------------------
+CASES = [  # (N, C, H, W, Co, k, stride, pad)
+    (1, 8, 16, 16, 16, 3, 1, 1),
+    (1, 8, 16, 16, 16, 3, 2, 1),
+    (2, 6, 10, 12, 5, 1, 1, 0),
+    (2, 3, 9, 11, 4, 3, 1, 1),
+    (1, 5, 13, 7, 6, 3, 2, 0),
+    (1, 64, 32, 32, 64, 3, 1, 1),
+    (1, 16, 8, 8, 32, 1, 1, 0),
+]
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("bias", [True, False])
+def test_conv_forward_and_input_grad(dt, case, bias):
+    N, C, H, W, Co, k, s, p = case
+    x = rnd((N, C, H, W), dt, 1)
+    w = rnd((Co, C, k, k), dt, 2, scale=0.3)
+    b = rnd((Co,), dt, 3) if bias else None
+    r = rnd((N, Co, (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1), torch.float32, 4)
+    ref = oracle.conv2d(f64(x), f64(w), f64(b) if bias else None, (s, s), (p, p))
+    gref, _, _ = oracle.conv2d_backward(f64(x), f64(w), f64(r.to(dt)), (s, s), (p, p))
+
+    xd = x.to(dev).requires_grad_(True)  # frozen weights, as in LoRA training: only the input gradient
+    out = F.conv2d(xd, w.to(dev), b.to(dev) if bias else None, stride=s, padding=p)
+    rel_close(out, ref, dt, "forward")
+    (out * r.to(dt).to(dev)).sum().backward()
+    rel_close(xd.grad, gref, dt, "grad_input")
+    no_fallback("aten::convolution_overrideable", "aten::convolution_backward_overrideable")
+    assert torch_vulkan.kernel_counts().get("aten::convolution_overrideable", 0) >= 1
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", [CASES[2], CASES[6], CASES[0], CASES[3], CASES[1]])
+def test_conv_weight_and_bias_grad(dt, case):
+    N, C, H, W, Co, k, s, p = case
+    x = rnd((N, C, H, W), dt, 5)
+    w = rnd((Co, C, k, k), dt, 6, scale=0.3)
+    b = rnd((Co,), dt, 7)
+    xd, wd, bd = x.to(dev).requires_grad_(True), w.to(dev).requires_grad_(True), b.to(dev).requires_grad_(True)
+    out = F.conv2d(xd, wd, bd, stride=s, padding=p)
+    r = rnd(out.shape, torch.float32, 8).to(dt)
+    (out * r.to(dev)).sum().backward()
+    gx, gw, gb = oracle.conv2d_backward(f64(x), f64(w), f64(r), (s, s), (p, p))
+    rel_close(xd.grad, gx, dt, "grad_input")
+    rel_close(wd.grad, gw, dt, "grad_weight")
+    rel_close(bd.grad, gb, dt, "grad_bias")
+    no_fallback("aten::convolution_overrideable", "aten::convolution_backward_overrideable")
+
+
+def test_conv_unsupported_cases_still_match_cpu_via_fallback():
+    """groups / dilation run on the CPU and come back (reference :108-114)."""
+    x, w = rnd((1, 4, 8, 8), seed=1), rnd((4, 2, 3, 3), seed=2)
+    out = F.conv2d(x.to(dev), w.to(dev), None, padding=1, groups=2)
+    assert out.device.type == "vk"
+    rel_close(out, F.conv2d(x, w, None, padding=1, groups=2).numpy(), torch.float32, "groups")
+    w2 = rnd((4, 4, 3, 3), seed=3)
+    out = F.conv2d(x.to(dev), w2.to(dev), None, padding=2, dilation=2)
+    rel_close(out, F.conv2d(x, w2, None, padding=2, dilation=2).numpy(), torch.float32, "dilation")
+
+
+def test_conv_rectangular_kernel_stride_padding_and_views():
+    x = rnd((2, 5, 17, 12), seed=9)
+    w = rnd((7, 5, 3, 5), seed=10, scale=0.3)
+    xv = x.to(dev).transpose(2, 3).contiguous().transpose(2, 3)  # non-contiguous input view
+    out = F.conv2d(xv, w.to(dev), None, stride=(2, 1), padding=(1, 2))
+    rel_close(out, oracle.conv2d(f64(x), f64(w), None, (2, 1), (1, 2)), torch.float32, "rect")
+
+
+# ---- nearest upsampling (reference tests/test_conv.py:117-135) -----------------------------------------------
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("shape,scale", [((1, 4, 8, 8), 2), ((2, 3, 5, 7), (2, 3)), ((1, 2, 4, 6), 1)])
+def test_nearest_upsample_forward_backward(dt, shape, scale):
+    x = rnd(shape, dt, 1)
+    sh, sw = (scale, scale) if isinstance(scale, int) else scale
+    xd = x.to(dev).requires_grad_(True)
+    out = F.interpolate(xd, scale_factor=scale, mode="nearest")
+    assert torch.equal(out.cpu(), torch.from_numpy(oracle.upsample_nearest(f64(x), shape[2] * sh, shape[3] * sw)).to(dt))
+    r = rnd(out.shape, torch.float32, 2).to(dt)
+    (out * r.to(dev)).sum().backward()
+    rel_close(xd.grad, oracle.upsample_nearest_backward(f64(r), shape[2], shape[3]), dt, "upsample grad")
+    no_fallback("aten::upsample_nearest2d", "aten::upsample_nearest2d_backward")
+
+
+def test_nearest_upsample_non_integer_factor_falls_back_correctly():
+    x = rnd((1, 2, 5, 5), seed=3)
+    out = F.interpolate(x.to(dev), size=(8, 8), mode="nearest")
+    assert torch.equal(out.cpu(), F.interpolate(x, size=(8, 8), mode="nearest"))
+
+
+# ---- group_norm (reference tests/test_group_norm.py) -------------------------------------------------------
+SHAPES = [((2, 8, 5, 5), 4), ((1, 6, 3, 7), 3), ((3, 4, 9), 2), ((2, 32, 16, 16), 32), ((1, 64, 8, 8), 32),
+          ((2, 12, 1, 1), 4),
+          # the reference's (tests/test_group_norm.py:17-24)
+          ((1, 320, 64, 64), 32), ((1, 1280, 8, 8), 32), ((1, 2560, 16, 16), 32), ((2, 64, 8, 8), 4), ((2, 96, 5, 7), 3),
+          ((2, 32, 1, 1), 32)]
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("affine", [True, False])
+@pytest.mark.parametrize("eps", [1e-5, 1e-6])
+@pytest.mark.parametrize("shape,G", SHAPES)
+def test_group_norm_forward(dt, affine, eps, shape, G):
+    x = rnd(shape, dt, 1, 3.0)
+    C = shape[1]
+    w = rnd((C,), dt, 2) if affine else None
+    b = rnd((C,), dt, 3) if affine else None
+    out = F.group_norm(x.to(dev), G, w.to(dev) if affine else None, b.to(dev) if affine else None, eps)
+    assert out.dtype == dt
+    y, _, _ = oracle.group_norm_fwd(f64(x), G, f64(w) if affine else None, f64(b) if affine else None, eps)
+    gn_close(out, y, dt, "y")
+    no_fallback("aten::native_group_norm")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_group_norm_mean_rstd_dtype_and_shape_match_cpu(dt):
+    x = rnd((2, 8, 4, 4), dt, 5)
+    gpu = torch.native_group_norm(x.to(dev), None, None, 2, 8, 16, 4, 1e-5)
+    cpu = torch.native_group_norm(x, None, None, 2, 8, 16, 4, 1e-5)
+    for c, g in zip(cpu, gpu):
+        assert c.dtype == g.dtype and c.shape == g.shape
+    _, mean, rstd = oracle.group_norm_fwd(f64(x), 4, eps=1e-5)
+    gn_close(gpu[1], mean, dt, "mean")
+    gn_close(gpu[2], rstd, dt, "rstd")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("affine", [True, False])
+@pytest.mark.parametrize("shape,G", SHAPES)
+def test_group_norm_backward(dt, affine, shape, G):
+    x = rnd(shape, dt, 6, 2.0)
+    C = shape[1]
+    w = rnd((C,), dt, 7) if affine else None
+    b = rnd((C,), dt, 8) if affine else None
+    g = rnd(shape, dt, 9)
+    xd = x.to(dev).requires_grad_(True)
+    params = [t.to(dev).requires_grad_(True) for t in (w, b)] if affine else [None, None]
+    out = F.group_norm(xd, G, params[0], params[1], 1e-5)
+    out.backward(g.to(dev))
+    _, mean, rstd = oracle.group_norm_fwd(f64(x), G, eps=1e-5)
+    dx, dw, db = oracle.group_norm_bwd(f64(g), f64(x), mean, rstd, G, f64(w) if affine else None)
+    gn_close(xd.grad, dx, dt, "dx", mult=2.0)
+    if affine:
+        assert params[0].grad.dtype == dt and params[1].grad.dtype == dt
+        gn_close(params[0].grad, dw, dt, "dw", mult=8.0)
+        gn_close(params[1].grad, db, dt, "db", mult=8.0)
+    no_fallback("aten::native_group_norm", "aten::native_group_norm_backward")
+
+
+def test_group_norm_non_contiguous_input_and_weight_dtype():
+    x = rnd((2, 16, 8, 12), torch.float32, 11)
+    w, b = rnd((16,), seed=12), rnd((16,), seed=13)
+    out = F.group_norm(x.to(dev)[:, :, :, ::2], 8, w.to(dev), b.to(dev), 1e-5)
+    y, _, _ = oracle.group_norm_fwd(f64(x[:, :, :, ::2]), 8, f64(w), f64(b), 1e-5)
+    gn_close(out, y, torch.float32)
+    xb = x.to(torch.bfloat16)
+    out = F.group_norm(xb.to(dev), 8, w.to(dev), b.to(dev), 1e-5)  # fp32 affine parameters on bf16 input
+    y, _, _ = oracle.group_norm_fwd(f64(xb), 8, f64(w.to(torch.bfloat16)), f64(b.to(torch.bfloat16)), 1e-5)
+    gn_close(out, y, torch.bfloat16)
+
+
+@pytest.mark.parametrize("HW,G", [(512 * 512, 32), (128 * 128, 8)])
+def test_group_norm_chunked_statistics(HW, G):
+    """Groups of 262144 and 32768 elements with a large mean offset: chunked, shifted fp32 statistics."""
+    C = 64
+    x = (rnd((1, C, HW), torch.float32, 14) + 20.0)
+    out, mean, rstd = torch.native_group_norm(x.to(dev), None, None, 1, C, HW, G, 1e-6)
+    y, m, r = oracle.group_norm_fwd(f64(x), G, eps=1e-6)
+    gn_close(mean, m, torch.float32, "mean")
+    gn_close(rstd, r, torch.float32, "rstd", mult=4.0)
+    gn_close(out, y, torch.float32, "y", mult=4.0)
+
+
+def test_vae_decoder_block_chain():
+    """conv3x3 -> group_norm -> silu -> upsample x2 -> conv3x3 in bf16 at 64x64, forward and backward."""
+    dt = torch.bfloat16
+    x = rnd((1, 128, 64, 64), dt, 20)
+    w1, w2 = rnd((128, 128, 3, 3), dt, 21, 0.05), rnd((64, 128, 3, 3), dt, 22, 0.05)
+    gw, gb = rnd((128,), dt, 23), rnd((128,), dt, 24)
+    xd = x.to(dev).requires_grad_(True)
+    h = F.conv2d(xd, w1.to(dev), None, padding=1)
+    h = F.silu(F.group_norm(h, 32, gw.to(dev), gb.to(dev), 1e-6))
+    h = F.interpolate(h, scale_factor=2, mode="nearest")
+    y = F.conv2d(h, w2.to(dev), None, padding=1)
+    g = rnd(y.shape, dt, 25)
+    y.backward(g.to(dev))
+    # reference: the same chain in float64 torch from the same bf16 inputs
+    xc = torch.from_numpy(f64(x)).requires_grad_(True)
+    hc = F.conv2d(xc, torch.from_numpy(f64(w1)), None, padding=1)
+    hc = F.silu(F.group_norm(hc, 32, torch.from_numpy(f64(gw)), torch.from_numpy(f64(gb)), 1e-6))
+    hc = F.interpolate(hc, scale_factor=2, mode="nearest")
+    yc = F.conv2d(hc, torch.from_numpy(f64(w2)), None, padding=1)
+    yc.backward(torch.from_numpy(f64(g)))
+    rel_close(y, yc.detach().numpy(), dt, "y")
+    rel_close(xd.grad, xc.grad.numpy(), dt, "dx")
+    no_fallback("aten::convolution_overrideable", "aten::convolution_backward_overrideable", "aten::native_group_norm",
+                "aten::native_group_norm_backward", "aten::upsample_nearest2d", "aten::upsample_nearest2d_backward")
+
+
+# ---- argument checks through the C ABI ----------------------------------------------------------------------
+def test_c_abi_rejects_inconsistent_shapes():
+    rt = abi.Runtime()
+    x = torch.zeros(1, 2, 8, 8, device=dev)
+    cols = torch.zeros(1, 18, 64, device=dev)
+    a = abi.Im2colArgs()
+    a.x, a.cols, a.N, a.C, a.H, a.W, a.OH, a.OW, a.KH, a.KW, a.SH, a.SW, a.PH, a.PW = (
+        x.data_ptr(), cols.data_ptr(), 1, 2, 8, 8, 8, 8, 3, 3, 1, 1, 1, 1)
+    rt.dispatch("im2col_f32", a)  # consistent: accepted
+    a.OH = 9
+    with pytest.raises(RuntimeError, match="OH/OW"):
+        rt.dispatch("im2col_f32", a)
+    u = abi.UpsampleArgs()
+    u.src, u.dst, u.NC, u.H, u.W, u.OH, u.OW = x.data_ptr(), cols.data_ptr(), 2, 8, 8, 12, 8
+    with pytest.raises(RuntimeError, match="integer factors"):
+        rt.dispatch("upsample_nearest_fwd_f32", u)
+    gn = abi.GnArgs()
+    gn.x, gn.N, gn.C, gn.HW, gn.G = x.data_ptr(), 1, 2, 64, 3
+    with pytest.raises(RuntimeError, match="G dividing C"):
+        rt.dispatch("gn_fwd_f32", gn)
+    rt.synchronize()

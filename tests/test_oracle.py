@@ -474,3 +474,92 @@ def test_reduce_oracle_closed_forms():
     # bf16 store rounding of the float64 result
     r, b = oracle.reduce_sum(np.full((3, 7), 1.0 / 3.0), (1,), out_kind="bf16")
     assert np.array_equal(b, oracle.round_bf16(np.full(3, 7.0 / 3.0, dtype=np.float32)))
+
+
+# ---- conv2d / nearest upsampling / group_norm --------------------------------------------------------------
+CONV_CASES = [(1, 8, 16, 16, 16, 3, 1, 1), (1, 8, 16, 16, 16, 3, 2, 1), (2, 6, 10, 12, 5, 1, 1, 0), (2, 3, 9, 11, 4, 3, 1, 1),
+              (1, 5, 13, 7, 6, 3, 2, 0), (1, 4, 9, 9, 3, (3, 5), (2, 1), (1, 2))]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv2d_oracle_matches_torch_and_autograd(case):
+    N, C, H, W, Co, k, s, p = case
+    k, s, p = (v if isinstance(v, tuple) else (v, v) for v in (k, s, p))
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(N, C, H, W, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(Co, C, *k, generator=g, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(Co, generator=g, dtype=torch.float64, requires_grad=True)
+    y = F.conv2d(x, w, b, stride=s, padding=p)
+    go = torch.randn(y.shape, generator=g, dtype=torch.float64)
+    y.backward(go)
+    np.testing.assert_allclose(oracle.conv2d(x.detach().numpy(), w.detach().numpy(), b.detach().numpy(), s, p), y.detach().numpy(),
+                               rtol=1e-12, atol=1e-12)
+    dx, dw, db = oracle.conv2d_backward(x.detach().numpy(), w.detach().numpy(), go.numpy(), s, p)
+    for got, ref in ((dx, x.grad), (dw, w.grad), (db, b.grad)):
+        np.testing.assert_allclose(got, ref.numpy(), rtol=1e-11, atol=1e-11)
+
+
+def test_conv2d_oracle_closed_forms():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 3, 7, 8))
+    delta = np.zeros((3, 3, 3, 3))
+    for c in range(3):
+        delta[c, c, 1, 1] = 1.0
+    np.testing.assert_array_equal(oracle.conv2d(x, delta, None, (1, 1), (1, 1)), x)  # identity kernel
+    w = rng.standard_normal((4, 3, 3, 3))
+    y = oracle.conv2d(x, w, None, (2, 2), (1, 1))
+    g = rng.standard_normal(y.shape)
+    dx, _, _ = oracle.conv2d_backward(x, w, g, (2, 2), (1, 1))
+    assert abs((y * g).sum() - (x * dx).sum()) < 1e-9  # the backward is the adjoint
+
+
+def test_upsample_oracle_matches_torch():
+    x = torch.randn(2, 3, 5, 7, dtype=torch.float64, requires_grad=True)
+    y = F.interpolate(x, scale_factor=(2, 3), mode="nearest")
+    g = torch.randn(y.shape, dtype=torch.float64)
+    y.backward(g)
+    np.testing.assert_array_equal(oracle.upsample_nearest(x.detach().numpy(), 10, 21), y.detach().numpy())
+    np.testing.assert_allclose(oracle.upsample_nearest_backward(g.numpy(), 5, 7), x.grad.numpy(), rtol=1e-13)
+    assert np.array_equal(oracle.upsample_nearest_backward(np.ones((1, 1, 4, 6)), 2, 3), np.full((1, 1, 2, 3), 4.0))
+
+
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("shape,G", [((2, 8, 5, 5), 4), ((1, 6, 3, 7), 3), ((3, 4, 9), 2), ((1, 32, 4, 4), 32)])
+def test_group_norm_oracle_matches_torch_and_autograd(affine, shape, G):
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(shape, generator=g, dtype=torch.float64) * 2 + 0.5).requires_grad_(True)
+    C = shape[1]
+    w = (torch.randn(C, generator=g, dtype=torch.float64)).requires_grad_(True) if affine else None
+    b = (torch.randn(C, generator=g, dtype=torch.float64)).requires_grad_(True) if affine else None
+    y = F.group_norm(x, G, w, b, 1e-5)
+    go = torch.randn(shape, generator=g, dtype=torch.float64)
+    y.backward(go)
+    wn = None if w is None else w.detach().numpy()
+    yo, mean, rstd = oracle.group_norm_fwd(x.detach().numpy(), G, wn, None if b is None else b.detach().numpy(), 1e-5)
+    np.testing.assert_allclose(yo, y.detach().numpy(), rtol=1e-10, atol=1e-10)
+    dx, dw, db = oracle.group_norm_bwd(go.numpy(), x.detach().numpy(), mean, rstd, G, wn)
+    np.testing.assert_allclose(dx, x.grad.numpy(), rtol=1e-9, atol=1e-9)
+    if affine:
+        np.testing.assert_allclose(dw, w.grad.numpy(), rtol=1e-9, atol=1e-9)
+        np.testing.assert_allclose(db, b.grad.numpy(), rtol=1e-9, atol=1e-9)
+    # each group of the plain output has mean 0 and variance 1 - eps-correction
+    y0, _, _ = oracle.group_norm_fwd(x.detach().numpy(), G)
+    yg = y0.reshape(shape[0], G, -1)
+    np.testing.assert_allclose(yg.mean(-1), 0.0, atol=1e-12)
+    assert np.all(np.abs(yg.var(-1) - 1.0) < 1e-3)
+
+
+def test_planted_group_norm_dropped_term_is_caught():
+    """A group_norm backward without its c3 term fails the autograd pin."""
+    x = torch.randn(2, 4, 6, dtype=torch.float64, requires_grad=True)
+    y = F.group_norm(x, 2, None, None, 1e-5)
+    go = torch.randn(y.shape, dtype=torch.float64)
+    y.backward(go)
+    _, mean, rstd = oracle.group_norm_fwd(x.detach().numpy(), 2)
+    dx, _, _ = oracle.group_norm_bwd(go.numpy(), x.detach().numpy(), mean, rstd, 2)
+    gf = go.numpy().reshape(2, 4, -1)
+    dsg = (gf * x.detach().numpy().reshape(2, 4, -1)).sum(-1).reshape(2, 2, 2).sum(-1)
+    dbg = gf.sum(-1).reshape(2, 2, 2).sum(-1)
+    c3 = -((dbg * mean - dsg) * rstd ** 3 / 12) * mean - dbg * rstd / 12
+    planted = dx - np.repeat(np.repeat(c3, 2, axis=1)[..., None], 6, axis=2).reshape(dx.shape)
+    assert np.abs(dx - x.grad.numpy()).max() < 1e-10 and np.abs(planted - x.grad.numpy()).max() > 1e-3

@@ -37,6 +37,7 @@ HRT_SOURCES = [
     "kernels/ew.hip",
     "kernels/ew_map.hip",
     "kernels/reduce.hip",
+    "kernels/conv_norm.hip",
     "kernels/dq8.hip",
     "kernels/gemm.hip",
     "kernels/gemm_mfma.hip",
@@ -52,6 +53,7 @@ SHIM_SOURCES = [
     "shim/ops_rows.cpp",
     "shim/ops_quant.cpp",
     "shim/ops_ew.cpp",
+    "shim/ops_conv.cpp",
 ]
 
 

@@ -1,0 +1,359 @@
+// The image-model operators of the step: conv2d's unfolding (im2col) and its adjoint (col2im), nearest
+// upsampling and its backward, and group_norm forward and backward.  Reference: csrc/ops_conv.cpp:31-221,
+// csrc/ops_norm.cpp:27-142 with vkrt/shaders/im2col.comp.in, upsample.comp.in, gn.comp.in.
+//
+// conv2d runs as im2col followed by the MFMA GEMM (the product dominates; the unfolding is a streaming
+// write of the column matrix, coalesced along the output pixels).  col2im is a gather: each input pixel
+// adds the KH*KW column entries it fed, in a fixed order, so the input gradient is deterministic without
+// atomics.  group_norm's statistics are fp32 partial sums over chunks of each group (a group of a VAE
+// layer spans up to millions of elements, so one workgroup per group would leave the GPU idle), each
+// shifted by the chunk's first element and merged with Chan's formula in a fixed order; applying the
+// normalisation and the backward's per-channel sums stream the tensor with coalesced loads.
+#include <algorithm>
+#include <string>
+
+#include "../hrt/registry.h"
+#include "device_common.h"
+
+namespace hk {
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float ldf(uint64_t p, int64_t i) {
+  if constexpr (std::is_same<T, F32>::value) return gcptr<float>(p)[i];
+  else return T::to_f32(gcptr<uint16_t>(p)[i]);
+}
+template <typename T>
+__device__ __forceinline__ void stf(uint64_t p, int64_t i, float v) {
+  if constexpr (std::is_same<T, F32>::value) gptr<float>(p)[i] = v;
+  else gptr<uint16_t>(p)[i] = T::from_f32(v);
+}
+template <typename T>
+constexpr uint64_t esz() {
+  return std::is_same<T, F32>::value ? 4 : 2;
+}
+
+// ---- im2col / col2im ----------------------------------------------------------------------------------
+// grid (cdiv(L, 256), K, N), K = C*KH*KW, L = OH*OW: block (k, n) writes row k of image n's columns.
+template <typename T>
+__global__ __launch_bounds__(256) void im2col_k(hrt_im2col_args a) {
+  const int64_t L = a.OH * a.OW;
+  const int64_t l = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (l >= L) return;
+  const int64_t k = blockIdx.y, n = blockIdx.z;
+  const int64_t kw = k % a.KW, kh = (k / a.KW) % a.KH, c = k / (a.KW * a.KH);
+  const int64_t oh = l / a.OW, ow = l - oh * a.OW;
+  const int64_t h = oh * a.SH - a.PH + kh, w = ow * a.SW - a.PW + kw;
+  float v = 0.0f;
+  if (h >= 0 && h < a.H && w >= 0 && w < a.W) v = ldf<T>(a.x, ((n * a.C + c) * a.H + h) * a.W + w);
+  stf<T>(a.cols, (n * (a.C * a.KH * a.KW) + k) * L + l, v);
+}
+
+// grid (cdiv(H*W, 256), C, N): each input pixel adds the entries im2col copied it to, kh then kw.
+template <typename T>
+__global__ __launch_bounds__(256) void col2im_k(hrt_im2col_args a) {
+  const int64_t HW = a.H * a.W;
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= HW) return;
+  const int64_t c = blockIdx.y, n = blockIdx.z;
+  const int64_t h = p / a.W, w = p - h * a.W;
+  const int64_t L = a.OH * a.OW, K = a.C * a.KH * a.KW;
+  float s = 0.0f;
+  for (int64_t kh = 0; kh < a.KH; ++kh) {
+    const int64_t th = h + a.PH - kh;
+    if (th < 0 || th % a.SH) continue;
+    const int64_t oh = th / a.SH;
+    if (oh >= a.OH) continue;
+    for (int64_t kw = 0; kw < a.KW; ++kw) {
+      const int64_t tw = w + a.PW - kw;
+      if (tw < 0 || tw % a.SW) continue;
+      const int64_t ow = tw / a.SW;
+      if (ow >= a.OW) continue;
+      s += ldf<T>(a.cols, (n * K + (c * a.KH + kh) * a.KW + kw) * L + oh * a.OW + ow);
+    }
+  }
+  stf<T>(a.x, (n * a.C + c) * HW + p, s);
+}
+
+bool im2col_check(const hrt_im2col_args& a, hrt::LaunchCtx& ctx, uint64_t es) {
+  if (a.N <= 0 || a.C <= 0 || a.H <= 0 || a.W <= 0 || a.KH <= 0 || a.KW <= 0 || a.SH <= 0 || a.SW <= 0 || a.PH < 0 ||
+      a.PW < 0)
+    return ctx.fail("sizes and strides must be positive, padding non-negative");
+  if (a.OH != (a.H + 2 * a.PH - a.KH) / a.SH + 1 || a.OW != (a.W + 2 * a.PW - a.KW) / a.SW + 1 ||
+      a.H + 2 * a.PH < a.KH || a.W + 2 * a.PW < a.KW)
+    return ctx.fail("OH/OW do not follow from H, W, the kernel, stride and padding");
+  if (a.C * a.KH * a.KW > 65535 || a.N > 65535 || a.C > 65535) return ctx.fail("C*KH*KW, C and N must be <= 65535");
+  return ctx.check(a.x, (uint64_t)(a.N * a.C * a.H * a.W) * es, "x") &&
+         ctx.check(a.cols, (uint64_t)(a.N * a.C * a.KH * a.KW * a.OH * a.OW) * es, "cols");
+}
+
+template <typename T>
+bool launch_im2col(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_im2col_args*>(p);
+  if (!im2col_check(a, ctx, esz<T>())) return false;
+  const dim3 g((uint32_t)cdiv(a.OH * a.OW, 256), (uint32_t)(a.C * a.KH * a.KW), (uint32_t)a.N);
+  hipLaunchKernelGGL(im2col_k<T>, g, dim3(256), 0, ctx.stream, a);
+  return hrt::launch_ok(hipGetLastError(), ctx, "im2col");
+}
+template <typename T>
+bool launch_col2im(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_im2col_args*>(p);
+  if (!im2col_check(a, ctx, esz<T>())) return false;
+  const dim3 g((uint32_t)cdiv(a.H * a.W, 256), (uint32_t)a.C, (uint32_t)a.N);
+  hipLaunchKernelGGL(col2im_k<T>, g, dim3(256), 0, ctx.stream, a);
+  return hrt::launch_ok(hipGetLastError(), ctx, "col2im");
+}
+HRT_REGISTER("im2col_f32", hrt_im2col_args, launch_im2col<F32>);
+HRT_REGISTER("im2col_bf16", hrt_im2col_args, launch_im2col<BF16>);
+HRT_REGISTER("im2col_f16", hrt_im2col_args, launch_im2col<F16>);
+HRT_REGISTER("col2im_f32", hrt_im2col_args, launch_col2im<F32>);
+HRT_REGISTER("col2im_bf16", hrt_im2col_args, launch_col2im<BF16>);
+HRT_REGISTER("col2im_f16", hrt_im2col_args, launch_col2im<F16>);
+
+// ---- nearest upsampling by integer factors ----------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void up_fwd_k(hrt_upsample_args a, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t ow = i % a.OW, t = i / a.OW, oh = t % a.OH, nc = t / a.OH;
+  const int64_t fh = a.OH / a.H, fw = a.OW / a.W;
+  stf<T>(a.dst, i, ldf<T>(a.src, (nc * a.H + oh / fh) * a.W + ow / fw));
+}
+
+// dst [NC, H, W] = block sums of src [NC, OH, OW] (rows of the block in order, then columns).
+template <typename T>
+__global__ __launch_bounds__(256) void up_bwd_k(hrt_upsample_args a, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t w = i % a.W, t = i / a.W, h = t % a.H, nc = t / a.H;
+  const int64_t fh = a.OH / a.H, fw = a.OW / a.W;
+  float s = 0.0f;
+  for (int64_t y = 0; y < fh; ++y)
+    for (int64_t x = 0; x < fw; ++x) s += ldf<T>(a.src, (nc * a.OH + h * fh + y) * a.OW + w * fw + x);
+  stf<T>(a.dst, i, s);
+}
+
+template <typename T, bool FWD>
+bool launch_up(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_upsample_args*>(p);
+  if (a.NC <= 0 || a.H <= 0 || a.W <= 0 || a.OH < a.H || a.OW < a.W || a.OH % a.H || a.OW % a.W)
+    return ctx.fail("upsample needs positive sizes and integer factors OH / H, OW / W");
+  const uint64_t small = (uint64_t)(a.NC * a.H * a.W) * esz<T>(), big = (uint64_t)(a.NC * a.OH * a.OW) * esz<T>();
+  if (!ctx.check(a.src, FWD ? small : big, "src") || !ctx.check(a.dst, FWD ? big : small, "dst")) return false;
+  const int64_t total = FWD ? a.NC * a.OH * a.OW : a.NC * a.H * a.W;
+  if (FWD) hipLaunchKernelGGL(up_fwd_k<T>, dim3((uint32_t)cdiv(total, 256)), dim3(256), 0, ctx.stream, a, total);
+  else hipLaunchKernelGGL(up_bwd_k<T>, dim3((uint32_t)cdiv(total, 256)), dim3(256), 0, ctx.stream, a, total);
+  return hrt::launch_ok(hipGetLastError(), ctx, "upsample_nearest");
+}
+HRT_REGISTER("upsample_nearest_fwd_f32", hrt_upsample_args, (launch_up<F32, true>));
+HRT_REGISTER("upsample_nearest_fwd_bf16", hrt_upsample_args, (launch_up<BF16, true>));
+HRT_REGISTER("upsample_nearest_fwd_f16", hrt_upsample_args, (launch_up<F16, true>));
+HRT_REGISTER("upsample_nearest_bwd_f32", hrt_upsample_args, (launch_up<F32, false>));
+HRT_REGISTER("upsample_nearest_bwd_bf16", hrt_upsample_args, (launch_up<BF16, false>));
+HRT_REGISTER("upsample_nearest_bwd_f16", hrt_upsample_args, (launch_up<F16, false>));
+
+// ---- group_norm ---------------------------------------------------------------------------------------------
+struct Wf {
+  float n, mean, m2;  // count, mean, sum of squared deviations
+};
+__device__ __forceinline__ Wf wf_merge(Wf a, Wf b) {
+  const float n = a.n + b.n;
+  if (n == 0.0f) return a;
+  const float d = b.mean - a.mean, f = b.n / n;
+  return {n, a.mean + d * f, a.m2 + b.m2 + d * d * a.n * f};
+}
+__device__ __forceinline__ Wf wf_shfl(Wf v, int m) {
+  return {__shfl_xor(v.n, m, 64), __shfl_xor(v.mean, m, 64), __shfl_xor(v.m2, m, 64)};
+}
+// Workgroup-wide merge of 256 lanes' statistics in a fixed tree order; the result is in lane 0 of wave 0.
+__device__ __forceinline__ Wf wf_block(Wf v, Wf* lds) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v = wf_merge(v, wf_shfl(v, m));
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds[w] = v;
+  __syncthreads();
+  return wf_merge(wf_merge(lds[0], lds[1]), wf_merge(lds[2], lds[3]));
+}
+
+// grid (chunks, N*G): statistics of chunk q of group ng (its elements are contiguous: x is [N, C, HW]),
+// each lane summing deviations from the chunk's first element.
+template <typename T>
+__global__ __launch_bounds__(256) void gn_stats_k(hrt_gn_args a, int64_t chunks, int64_t cs) {
+  __shared__ Wf lds[4];
+  const int64_t M = (a.C / a.G) * a.HW;
+  const int64_t ng = blockIdx.y, q = blockIdx.x;
+  const int64_t lo = q * cs, hi = min(M, lo + cs);
+  const int64_t base = ng * M;
+  const float k = lo < hi ? ldf<T>(a.x, base + lo) : 0.0f;  // an empty last chunk reads nothing
+  float s = 0.0f, s2 = 0.0f, cnt = 0.0f;
+  for (int64_t e = lo + threadIdx.x; e < hi; e += 256) {
+    const float d = ldf<T>(a.x, base + e) - k;
+    s += d;
+    s2 += d * d;
+    cnt += 1.0f;
+  }
+  Wf v = cnt > 0.0f ? Wf{cnt, k + s / cnt, s2 - s * s / cnt} : Wf{0.0f, 0.0f, 0.0f};
+  v = wf_block(v, lds);
+  if (threadIdx.x == 0) {
+    HK_G float* ws = gptr<float>(a.ws) + (ng * chunks + q) * 3;
+    ws[0] = v.n;
+    ws[1] = v.mean;
+    ws[2] = fmaxf(v.m2, 0.0f);
+  }
+}
+
+// grid (chunks, N*G): merge the group's chunk statistics (in chunk order), write mean / rstd (chunk 0),
+// normalise chunk q.
+template <typename T>
+__global__ __launch_bounds__(256) void gn_apply_k(hrt_gn_args a, int64_t chunks, int64_t cs) {
+  __shared__ float st[2];
+  const int64_t Cg = a.C / a.G, M = Cg * a.HW;
+  const int64_t ng = blockIdx.y, q = blockIdx.x;
+  if (threadIdx.x == 0) {
+    const HK_G float* ws = gcptr<float>(a.ws) + ng * chunks * 3;
+    Wf v{ws[0], ws[1], ws[2]};
+    for (int64_t i = 1; i < chunks; ++i) v = wf_merge(v, Wf{ws[3 * i], ws[3 * i + 1], ws[3 * i + 2]});
+    const float var = v.m2 / v.n;
+    st[0] = v.mean;
+    st[1] = 1.0f / sqrtf(var + a.eps);
+    if (q == 0) {
+      stf<T>(a.mean, ng, st[0]);
+      stf<T>(a.rstd, ng, st[1]);
+    }
+  }
+  __syncthreads();
+  const float mean = st[0], rstd = st[1];
+  const int64_t g = ng % a.G;
+  const int64_t lo = q * cs, hi = min(M, lo + cs), base = ng * M;
+  for (int64_t e = lo + threadIdx.x; e < hi; e += 256) {
+    const int64_t c = g * Cg + e / a.HW;
+    float y = (ldf<T>(a.x, base + e) - mean) * rstd;
+    if (a.w) y *= ldf<T>(a.w, c);
+    if (a.b) y += ldf<T>(a.b, c);
+    stf<T>(a.y, base + e, y);
+  }
+}
+
+// grid (N*C): ws[nc] = sum_hw g*x, ws[N*C + nc] = sum_hw g.
+template <typename T>
+__global__ __launch_bounds__(256) void gn_bwd_sums_k(hrt_gn_args a) {
+  __shared__ float red[4];
+  const int64_t nc = blockIdx.x, base = nc * a.HW;
+  float ds = 0.0f, db = 0.0f;
+  for (int64_t e = threadIdx.x; e < a.HW; e += 256) {
+    const float g = ldf<T>(a.g, base + e);
+    ds += g * ldf<T>(a.x, base + e);
+    db += g;
+  }
+  ds = block_sum<4>(ds, red);
+  __syncthreads();
+  db = block_sum<4>(db, red);
+  if (threadIdx.x == 0) {
+    gptr<float>(a.ws)[nc] = ds;
+    gptr<float>(a.ws)[a.N * a.C + nc] = db;
+  }
+}
+
+// Per (n, g): c2 and c3 of dx = rstd*w*g + c2*x + c3, into ws[2*N*C + 2*ng + {0, 1}].
+template <typename T>
+__global__ __launch_bounds__(256) void gn_bwd_coef_k(hrt_gn_args a) {
+  const int64_t ng = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (ng >= a.N * a.G) return;
+  const int64_t Cg = a.C / a.G, n = ng / a.G, g = ng % a.G;
+  const HK_G float* ws = gcptr<float>(a.ws);
+  float dsg = 0.0f, dbg = 0.0f;
+  for (int64_t j = 0; j < Cg; ++j) {
+    const int64_t c = g * Cg + j;
+    const float w = a.w ? ldf<T>(a.w, c) : 1.0f;
+    dsg += ws[n * a.C + c] * w;
+    dbg += ws[a.N * a.C + n * a.C + c] * w;
+  }
+  const float mean = ldf<T>(a.mean, ng), rstd = ldf<T>(a.rstd, ng);
+  const float s = 1.0f / (float)(Cg * a.HW);
+  const float c2 = (dbg * mean - dsg) * rstd * rstd * rstd * s;
+  const float c3 = -c2 * mean - dbg * rstd * s;
+  gptr<float>(a.ws)[2 * a.N * a.C + 2 * ng] = c2;
+  gptr<float>(a.ws)[2 * a.N * a.C + 2 * ng + 1] = c3;
+}
+
+// grid (cdiv(HW, 256), N*C): dx = rstd*w*g + c2*x + c3.
+template <typename T>
+__global__ __launch_bounds__(256) void gn_bwd_dx_k(hrt_gn_args a) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= a.HW) return;
+  const int64_t nc = blockIdx.y, n = nc / a.C, c = nc % a.C, ng = n * a.G + c / (a.C / a.G);
+  const HK_G float* ws = gcptr<float>(a.ws) + 2 * a.N * a.C + 2 * ng;
+  const float c1 = ldf<T>(a.rstd, ng) * (a.w ? ldf<T>(a.w, c) : 1.0f);
+  const int64_t i = nc * a.HW + e;
+  stf<T>(a.dx, i, c1 * ldf<T>(a.g, i) + ws[0] * ldf<T>(a.x, i) + ws[1]);
+}
+
+// Thread per channel: dw[c] = sum_n (ds - db*mean)*rstd, db[c] = sum_n db, n in order.
+template <typename T>
+__global__ __launch_bounds__(256) void gn_bwd_wgrad_k(hrt_gn_args a) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= a.C) return;
+  const HK_G float* ws = gcptr<float>(a.ws);
+  const int64_t g = c / (a.C / a.G);
+  float dw = 0.0f, db = 0.0f;
+  for (int64_t n = 0; n < a.N; ++n) {
+    const float ds = ws[n * a.C + c], dbn = ws[a.N * a.C + n * a.C + c];
+    dw += (ds - dbn * ldf<T>(a.mean, n * a.G + g)) * ldf<T>(a.rstd, n * a.G + g);
+    db += dbn;
+  }
+  if (a.dw) stf<T>(a.dw, c, dw);
+  if (a.db) stf<T>(a.db, c, db);
+}
+
+template <typename T>
+bool gn_check(const hrt_gn_args& a, hrt::LaunchCtx& ctx) {
+  if (a.N <= 0 || a.C <= 0 || a.HW <= 0 || a.G <= 0 || a.C % a.G) return ctx.fail("need N, C, HW, G > 0 and G dividing C");
+  const uint64_t es = esz<T>(), n = (uint64_t)(a.N * a.C * a.HW) * es;
+  if (!ctx.check(a.x, n, "x") || !ctx.check(a.ws, (uint64_t)hrt_gn_workspace(a.N, a.C, a.HW, a.G) * 4, "ws")) return false;
+  if (!ctx.check(a.mean, (uint64_t)(a.N * a.G) * es, "mean") || !ctx.check(a.rstd, (uint64_t)(a.N * a.G) * es, "rstd"))
+    return false;
+  if (a.w && !ctx.check(a.w, (uint64_t)a.C * es, "w")) return false;
+  return true;
+}
+
+template <typename T>
+bool launch_gn_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_gn_args*>(p);
+  if (!gn_check<T>(a, ctx)) return false;
+  if (!ctx.check(a.y, (uint64_t)(a.N * a.C * a.HW) * esz<T>(), "y")) return false;
+  if (a.b && !ctx.check(a.b, (uint64_t)a.C * esz<T>(), "b")) return false;
+  if (a.N * a.G > 65535) return ctx.fail("N * G must be <= 65535");
+  const int64_t chunks = hrt_gn_chunks(a.C, a.HW, a.G), M = (a.C / a.G) * a.HW, cs = cdiv(M, chunks);
+  const dim3 g((uint32_t)chunks, (uint32_t)(a.N * a.G));
+  hipLaunchKernelGGL(gn_stats_k<T>, g, dim3(256), 0, ctx.stream, a, chunks, cs);
+  hipLaunchKernelGGL(gn_apply_k<T>, g, dim3(256), 0, ctx.stream, a, chunks, cs);
+  return hrt::launch_ok(hipGetLastError(), ctx, "gn_fwd");
+}
+
+template <typename T>
+bool launch_gn_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_gn_args*>(p);
+  if (!gn_check<T>(a, ctx)) return false;
+  const uint64_t n = (uint64_t)(a.N * a.C * a.HW) * esz<T>();
+  if (!ctx.check(a.g, n, "g") || (a.dx && !ctx.check(a.dx, n, "dx")) ||
+      (a.dw && !ctx.check(a.dw, (uint64_t)a.C * esz<T>(), "dw")) || (a.db && !ctx.check(a.db, (uint64_t)a.C * esz<T>(), "db")))
+    return false;
+  if (a.N * a.C >= ((int64_t)1 << 31)) return ctx.fail("N * C must be < 2^31");
+  if (a.dx && a.N * a.C > 65535) return ctx.fail("N * C must be <= 65535 for dx");
+  hipLaunchKernelGGL(gn_bwd_sums_k<T>, dim3((uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
+  if (a.dx) {
+    hipLaunchKernelGGL(gn_bwd_coef_k<T>, dim3((uint32_t)cdiv(a.N * a.G, 256)), dim3(256), 0, ctx.stream, a);
+    hipLaunchKernelGGL(gn_bwd_dx_k<T>, dim3((uint32_t)cdiv(a.HW, 256), (uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
+  }
+  if (a.dw || a.db) hipLaunchKernelGGL(gn_bwd_wgrad_k<T>, dim3((uint32_t)cdiv(a.C, 256)), dim3(256), 0, ctx.stream, a);
+  return hrt::launch_ok(hipGetLastError(), ctx, "gn_bwd");
+}
+HRT_REGISTER("gn_fwd_f32", hrt_gn_args, launch_gn_fwd<F32>);
+HRT_REGISTER("gn_fwd_bf16", hrt_gn_args, launch_gn_fwd<BF16>);
+HRT_REGISTER("gn_fwd_f16", hrt_gn_args, launch_gn_fwd<F16>);
+HRT_REGISTER("gn_bwd_f32", hrt_gn_args, launch_gn_bwd<F32>);
+HRT_REGISTER("gn_bwd_bf16", hrt_gn_args, launch_gn_bwd<BF16>);
+HRT_REGISTER("gn_bwd_f16", hrt_gn_args, launch_gn_bwd<F16>);
+
+}  // namespace
+}  // namespace hk

@@ -53,6 +53,26 @@ class ReduceArgs(ctypes.Structure):
                 ("reduce_mask", u32), ("div", f32), ("pad", u32), ("sizes", i64 * MAX_DIMS), ("strides", i64 * MAX_DIMS)]
 
 
+class Im2colArgs(ctypes.Structure):
+    _fields_ = [("x", u64), ("cols", u64)] + [(n, i64) for n in ("N", "C", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW", "PH", "PW")]
+
+
+class UpsampleArgs(ctypes.Structure):
+    _fields_ = [("src", u64), ("dst", u64), ("NC", i64), ("H", i64), ("W", i64), ("OH", i64), ("OW", i64)]
+
+
+class GnArgs(ctypes.Structure):
+    _fields_ = [(n, u64) for n in ("x", "y", "g", "mean", "rstd", "w", "b", "dx", "dw", "db", "ws")] + [
+        ("N", i64), ("C", i64), ("HW", i64), ("G", i64), ("eps", f32), ("pad", u32)]
+
+
+def gn_workspace(N, C, HW, G):
+    """hrt_gn_workspace (include/hrt_ops.h): fp32 elements of the group_norm workspace."""
+    m = (C // G) * HW
+    chunks = min(max((m + 16383) // 16384, 1), 256)
+    return max(N * G * chunks * 3, 2 * N * C + 2 * N * G)
+
+
 class MmArgs(ctypes.Structure):
     _fields_ = [("a", u64), ("b", u64), ("c", u64), ("bias", u64), ("M", i64), ("N", i64), ("K", i64), ("batch", i64),
                 ("a_sb", i64), ("a_sm", i64), ("a_sk", i64), ("b_sb", i64), ("b_sk", i64), ("b_sn", i64),
