@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
     ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy", "gemm", "gemm1024", "dq8", "softmax", "ln", "dequant",
-                                          "dit", "ew", "reduce"],
+                                          "dit", "ew", "reduce", "image"],
                     help="launch one kernel (or one benchmark workload) --steps times, untimed")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR", help="summarise rocprofv3 --pmc output directories")
     return ap.parse_args()
@@ -719,7 +719,7 @@ class Bench:
         workloads = {"gemm": lambda: self.gemm(1024, 2048, 8192, "nt"), "gemm1024": lambda: self.gemm(1024, 1024, 1024, "nn", True),
                      "dq8": lambda: self.dq8_linear(1024), "softmax": self.softmax, "ln": self.layer_norm,
                      "dequant": self.dequant, "dit": self.dit_lora_stack, "ew": self.elementwise,
-                     "reduce": self.reductions}
+                     "reduce": self.reductions, "image": self.image_ops}
         if which in workloads:
             self.profile_n = n
             workloads[which]()

@@ -32,6 +32,58 @@ template <typename T>
 constexpr uint64_t esz() {
   return std::is_same<T, F32>::value ? 4 : 2;
 }
+// Elements per 16-byte access.
+template <typename T>
+constexpr int vec16() {
+  return std::is_same<T, F32>::value ? 4 : 8;
+}
+// 16 bytes at element i (a multiple of vec16<T>() from a 16-byte aligned base).
+template <typename T>
+__device__ __forceinline__ void ldv(uint64_t p, int64_t i, float (&v)[vec16<T>()]) {
+  if constexpr (std::is_same<T, F32>::value) {
+    const f32x4 u = gcptr<f32x4>(p)[i / 4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = u[j];
+  } else {
+    const u32x4 u = gcptr<u32x4>(p)[i / 8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = lo16<T>(u[j]);
+      v[2 * j + 1] = hi16<T>(u[j]);
+    }
+  }
+}
+template <typename T>
+__device__ __forceinline__ void stv(uint64_t p, int64_t i, const float (&v)[vec16<T>()]) {
+  if constexpr (std::is_same<T, F32>::value) {
+    gptr<f32x4>(p)[i / 4] = f32x4{v[0], v[1], v[2], v[3]};
+  } else {
+    u32x4 u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) u[j] = pack2<T>(v[2 * j], v[2 * j + 1]);
+    gptr<u32x4>(p)[i / 8] = u;
+  }
+}
+
+// V elements at i: one 16-byte access when V == vec16<T>(), else V single ones.
+template <typename T, int V>
+__device__ __forceinline__ void ldn(uint64_t p, int64_t i, float (&v)[V]) {
+  if constexpr (V == vec16<T>()) {
+    ldv<T>(p, i, v);
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = ldf<T>(p, i + j);
+  }
+}
+template <typename T, int V>
+__device__ __forceinline__ void stn(uint64_t p, int64_t i, const float (&v)[V]) {
+  if constexpr (V == vec16<T>()) {
+    stv<T>(p, i, v);
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) stf<T>(p, i + j, v[j]);
+  }
+}
 
 // ---- im2col / col2im ----------------------------------------------------------------------------------
 // grid (cdiv(L, 256), K, N), K = C*KH*KW, L = OH*OW: block (k, n) writes row k of image n's columns.
@@ -47,6 +99,28 @@ __global__ __launch_bounds__(256) void im2col_k(hrt_im2col_args a) {
   float v = 0.0f;
   if (h >= 0 && h < a.H && w >= 0 && w < a.W) v = ldf<T>(a.x, ((n * a.C + c) * a.H + h) * a.W + w);
   stf<T>(a.cols, (n * (a.C * a.KH * a.KW) + k) * L + l, v);
+}
+
+// As im2col_k with vec16 consecutive output pixels per lane (OW a multiple of it: one 16-byte store).
+template <typename T>
+__global__ __launch_bounds__(256) void im2col_vec_k(hrt_im2col_args a) {
+  constexpr int V = vec16<T>();
+  const int64_t L = a.OH * a.OW;
+  const int64_t l0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+  if (l0 >= L) return;
+  const int64_t k = blockIdx.y, n = blockIdx.z;
+  const int64_t kw = k % a.KW, kh = (k / a.KW) % a.KH, c = k / (a.KW * a.KH);
+  const int64_t oh = l0 / a.OW, ow0 = l0 - oh * a.OW;
+  const int64_t h = oh * a.SH - a.PH + kh;
+  float v[V];
+  const bool row = h >= 0 && h < a.H;
+  const int64_t xrow = ((n * a.C + c) * a.H + h) * a.W;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int64_t w = (ow0 + j) * a.SW - a.PW + kw;
+    v[j] = (row && w >= 0 && w < a.W) ? ldf<T>(a.x, xrow + w) : 0.0f;
+  }
+  stv<T>(a.cols, (n * (a.C * a.KH * a.KW) + k) * L + l0, v);
 }
 
 // grid (cdiv(H*W, 256), C, N): each input pixel adds the entries im2col copied it to, kh then kw.
@@ -91,8 +165,14 @@ template <typename T>
 bool launch_im2col(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_im2col_args*>(p);
   if (!im2col_check(a, ctx, esz<T>())) return false;
-  const dim3 g((uint32_t)cdiv(a.OH * a.OW, 256), (uint32_t)(a.C * a.KH * a.KW), (uint32_t)a.N);
-  hipLaunchKernelGGL(im2col_k<T>, g, dim3(256), 0, ctx.stream, a);
+  constexpr int V = vec16<T>();
+  if (a.OW % V == 0 && a.cols % 16 == 0) {
+    const dim3 g((uint32_t)cdiv(a.OH * a.OW / V, 256), (uint32_t)(a.C * a.KH * a.KW), (uint32_t)a.N);
+    hipLaunchKernelGGL(im2col_vec_k<T>, g, dim3(256), 0, ctx.stream, a);
+  } else {
+    const dim3 g((uint32_t)cdiv(a.OH * a.OW, 256), (uint32_t)(a.C * a.KH * a.KW), (uint32_t)a.N);
+    hipLaunchKernelGGL(im2col_k<T>, g, dim3(256), 0, ctx.stream, a);
+  }
   return hrt::launch_ok(hipGetLastError(), ctx, "im2col");
 }
 template <typename T>
@@ -120,6 +200,21 @@ __global__ __launch_bounds__(256) void up_fwd_k(hrt_upsample_args a, int64_t tot
   stf<T>(a.dst, i, ldf<T>(a.src, (nc * a.H + oh / fh) * a.W + ow / fw));
 }
 
+// vec16 consecutive output pixels of one output row per lane (OW a multiple of it): one 16-byte store.
+template <typename T>
+__global__ __launch_bounds__(256) void up_fwd_vec_k(hrt_upsample_args a, int64_t total) {
+  constexpr int V = vec16<T>();
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+  if (i >= total) return;
+  const int64_t ow0 = i % a.OW, t = i / a.OW, oh = t % a.OH, nc = t / a.OH;
+  const int64_t fh = a.OH / a.H, fw = a.OW / a.W;
+  const int64_t srow = (nc * a.H + oh / fh) * a.W;
+  float v[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) v[j] = ldf<T>(a.src, srow + (ow0 + j) / fw);
+  stv<T>(a.dst, i, v);
+}
+
 // dst [NC, H, W] = block sums of src [NC, OH, OW] (rows of the block in order, then columns).
 template <typename T>
 __global__ __launch_bounds__(256) void up_bwd_k(hrt_upsample_args a, int64_t total) {
@@ -141,8 +236,13 @@ bool launch_up(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const uint64_t small = (uint64_t)(a.NC * a.H * a.W) * esz<T>(), big = (uint64_t)(a.NC * a.OH * a.OW) * esz<T>();
   if (!ctx.check(a.src, FWD ? small : big, "src") || !ctx.check(a.dst, FWD ? big : small, "dst")) return false;
   const int64_t total = FWD ? a.NC * a.OH * a.OW : a.NC * a.H * a.W;
-  if (FWD) hipLaunchKernelGGL(up_fwd_k<T>, dim3((uint32_t)cdiv(total, 256)), dim3(256), 0, ctx.stream, a, total);
-  else hipLaunchKernelGGL(up_bwd_k<T>, dim3((uint32_t)cdiv(total, 256)), dim3(256), 0, ctx.stream, a, total);
+  constexpr int V = vec16<T>();
+  if (FWD && a.OW % V == 0 && a.dst % 16 == 0)
+    hipLaunchKernelGGL(up_fwd_vec_k<T>, dim3((uint32_t)cdiv(total / V, 256)), dim3(256), 0, ctx.stream, a, total);
+  else if (FWD)
+    hipLaunchKernelGGL(up_fwd_k<T>, dim3((uint32_t)cdiv(total, 256)), dim3(256), 0, ctx.stream, a, total);
+  else
+    hipLaunchKernelGGL(up_bwd_k<T>, dim3((uint32_t)cdiv(total, 256)), dim3(256), 0, ctx.stream, a, total);
   return hrt::launch_ok(hipGetLastError(), ctx, "upsample_nearest");
 }
 HRT_REGISTER("upsample_nearest_fwd_f32", hrt_upsample_args, (launch_up<F32, true>));
@@ -176,8 +276,9 @@ __device__ __forceinline__ Wf wf_block(Wf v, Wf* lds) {
 }
 
 // grid (chunks, N*G): statistics of chunk q of group ng (its elements are contiguous: x is [N, C, HW]),
-// each lane summing deviations from the chunk's first element.
-template <typename T>
+// each lane summing deviations from the chunk's first element.  V elements per access (V divides HW and
+// the chunk size).
+template <typename T, int V>
 __global__ __launch_bounds__(256) void gn_stats_k(hrt_gn_args a, int64_t chunks, int64_t cs) {
   __shared__ Wf lds[4];
   const int64_t M = (a.C / a.G) * a.HW;
@@ -186,25 +287,30 @@ __global__ __launch_bounds__(256) void gn_stats_k(hrt_gn_args a, int64_t chunks,
   const int64_t base = ng * M;
   const float k = lo < hi ? ldf<T>(a.x, base + lo) : 0.0f;  // an empty last chunk reads nothing
   float s = 0.0f, s2 = 0.0f, cnt = 0.0f;
-  for (int64_t e = lo + threadIdx.x; e < hi; e += 256) {
-    const float d = ldf<T>(a.x, base + e) - k;
-    s += d;
-    s2 += d * d;
-    cnt += 1.0f;
+  for (int64_t e = lo + (int64_t)threadIdx.x * V; e < hi; e += 256 * V) {
+    float v[V];
+    ldn<T, V>(a.x, base + e, v);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float d = v[j] - k;
+      s += d;
+      s2 += d * d;
+    }
+    cnt += (float)V;
   }
-  Wf v = cnt > 0.0f ? Wf{cnt, k + s / cnt, s2 - s * s / cnt} : Wf{0.0f, 0.0f, 0.0f};
-  v = wf_block(v, lds);
+  Wf w = cnt > 0.0f ? Wf{cnt, k + s / cnt, s2 - s * s / cnt} : Wf{0.0f, 0.0f, 0.0f};
+  w = wf_block(w, lds);
   if (threadIdx.x == 0) {
     HK_G float* ws = gptr<float>(a.ws) + (ng * chunks + q) * 3;
-    ws[0] = v.n;
-    ws[1] = v.mean;
-    ws[2] = fmaxf(v.m2, 0.0f);
+    ws[0] = w.n;
+    ws[1] = w.mean;
+    ws[2] = fmaxf(w.m2, 0.0f);
   }
 }
 
 // grid (chunks, N*G): merge the group's chunk statistics (in chunk order), write mean / rstd (chunk 0),
-// normalise chunk q.
-template <typename T>
+// normalise chunk q (V consecutive elements share a channel since V divides HW).
+template <typename T, int V>
 __global__ __launch_bounds__(256) void gn_apply_k(hrt_gn_args a, int64_t chunks, int64_t cs) {
   __shared__ float st[2];
   const int64_t Cg = a.C / a.G, M = Cg * a.HW;
@@ -225,25 +331,32 @@ __global__ __launch_bounds__(256) void gn_apply_k(hrt_gn_args a, int64_t chunks,
   const float mean = st[0], rstd = st[1];
   const int64_t g = ng % a.G;
   const int64_t lo = q * cs, hi = min(M, lo + cs), base = ng * M;
-  for (int64_t e = lo + threadIdx.x; e < hi; e += 256) {
+  for (int64_t e = lo + (int64_t)threadIdx.x * V; e < hi; e += 256 * V) {
     const int64_t c = g * Cg + e / a.HW;
-    float y = (ldf<T>(a.x, base + e) - mean) * rstd;
-    if (a.w) y *= ldf<T>(a.w, c);
-    if (a.b) y += ldf<T>(a.b, c);
-    stf<T>(a.y, base + e, y);
+    const float wc = a.w ? ldf<T>(a.w, c) : 1.0f, bc = a.b ? ldf<T>(a.b, c) : 0.0f;
+    float v[V];
+    ldn<T, V>(a.x, base + e, v);
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = (v[j] - mean) * rstd * wc + bc;
+    stn<T, V>(a.y, base + e, v);
   }
 }
 
 // grid (N*C): ws[nc] = sum_hw g*x, ws[N*C + nc] = sum_hw g.
-template <typename T>
+template <typename T, int V>
 __global__ __launch_bounds__(256) void gn_bwd_sums_k(hrt_gn_args a) {
   __shared__ float red[4];
   const int64_t nc = blockIdx.x, base = nc * a.HW;
   float ds = 0.0f, db = 0.0f;
-  for (int64_t e = threadIdx.x; e < a.HW; e += 256) {
-    const float g = ldf<T>(a.g, base + e);
-    ds += g * ldf<T>(a.x, base + e);
-    db += g;
+  for (int64_t e = (int64_t)threadIdx.x * V; e < a.HW; e += 256 * V) {
+    float g[V], x[V];
+    ldn<T, V>(a.g, base + e, g);
+    ldn<T, V>(a.x, base + e, x);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      ds += g[j] * x[j];
+      db += g[j];
+    }
   }
   ds = block_sum<4>(ds, red);
   __syncthreads();
@@ -276,16 +389,21 @@ __global__ __launch_bounds__(256) void gn_bwd_coef_k(hrt_gn_args a) {
   gptr<float>(a.ws)[2 * a.N * a.C + 2 * ng + 1] = c3;
 }
 
-// grid (cdiv(HW, 256), N*C): dx = rstd*w*g + c2*x + c3.
-template <typename T>
+// grid (cdiv(HW / V, 256), N*C): dx = rstd*w*g + c2*x + c3.
+template <typename T, int V>
 __global__ __launch_bounds__(256) void gn_bwd_dx_k(hrt_gn_args a) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
   if (e >= a.HW) return;
   const int64_t nc = blockIdx.y, n = nc / a.C, c = nc % a.C, ng = n * a.G + c / (a.C / a.G);
   const HK_G float* ws = gcptr<float>(a.ws) + 2 * a.N * a.C + 2 * ng;
-  const float c1 = ldf<T>(a.rstd, ng) * (a.w ? ldf<T>(a.w, c) : 1.0f);
+  const float c1 = ldf<T>(a.rstd, ng) * (a.w ? ldf<T>(a.w, c) : 1.0f), c2 = ws[0], c3 = ws[1];
   const int64_t i = nc * a.HW + e;
-  stf<T>(a.dx, i, c1 * ldf<T>(a.g, i) + ws[0] * ldf<T>(a.x, i) + ws[1]);
+  float g[V], x[V];
+  ldn<T, V>(a.g, i, g);
+  ldn<T, V>(a.x, i, x);
+#pragma unroll
+  for (int j = 0; j < V; ++j) g[j] = c1 * g[j] + c2 * x[j] + c3;
+  stn<T, V>(a.dx, i, g);
 }
 
 // Thread per channel: dw[c] = sum_n (ds - db*mean)*rstd, db[c] = sum_n db, n in order.
@@ -323,10 +441,18 @@ bool launch_gn_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!ctx.check(a.y, (uint64_t)(a.N * a.C * a.HW) * esz<T>(), "y")) return false;
   if (a.b && !ctx.check(a.b, (uint64_t)a.C * esz<T>(), "b")) return false;
   if (a.N * a.G > 65535) return ctx.fail("N * G must be <= 65535");
-  const int64_t chunks = hrt_gn_chunks(a.C, a.HW, a.G), M = (a.C / a.G) * a.HW, cs = cdiv(M, chunks);
+  constexpr int V = vec16<T>();
+  const bool vec = a.HW % V == 0 && a.x % 16 == 0 && a.y % 16 == 0;
+  const int64_t chunks = hrt_gn_chunks(a.C, a.HW, a.G), M = (a.C / a.G) * a.HW;
+  const int64_t cs = vec ? cdiv(cdiv(M, chunks), V) * V : cdiv(M, chunks);  // chunks start on a vector
   const dim3 g((uint32_t)chunks, (uint32_t)(a.N * a.G));
-  hipLaunchKernelGGL(gn_stats_k<T>, g, dim3(256), 0, ctx.stream, a, chunks, cs);
-  hipLaunchKernelGGL(gn_apply_k<T>, g, dim3(256), 0, ctx.stream, a, chunks, cs);
+  if (vec) {
+    hipLaunchKernelGGL((gn_stats_k<T, V>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
+    hipLaunchKernelGGL((gn_apply_k<T, V>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
+  } else {
+    hipLaunchKernelGGL((gn_stats_k<T, 1>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
+    hipLaunchKernelGGL((gn_apply_k<T, 1>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
+  }
   return hrt::launch_ok(hipGetLastError(), ctx, "gn_fwd");
 }
 
@@ -340,10 +466,15 @@ bool launch_gn_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
     return false;
   if (a.N * a.C >= ((int64_t)1 << 31)) return ctx.fail("N * C must be < 2^31");
   if (a.dx && a.N * a.C > 65535) return ctx.fail("N * C must be <= 65535 for dx");
-  hipLaunchKernelGGL(gn_bwd_sums_k<T>, dim3((uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
+  constexpr int V = vec16<T>();
+  const bool vec = a.HW % V == 0 && a.x % 16 == 0 && a.g % 16 == 0 && a.dx % 16 == 0;
+  if (vec) hipLaunchKernelGGL((gn_bwd_sums_k<T, V>), dim3((uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
+  else hipLaunchKernelGGL((gn_bwd_sums_k<T, 1>), dim3((uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
   if (a.dx) {
     hipLaunchKernelGGL(gn_bwd_coef_k<T>, dim3((uint32_t)cdiv(a.N * a.G, 256)), dim3(256), 0, ctx.stream, a);
-    hipLaunchKernelGGL(gn_bwd_dx_k<T>, dim3((uint32_t)cdiv(a.HW, 256), (uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
+    const dim3 g((uint32_t)cdiv(vec ? a.HW / V : a.HW, 256), (uint32_t)(a.N * a.C));
+    if (vec) hipLaunchKernelGGL((gn_bwd_dx_k<T, V>), g, dim3(256), 0, ctx.stream, a);
+    else hipLaunchKernelGGL((gn_bwd_dx_k<T, 1>), g, dim3(256), 0, ctx.stream, a);
   }
   if (a.dw || a.db) hipLaunchKernelGGL(gn_bwd_wgrad_k<T>, dim3((uint32_t)cdiv(a.C, 256)), dim3(256), 0, ctx.stream, a);
   return hrt::launch_ok(hipGetLastError(), ctx, "gn_bwd");
