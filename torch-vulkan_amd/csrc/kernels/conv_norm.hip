@@ -149,6 +149,168 @@ __global__ __launch_bounds__(256) void col2im_k(hrt_im2col_args a) {
   stf<T>(a.x, (n * a.C + c) * HW + p, s);
 }
 
+// ---- LDS-staged unfolding ------------------------------------------------------------------------------
+// Raw element type: values are moved, never converted.
+template <typename T>
+using raw_t = std::conditional_t<std::is_same<T, F32>::value, uint32_t, uint16_t>;
+template <typename T>
+__device__ __forceinline__ u32x4 pack_raw(const raw_t<T> (&v)[vec16<T>()]) {
+  if constexpr (std::is_same<T, F32>::value) return u32x4{v[0], v[1], v[2], v[3]};
+  else
+    return u32x4{v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16), v[4] | ((uint32_t)v[5] << 16),
+                 v[6] | ((uint32_t)v[7] << 16)};
+}
+template <typename T>
+__device__ __forceinline__ float raw_f32(raw_t<T> v) {
+  if constexpr (std::is_same<T, F32>::value) return __uint_as_float(v);
+  else return T::to_f32(v);
+}
+
+// grid (cdiv(OH, RB), C, N): workgroup (row block, c, n) copies the (rb - 1) SH + KH input rows its rb
+// output rows read into LDS once, zero-padded (PW columns on each side, rows outside the image zero), then
+// writes the KH*KW column rows of channel c for those output rows (a contiguous span of rb*OW elements
+// each) from LDS; VEC (OW a multiple of the 16-byte vector, 16-byte aligned cols): one 16-byte store per
+// lane and vector.  Input rows are read once per row block, output pixels are written once.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void im2col_lds_k(hrt_im2col_args a, int RB) {
+  using E = raw_t<T>;
+  constexpr int V = vec16<T>();
+  extern __shared__ __attribute__((aligned(16))) uint8_t im_lds[];
+  E* const tile = reinterpret_cast<E*>(im_lds);
+  const int OH = (int)a.OH, OW = (int)a.OW, H = (int)a.H, W = (int)a.W, SH = (int)a.SH, SW = (int)a.SW;
+  const int PW = (int)a.PW, KH = (int)a.KH, KW = (int)a.KW, KK = KH * KW;
+  const int oh0 = (int)blockIdx.x * RB, rb = min(RB, OH - oh0);
+  const int c = blockIdx.y;
+  const int64_t n = blockIdx.z;
+  const int TR = (rb - 1) * SH + KH, TW = W + 2 * PW, h0 = oh0 * SH - (int)a.PH;
+  const HK_G E* xs = gcptr<E>(a.x) + (n * a.C + c) * a.H * a.W;
+  for (int i = threadIdx.x; i < TR * TW; i += 256) {
+    const int r = i / TW, col = i - r * TW;
+    const int h = h0 + r, w = col - PW;
+    tile[i] = (h >= 0 && h < H && w >= 0 && w < W) ? xs[(int64_t)h * W + w] : (E)0;
+  }
+  __syncthreads();
+  const int64_t K = a.C * KK;
+  HK_G E* const cols = gptr<E>(a.cols) + ((n * K + (int64_t)c * KK) * OH + oh0) * (int64_t)OW;
+  const int64_t rowlen = (int64_t)OH * OW;  // elements between consecutive k rows
+  if constexpr (VEC) {
+    const int per = rb * OW / V;  // vectors per k row span (OW % V == 0)
+    for (int q = threadIdx.x; q < KK * per; q += 256) {
+      const int kk = q / per, e0 = (q - kk * per) * V;
+      const int kh = kk / KW, kw = kk - kh * KW;
+      const int r = e0 / OW, ow0 = e0 - r * OW;
+      const E* src = tile + (r * SH + kh) * TW + ow0 * SW + kw;
+      E v[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[j] = src[j * SW];
+      *reinterpret_cast<HK_G u32x4*>(cols + kk * rowlen + e0) = pack_raw<T>(v);
+    }
+  } else {
+    const int span = rb * OW;
+    for (int q = threadIdx.x; q < KK * span; q += 256) {
+      const int kk = q / span, e = q - kk * span;
+      const int kh = kk / KW, kw = kk - kh * KW;
+      const int r = e / OW, ow = e - r * OW;
+      cols[kk * rowlen + e] = tile[(r * SH + kh) * TW + ow * SW + kw];
+    }
+  }
+}
+
+// grid (cdiv(H, RB), C, N): the adjoint.  For each (kh, kw) the output rows that feed input rows
+// [h0, h0 + rb) form a contiguous span of column row (c, kh, kw) (at most RO = (rb - 1) / SH + 1 rows); the
+// workgroup copies all KH*KW spans into LDS (16-byte loads when VEC), then each lane sums, for its input
+// pixels, the entries it fed in the order kh, then kw (the order of col2im_k, so the two agree bit for
+// bit).  S1: unit strides (no divisibility tests).
+template <typename T, bool VEC, bool S1>
+__global__ __launch_bounds__(256) void col2im_lds_k(hrt_im2col_args a, int RB) {
+  using E = raw_t<T>;
+  constexpr int V = vec16<T>();
+  extern __shared__ __attribute__((aligned(16))) uint8_t im_lds[];
+  E* const tile = reinterpret_cast<E*>(im_lds);
+  const int OH = (int)a.OH, OW = (int)a.OW, H = (int)a.H, W = (int)a.W, SH = (int)a.SH, SW = (int)a.SW;
+  const int PH = (int)a.PH, PW = (int)a.PW, KH = (int)a.KH, KW = (int)a.KW, KK = KH * KW;
+  const int h0 = (int)blockIdx.x * RB, rb = min(RB, H - h0);
+  const int RO = (RB - 1) / SH + 1;  // LDS rows per (kh, kw)
+  const int c = blockIdx.y;
+  const int64_t n = blockIdx.z;
+  const int64_t K = a.C * KK, rowlen = (int64_t)OH * OW;
+  const HK_G E* cs = gcptr<E>(a.cols) + (n * K + (int64_t)c * KK) * rowlen;
+  // first output row and row count of kernel row kh for this block
+  auto ohlo = [&](int kh) {
+    const int t = h0 + PH - kh;
+    return t <= 0 ? 0 : (t + SH - 1) / SH;
+  };
+  auto ohcnt = [&](int kh) {
+    const int t = h0 + rb - 1 + PH - kh;
+    if (t < 0) return 0;
+    const int hi = min(t / SH, OH - 1), lo = ohlo(kh);
+    return hi >= lo ? hi - lo + 1 : 0;
+  };
+  if constexpr (VEC) {
+    const int per = RO * OW / V;
+    for (int q = threadIdx.x; q < KK * per; q += 256) {
+      const int kk = q / per, e0 = (q - kk * per) * V;
+      const int kh = kk / KW;
+      if (e0 < ohcnt(kh) * OW)
+        *reinterpret_cast<u32x4*>(tile + kk * RO * OW + e0) =
+            *reinterpret_cast<const HK_G u32x4*>(cs + kk * rowlen + (int64_t)ohlo(kh) * OW + e0);
+    }
+  } else {
+    const int per = RO * OW;
+    for (int q = threadIdx.x; q < KK * per; q += 256) {
+      const int kk = q / per, e = q - kk * per;
+      const int kh = kk / KW;
+      if (e < ohcnt(kh) * OW) tile[q] = cs[kk * rowlen + (int64_t)ohlo(kh) * OW + e];
+    }
+  }
+  __syncthreads();
+  constexpr int NV = VEC ? V : 1;
+  const int per = rb * W / NV;  // VEC: W % V == 0
+  for (int q = threadIdx.x; q < per; q += 256) {
+    const int e0 = q * NV, r = e0 / W, w0 = e0 - r * W, h = h0 + r;
+    float s[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) s[j] = 0.0f;
+    for (int kh = 0; kh < KH; ++kh) {
+      const int th = h + PH - kh;
+      if (th < 0 || (!S1 && th % SH)) continue;
+      const int oh = S1 ? th : th / SH;
+      if (oh >= OH) continue;
+      const E* trow = tile + (kh * KW * RO + (oh - ohlo(kh))) * OW;
+      for (int kw = 0; kw < KW; ++kw) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          const int tw = w0 + j + PW - kw;
+          if (tw < 0 || (!S1 && tw % SW)) continue;
+          const int ow = S1 ? tw : tw / SW;
+          if (ow < OW) s[j] += raw_f32<T>(trow[kw * RO * OW + ow]);
+        }
+      }
+    }
+    if constexpr (VEC) stv<T>(a.x, ((n * a.C + c) * a.H + h0) * a.W + e0, s);
+    else stf<T>(a.x, ((n * a.C + c) * a.H + h0) * a.W + e0, s[0]);
+  }
+}
+
+// Row blocks of the LDS-staged kernels: about 1024 output (im2col) or input (col2im) pixels per
+// workgroup (faster than 512 or 2048 on a 64x64 image), halved until the staged rows take at most
+// 32 KiB; 0 when one row block does not fit 64 KiB (then the per-element kernels run).
+int64_t im2col_rows(const hrt_im2col_args& a, uint64_t es, int64_t* lds) {
+  const int64_t TW = a.W + 2 * a.PW;
+  auto need = [&](int64_t rb) { return ((rb - 1) * a.SH + a.KH) * TW * (int64_t)es; };
+  int64_t rb = std::max<int64_t>(1, std::min<int64_t>(a.OH, 1024 / std::max<int64_t>(a.OW, 1)));
+  while (rb > 1 && need(rb) > 32768) rb = (rb + 1) / 2;
+  *lds = (need(rb) + 15) / 16 * 16;
+  return *lds <= 65536 ? rb : 0;
+}
+int64_t col2im_rows(const hrt_im2col_args& a, uint64_t es, int64_t* lds) {
+  auto need = [&](int64_t rb) { return a.KH * a.KW * ((rb - 1) / a.SH + 1) * a.OW * (int64_t)es; };
+  int64_t rb = std::max<int64_t>(1, std::min<int64_t>(a.H, 1024 / std::max<int64_t>(a.W, 1)));
+  while (rb > 1 && need(rb) > 32768) rb = (rb + 1) / 2;
+  *lds = (need(rb) + 15) / 16 * 16;
+  return *lds <= 65536 ? rb : 0;
+}
+
 bool im2col_check(const hrt_im2col_args& a, hrt::LaunchCtx& ctx, uint64_t es) {
   if (a.N <= 0 || a.C <= 0 || a.H <= 0 || a.W <= 0 || a.KH <= 0 || a.KW <= 0 || a.SH <= 0 || a.SW <= 0 || a.PH < 0 ||
       a.PW < 0)
@@ -166,7 +328,15 @@ bool launch_im2col(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_im2col_args*>(p);
   if (!im2col_check(a, ctx, esz<T>())) return false;
   constexpr int V = vec16<T>();
-  if (a.OW % V == 0 && a.cols % 16 == 0) {
+  int64_t lds = 0;
+  const int64_t rb = im2col_rows(a, esz<T>(), &lds);
+  if (rb > 0) {
+    const dim3 g((uint32_t)cdiv(a.OH, rb), (uint32_t)a.C, (uint32_t)a.N);
+    if (a.OW % V == 0 && a.cols % 16 == 0)
+      hipLaunchKernelGGL((im2col_lds_k<T, true>), g, dim3(256), (uint32_t)lds, ctx.stream, a, (int)rb);
+    else
+      hipLaunchKernelGGL((im2col_lds_k<T, false>), g, dim3(256), (uint32_t)lds, ctx.stream, a, (int)rb);
+  } else if (a.OW % V == 0 && a.cols % 16 == 0) {
     const dim3 g((uint32_t)cdiv(a.OH * a.OW / V, 256), (uint32_t)(a.C * a.KH * a.KW), (uint32_t)a.N);
     hipLaunchKernelGGL(im2col_vec_k<T>, g, dim3(256), 0, ctx.stream, a);
   } else {
@@ -179,8 +349,22 @@ template <typename T>
 bool launch_col2im(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_im2col_args*>(p);
   if (!im2col_check(a, ctx, esz<T>())) return false;
-  const dim3 g((uint32_t)cdiv(a.H * a.W, 256), (uint32_t)a.C, (uint32_t)a.N);
-  hipLaunchKernelGGL(col2im_k<T>, g, dim3(256), 0, ctx.stream, a);
+  constexpr int V = vec16<T>();
+  int64_t lds = 0;
+  const int64_t rb = col2im_rows(a, esz<T>(), &lds);
+  if (rb > 0) {
+    const dim3 g((uint32_t)cdiv(a.H, rb), (uint32_t)a.C, (uint32_t)a.N);
+    const bool vec = a.OW % V == 0 && a.W % V == 0 && a.cols % 16 == 0 && a.x % 16 == 0;
+    const bool s1 = a.SH == 1 && a.SW == 1;
+    const uint32_t sh = (uint32_t)lds;
+    if (vec && s1) hipLaunchKernelGGL((col2im_lds_k<T, true, true>), g, dim3(256), sh, ctx.stream, a, (int)rb);
+    else if (vec) hipLaunchKernelGGL((col2im_lds_k<T, true, false>), g, dim3(256), sh, ctx.stream, a, (int)rb);
+    else if (s1) hipLaunchKernelGGL((col2im_lds_k<T, false, true>), g, dim3(256), sh, ctx.stream, a, (int)rb);
+    else hipLaunchKernelGGL((col2im_lds_k<T, false, false>), g, dim3(256), sh, ctx.stream, a, (int)rb);
+  } else {
+    const dim3 g((uint32_t)cdiv(a.H * a.W, 256), (uint32_t)a.C, (uint32_t)a.N);
+    hipLaunchKernelGGL(col2im_k<T>, g, dim3(256), 0, ctx.stream, a);
+  }
   return hrt::launch_ok(hipGetLastError(), ctx, "col2im");
 }
 HRT_REGISTER("im2col_f32", hrt_im2col_args, launch_im2col<F32>);
