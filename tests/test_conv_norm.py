@@ -134,7 +134,8 @@ def test_conv_rectangular_kernel_stride_padding_and_views():
 
 # ---- nearest upsampling (reference tests/test_conv.py:117-135) -----------------------------------------------
 @pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("shape,scale", [((1, 4, 8, 8), 2), ((2, 3, 5, 7), (2, 3)), ((1, 2, 4, 6), 1)])
+@pytest.mark.parametrize("shape,scale", [((1, 4, 8, 8), 2), ((2, 3, 5, 7), (2, 3)), ((1, 2, 4, 6), 1),
+                                         ((1, 2, 4, 8), (3, 2)), ((1, 3, 3, 8), 3), ((2, 8, 16, 32), 2)])
 def test_nearest_upsample_forward_backward(dt, shape, scale):
     x = rnd(shape, dt, 1)
     sh, sw = (scale, scale) if isinstance(scale, int) else scale

@@ -384,21 +384,6 @@ __global__ __launch_bounds__(256) void up_fwd_k(hrt_upsample_args a, int64_t tot
   stf<T>(a.dst, i, ldf<T>(a.src, (nc * a.H + oh / fh) * a.W + ow / fw));
 }
 
-// vec16 consecutive output pixels of one output row per lane (OW a multiple of it): one 16-byte store.
-template <typename T>
-__global__ __launch_bounds__(256) void up_fwd_vec_k(hrt_upsample_args a, int64_t total) {
-  constexpr int V = vec16<T>();
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
-  if (i >= total) return;
-  const int64_t ow0 = i % a.OW, t = i / a.OW, oh = t % a.OH, nc = t / a.OH;
-  const int64_t fh = a.OH / a.H, fw = a.OW / a.W;
-  const int64_t srow = (nc * a.H + oh / fh) * a.W;
-  float v[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) v[j] = ldf<T>(a.src, srow + (ow0 + j) / fw);
-  stv<T>(a.dst, i, v);
-}
-
 // dst [NC, H, W] = block sums of src [NC, OH, OW] (rows of the block in order, then columns).
 template <typename T>
 __global__ __launch_bounds__(256) void up_bwd_k(hrt_upsample_args a, int64_t total) {
@@ -412,6 +397,64 @@ __global__ __launch_bounds__(256) void up_bwd_k(hrt_upsample_args a, int64_t tot
   stf<T>(a.dst, i, s);
 }
 
+// One lane per 16-byte output vector of an input row: the vector's source elements are loaded once (one
+// 8-byte load when F2, i.e. fw == 2: each source element fills two output slots) and the vector is stored
+// to the fh output rows that repeat the input row.  total = NC * H * OW / V vectors; OW % V == 0.
+template <typename T, bool F2>
+__global__ __launch_bounds__(256) void up_fwd_rows_k(hrt_upsample_args a, int64_t total) {
+  constexpr int V = vec16<T>();
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t per = a.OW / V, srow = i / per, ow0 = (i - srow * per) * V;  // srow = nc * H + ih
+  const int64_t fh = a.OH / a.H, nc = srow / a.H, ih = srow - nc * a.H;
+  u32x4 out;
+  if constexpr (F2) {
+    const u32x2 u = *reinterpret_cast<const HK_G u32x2*>(gcptr<raw_t<T>>(a.src) + srow * a.W + ow0 / 2);
+    if constexpr (std::is_same<T, F32>::value) {
+      out = u32x4{u.x, u.x, u.y, u.y};
+    } else {
+      auto dup = [](uint32_t e) { return (e & 0xffffu) | (e << 16); };
+      out = u32x4{dup(u.x & 0xffffu), dup(u.x >> 16), dup(u.y & 0xffffu), dup(u.y >> 16)};
+    }
+  } else {
+    const int64_t fw = a.OW / a.W;
+    raw_t<T> v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = gcptr<raw_t<T>>(a.src)[srow * a.W + (ow0 + j) / fw];
+    out = pack_raw<T>(v);
+  }
+  HK_G raw_t<T>* dst = gptr<raw_t<T>>(a.dst) + (nc * a.OH + ih * fh) * a.OW + ow0;
+  for (int64_t y = 0; y < fh; ++y) *reinterpret_cast<HK_G u32x4*>(dst + y * a.OW) = out;
+}
+
+// Backward for fw == 2 and W % V == 0: a lane sums V input pixels; each of the fh source rows gives two
+// 16-byte loads (2V columns).  Same order as up_bwd_k: rows, then the two columns of each.
+template <typename T>
+__global__ __launch_bounds__(256) void up_bwd_vec2_k(hrt_upsample_args a, int64_t total) {
+  constexpr int V = vec16<T>();
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+  if (i >= total) return;
+  const int64_t row = i / a.W, w0 = i - row * a.W, nc = row / a.H, h = row - nc * a.H;
+  const int64_t fh = a.OH / a.H;
+  float s[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) s[j] = 0.0f;
+  for (int64_t y = 0; y < fh; ++y) {
+    const int64_t sb = (nc * a.OH + h * fh + y) * a.OW + 2 * w0;
+    float u0[V], u1[V];
+    ldv<T>(a.src, sb, u0);
+    ldv<T>(a.src, sb + V, u1);
+#pragma unroll
+    for (int j = 0; j < V / 2; ++j) {
+      s[j] += u0[2 * j];
+      s[j] += u0[2 * j + 1];
+      s[V / 2 + j] += u1[2 * j];
+      s[V / 2 + j] += u1[2 * j + 1];
+    }
+  }
+  stv<T>(a.dst, i, s);
+}
+
 template <typename T, bool FWD>
 bool launch_up(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_upsample_args*>(p);
@@ -421,8 +464,14 @@ bool launch_up(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!ctx.check(a.src, FWD ? small : big, "src") || !ctx.check(a.dst, FWD ? big : small, "dst")) return false;
   const int64_t total = FWD ? a.NC * a.OH * a.OW : a.NC * a.H * a.W;
   constexpr int V = vec16<T>();
-  if (FWD && a.OW % V == 0 && a.dst % 16 == 0)
-    hipLaunchKernelGGL(up_fwd_vec_k<T>, dim3((uint32_t)cdiv(total / V, 256)), dim3(256), 0, ctx.stream, a, total);
+  const int64_t fw = a.OW / a.W;
+  if (FWD && a.OW % V == 0 && a.dst % 16 == 0) {
+    const int64_t vecs = a.NC * a.H * (a.OW / V);
+    const dim3 g((uint32_t)cdiv(vecs, 256));
+    if (fw == 2 && a.src % 8 == 0) hipLaunchKernelGGL((up_fwd_rows_k<T, true>), g, dim3(256), 0, ctx.stream, a, vecs);
+    else hipLaunchKernelGGL((up_fwd_rows_k<T, false>), g, dim3(256), 0, ctx.stream, a, vecs);
+  } else if (!FWD && fw == 2 && a.W % V == 0 && a.src % 16 == 0 && a.dst % 16 == 0)
+    hipLaunchKernelGGL(up_bwd_vec2_k<T>, dim3((uint32_t)cdiv(total / V, 256)), dim3(256), 0, ctx.stream, a, total);
   else if (FWD)
     hipLaunchKernelGGL(up_fwd_k<T>, dim3((uint32_t)cdiv(total, 256)), dim3(256), 0, ctx.stream, a, total);
   else
@@ -459,6 +508,39 @@ __device__ __forceinline__ Wf wf_block(Wf v, Wf* lds) {
   return wf_merge(wf_merge(lds[0], lds[1]), wf_merge(lds[2], lds[3]));
 }
 
+// Visits e = first, first + step, ... < end in order, calling f(e, v) with v the V elements of p at base
+// + e; the loads of four consecutive visits are issued before the first of them is used (one 16-byte load
+// in flight per lane leaves HBM latency-bound at these grid sizes).
+template <typename T, int V, class F>
+__device__ __forceinline__ void visit4(uint64_t p, int64_t base, int64_t first, int64_t end, int64_t step, F&& f) {
+  for (int64_t e0 = first; e0 < end; e0 += 4 * step) {
+    float v[4][V];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (e0 + u * step < end) ldn<T, V>(p, base + e0 + u * step, v[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (e0 + u * step < end) f(e0 + u * step, v[u]);
+  }
+}
+// The same over two tensors read at the same positions.
+template <typename T, int V, class F>
+__device__ __forceinline__ void visit4x2(uint64_t p, uint64_t r, int64_t base, int64_t first, int64_t end, int64_t step,
+                                         F&& f) {
+  for (int64_t e0 = first; e0 < end; e0 += 4 * step) {
+    float v[4][V], w[4][V];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (e0 + u * step < end) {
+        ldn<T, V>(p, base + e0 + u * step, v[u]);
+        ldn<T, V>(r, base + e0 + u * step, w[u]);
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (e0 + u * step < end) f(v[u], w[u]);
+  }
+}
+
 // grid (chunks, N*G): statistics of chunk q of group ng (its elements are contiguous: x is [N, C, HW]),
 // each lane summing deviations from the chunk's first element.  V elements per access (V divides HW and
 // the chunk size).
@@ -471,9 +553,7 @@ __global__ __launch_bounds__(256) void gn_stats_k(hrt_gn_args a, int64_t chunks,
   const int64_t base = ng * M;
   const float k = lo < hi ? ldf<T>(a.x, base + lo) : 0.0f;  // an empty last chunk reads nothing
   float s = 0.0f, s2 = 0.0f, cnt = 0.0f;
-  for (int64_t e = lo + (int64_t)threadIdx.x * V; e < hi; e += 256 * V) {
-    float v[V];
-    ldn<T, V>(a.x, base + e, v);
+  visit4<T, V>(a.x, base, lo + (int64_t)threadIdx.x * V, hi, 256 * V, [&](int64_t, const float (&v)[V]) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const float d = v[j] - k;
@@ -481,7 +561,7 @@ __global__ __launch_bounds__(256) void gn_stats_k(hrt_gn_args a, int64_t chunks,
       s2 += d * d;
     }
     cnt += (float)V;
-  }
+  });
   Wf w = cnt > 0.0f ? Wf{cnt, k + s / cnt, s2 - s * s / cnt} : Wf{0.0f, 0.0f, 0.0f};
   w = wf_block(w, lds);
   if (threadIdx.x == 0) {
@@ -492,37 +572,66 @@ __global__ __launch_bounds__(256) void gn_stats_k(hrt_gn_args a, int64_t chunks,
   }
 }
 
-// grid (chunks, N*G): merge the group's chunk statistics (in chunk order), write mean / rstd (chunk 0),
-// normalise chunk q (V consecutive elements share a channel since V divides HW).
+// grid (cdiv(M, cs), N*G): merge the group's `chunks` statistics partials, write mean / rstd (block 0),
+// normalise elements [q cs, (q + 1) cs) of the group (V consecutive elements share a channel since V
+// divides HW).  cs is the apply block (4096), finer than the statistics chunks, so that more workgroups
+// are resident to stream the tensor.
 template <typename T, int V>
 __global__ __launch_bounds__(256) void gn_apply_k(hrt_gn_args a, int64_t chunks, int64_t cs) {
   __shared__ float st[2];
   const int64_t Cg = a.C / a.G, M = Cg * a.HW;
   const int64_t ng = blockIdx.y, q = blockIdx.x;
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 64) {
+    // the group's chunk statistics, merged by wave 0 in a fixed order: lane l takes chunks l, l + 64, ..,
+    // then a butterfly in which both partners merge (lower lane, upper lane), so every lane, and every
+    // workgroup of the group, ends with the same bits
     const HK_G float* ws = gcptr<float>(a.ws) + ng * chunks * 3;
-    Wf v{ws[0], ws[1], ws[2]};
-    for (int64_t i = 1; i < chunks; ++i) v = wf_merge(v, Wf{ws[3 * i], ws[3 * i + 1], ws[3 * i + 2]});
-    const float var = v.m2 / v.n;
-    st[0] = v.mean;
-    st[1] = 1.0f / sqrtf(var + a.eps);
-    if (q == 0) {
-      stf<T>(a.mean, ng, st[0]);
-      stf<T>(a.rstd, ng, st[1]);
+    Wf v{0.0f, 0.0f, 0.0f};
+    for (int64_t i = threadIdx.x; i < chunks; i += 64) v = wf_merge(v, Wf{ws[3 * i], ws[3 * i + 1], ws[3 * i + 2]});
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const Wf o = wf_shfl(v, m);
+      v = (threadIdx.x & m) ? wf_merge(o, v) : wf_merge(v, o);
+    }
+    if (threadIdx.x == 0) {
+      const float var = v.m2 / v.n;
+      st[0] = v.mean;
+      st[1] = 1.0f / sqrtf(var + a.eps);
+      if (q == 0) {
+        stf<T>(a.mean, ng, st[0]);
+        stf<T>(a.rstd, ng, st[1]);
+      }
     }
   }
   __syncthreads();
   const float mean = st[0], rstd = st[1];
   const int64_t g = ng % a.G;
   const int64_t lo = q * cs, hi = min(M, lo + cs), base = ng * M;
-  for (int64_t e = lo + (int64_t)threadIdx.x * V; e < hi; e += 256 * V) {
-    const int64_t c = g * Cg + e / a.HW;
-    const float wc = a.w ? ldf<T>(a.w, c) : 1.0f, bc = a.b ? ldf<T>(a.b, c) : 0.0f;
-    float v[V];
-    ldn<T, V>(a.x, base + e, v);
+  // four vectors per round, with their x, w and b loads all issued before the first store (y may alias w
+  // and b as far as the compiler knows, so loads after a store would wait for it)
+  constexpr int64_t step = 256 * V;
+  for (int64_t e0 = lo + (int64_t)threadIdx.x * V; e0 < hi; e0 += 4 * step) {
+    float x[4][V], wc[4], bc[4];
 #pragma unroll
-    for (int j = 0; j < V; ++j) v[j] = (v[j] - mean) * rstd * wc + bc;
-    stn<T, V>(a.y, base + e, v);
+    for (int u = 0; u < 4; ++u) {
+      const int64_t e = e0 + u * step;
+      if (e < hi) {
+        ldn<T, V>(a.x, base + e, x[u]);
+        const int64_t c = g * Cg + e / a.HW;
+        wc[u] = a.w ? ldf<T>(a.w, c) : 1.0f;
+        bc[u] = a.b ? ldf<T>(a.b, c) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t e = e0 + u * step;
+      if (e < hi) {
+        float v[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) v[j] = (x[u][j] - mean) * rstd * wc[u] + bc[u];
+        stn<T, V>(a.y, base + e, v);
+      }
+    }
   }
 }
 
@@ -532,16 +641,13 @@ __global__ __launch_bounds__(256) void gn_bwd_sums_k(hrt_gn_args a) {
   __shared__ float red[4];
   const int64_t nc = blockIdx.x, base = nc * a.HW;
   float ds = 0.0f, db = 0.0f;
-  for (int64_t e = (int64_t)threadIdx.x * V; e < a.HW; e += 256 * V) {
-    float g[V], x[V];
-    ldn<T, V>(a.g, base + e, g);
-    ldn<T, V>(a.x, base + e, x);
+  visit4x2<T, V>(a.g, a.x, base, (int64_t)threadIdx.x * V, a.HW, 256 * V, [&](const float (&g)[V], const float (&x)[V]) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       ds += g[j] * x[j];
       db += g[j];
     }
-  }
+  });
   ds = block_sum<4>(ds, red);
   __syncthreads();
   db = block_sum<4>(db, red);
@@ -630,12 +736,14 @@ bool launch_gn_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int64_t chunks = hrt_gn_chunks(a.C, a.HW, a.G), M = (a.C / a.G) * a.HW;
   const int64_t cs = vec ? cdiv(cdiv(M, chunks), V) * V : cdiv(M, chunks);  // chunks start on a vector
   const dim3 g((uint32_t)chunks, (uint32_t)(a.N * a.G));
+  constexpr int64_t AS = 4096;  // apply block, a multiple of every V
+  const dim3 ga((uint32_t)cdiv(M, AS), (uint32_t)(a.N * a.G));
   if (vec) {
     hipLaunchKernelGGL((gn_stats_k<T, V>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
-    hipLaunchKernelGGL((gn_apply_k<T, V>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
+    hipLaunchKernelGGL((gn_apply_k<T, V>), ga, dim3(256), 0, ctx.stream, a, chunks, AS);
   } else {
     hipLaunchKernelGGL((gn_stats_k<T, 1>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
-    hipLaunchKernelGGL((gn_apply_k<T, 1>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
+    hipLaunchKernelGGL((gn_apply_k<T, 1>), ga, dim3(256), 0, ctx.stream, a, chunks, AS);
   }
   return hrt::launch_ok(hipGetLastError(), ctx, "gn_fwd");
 }
