@@ -552,12 +552,14 @@ __global__ __launch_bounds__(256) void ln_bwd_row(const typename T::storage* __r
 }
 
 // dw[d] = sum_c ws[c][0][d], db[d] = sum_c ws[c][1][d]: workgroup (column block of 64, quantity) with
-// 4 chunk groups of 64 threads; each thread keeps 8 loads in flight (independent partial sums), and the
-// groups are combined in a fixed order, so the result does not depend on timing.
+// 16 chunk groups of 64 threads (chunk group k takes chunks k, k + 16, ..); each thread keeps 8 loads in
+// flight (independent partial sums), and the groups are combined in a fixed tree order, so the result
+// does not depend on timing.  16 groups leave two rounds of loads per thread at 256 chunks.
 template <typename T>
-__global__ __launch_bounds__(256) void ln_wgrad_reduce(const float* __restrict__ ws, typename T::storage* __restrict__ dw,
-                                                       typename T::storage* __restrict__ db, int64_t chunks, int64_t D) {
-  __shared__ float sp[4][64];
+__global__ __launch_bounds__(1024) void ln_wgrad_reduce(const float* __restrict__ ws, typename T::storage* __restrict__ dw,
+                                                        typename T::storage* __restrict__ db, int64_t chunks, int64_t D) {
+  constexpr int NG = 16;
+  __shared__ float sp[NG][64];
   const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int qn = blockIdx.y;  // 0: dw, 1: db
   typename T::storage* dst = qn ? db : dw;
@@ -567,15 +569,21 @@ __global__ __launch_bounds__(256) void ln_wgrad_reduce(const float* __restrict__
   if (col < D) {
     const float* src = ws + qn * D + col;
     int64_t c = grp;
-    for (; c + 28 < chunks; c += 32) {
+    for (; c + 7 * NG < chunks; c += 8 * NG) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] += src[(c + 4 * u) * 2 * D];
+      for (int u = 0; u < 8; ++u) acc[u] += src[(c + NG * u) * 2 * D];
     }
-    for (int u = 0; c < chunks; c += 4, ++u) acc[u & 7] += src[c * 2 * D];
+    for (int u = 0; c < chunks; c += NG, ++u) acc[u & 7] += src[c * 2 * D];
   }
   sp[grp][cl] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (grp == 0 && col < D) dst[col] = T::from_f32((sp[0][cl] + sp[1][cl]) + (sp[2][cl] + sp[3][cl]));
+  if (grp == 0 && col < D) {
+    float t[NG / 2];
+#pragma unroll
+    for (int k = 0; k < NG / 2; ++k) t[k] = sp[2 * k][cl] + sp[2 * k + 1][cl];
+    const float s = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    dst[col] = T::from_f32(s);
+  }
 }
 
 template <typename T>
@@ -648,7 +656,7 @@ bool launch_ln_wgrad(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws") || (a.dw && !ctx.check(a.dw, a.D * sizeof(S), "dw")) ||
       (a.db && !ctx.check(a.db, a.D * sizeof(S), "db")))
     return false;
-  hipLaunchKernelGGL(ln_wgrad_reduce<T>, dim3((uint32_t)cdiv(a.D, 64), 2), dim3(256), 0, ctx.stream, (const float*)a.ws,
+  hipLaunchKernelGGL(ln_wgrad_reduce<T>, dim3((uint32_t)cdiv(a.D, 64), 2), dim3(1024), 0, ctx.stream, (const float*)a.ws,
                      (S*)a.dw, (S*)a.db, chunks, a.D);
   return hrt::launch_ok(hipGetLastError(), ctx, "ln_wgrad");
 }
