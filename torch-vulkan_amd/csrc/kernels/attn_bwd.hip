@@ -776,11 +776,18 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   // branch-free (stage_origin, as in the other attention kernels).
   constexpr int IPW = QST * NCH / 64 / NW;
   static_assert(IPW <= 2 * DCH, "a half's copies fit between its S / dP products");
-  // S = Q_t K^T and dP = dO_t V^T of one 64-query half (tile rows at Qt / Ot), with copy parts of the next
-  // stage placed after the first IPW MFMA pairs when COPY
-  auto sdp = [&](auto cc, const HK_L uint8_t* Qt, const HK_L uint8_t* Ot, f32x4* s, f32x4* dp,
-                 const HK_G uint8_t* src, uint32_t ss, HK_L uint8_t* dst, const DmaLanes& lo) {
+  auto half_stage = [&](auto bc, auto hc, auto cc, int st) {
+    constexpr int BUF = decltype(bc)::value;
+    constexpr int HALF = decltype(hc)::value;
     constexpr bool COPY = decltype(cc)::value;
+    const HK_G uint8_t* src = HALF ? Ob + stage_origin<QST>(st + 1, nst, Sq) * oss
+                                   : Qb + stage_origin<QST>(st + 1, nst, Sq) * qss;
+    const bool more = HALF == 0 || st + 1 < nst;
+    f32x4 nn[2], dn[2];
+    if (more) fetch(HALF ? st + 1 : st, HALF ^ 1, nn, dn);
+    const HK_L uint8_t* Qt = (BUF ? Q1 : Q0) + HALF * QHALF * ROWB;
+    const HK_L uint8_t* Ot = (BUF ? O1 : O0) + HALF * QHALF * ROWB;
+    f32x4 s[2], dp[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       s[t] = dp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -790,27 +797,22 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
         dp[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Ot + roff[ks] + t * 16 * ROWB), vf[ks], dp[t]);
         if constexpr (COPY) {
           const int c = t * DCH + ks;
-          if (c < IPW) dma_tile_part<NCH, QST, NW>(src, ss, dst, wave, lo, c);
+          if (c < IPW) dma_tile_part<NCH, QST, NW>(src, HALF ? oss : qss, HALF ? (BUF ? O0 : O1) : (BUF ? Q0 : Q1),
+                                                   wave, HALF ? olo : qlo, c);
         }
       }
     }
-  };
-  // P = exp2(S sl2 - lse log2e), dS = P (dP - delta), rounded to the input dtype and packed as A operands
-  auto pds = [&](const f32x4* s, const f32x4* dp, const f32x4* lo, const f32x4* dlo, u32x4& pa, u32x4& da) {
     float pv[8], ds[8];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pe = __builtin_amdgcn_exp2f(fmaf(s[t][i], sl2, -lo[t][i] * kLog2e));
+        const float pe = __builtin_amdgcn_exp2f(fmaf(s[t][i], sl2, -nl[t][i] * kLog2e));
         pv[t * 4 + i] = pe;
-        ds[t * 4 + i] = pe * (dp[t][i] - dlo[t][i]);
+        ds[t * 4 + i] = pe * (dp[t][i] - dl[t][i]);
       }
-    pa = u32x4{cvt2<T>(pv[0], pv[1]), cvt2<T>(pv[2], pv[3]), cvt2<T>(pv[4], pv[5]), cvt2<T>(pv[6], pv[7])};
-    da = u32x4{cvt2<T>(ds[0], ds[1]), cvt2<T>(ds[2], ds[3]), cvt2<T>(ds[4], ds[5]), cvt2<T>(ds[6], ds[7])};
-  };
-  // dV += P^T dO, dK += dS^T Q of one half
-  auto dvdk = [&](const HK_L uint8_t* Qt, const HK_L uint8_t* Ot, const u32x4& pa, const u32x4& da) {
+    const u32x4 pa = u32x4{cvt2<T>(pv[0], pv[1]), cvt2<T>(pv[2], pv[3]), cvt2<T>(pv[4], pv[5]), cvt2<T>(pv[6], pv[7])};
+    const u32x4 da = u32x4{cvt2<T>(ds[0], ds[1]), cvt2<T>(ds[2], ds[3]), cvt2<T>(ds[4], ds[5]), cvt2<T>(ds[6], ds[7])};
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const u32x2 a0 = lds_tr4(Ot + coff[dt]), a1 = lds_tr4(Ot + coff[dt] + 16 * ROWB);
@@ -818,59 +820,25 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
       const u32x2 b0 = lds_tr4(Qt + coff[dt]), b1 = lds_tr4(Qt + coff[dt] + 16 * ROWB);
       dk[dt] = Mfma<T>::mac(da, u32x4{b0.x, b0.y, b1.x, b1.y}, dk[dt]);
     }
-  };
-  // One 128-query stage, software-pipelined over its two halves: S/dP(half 0); S/dP(half 1) on the matrix
-  // cores while the vector units turn half 0 into P/dS; dV/dK(half 0) while half 1 is turned; dV/dK(half 1).
-  // The MFMA and VALU streams of the middle two phases are interleaved by sched_group_barrier.  lse/delta
-  // of half 1 and of the next stage's half 0 are loaded at the start of the stage (nl / dl hold half 0's).
-  auto stage = [&](auto bc, auto cc, int st) {
-    constexpr int BUF = decltype(bc)::value;
-    constexpr bool COPY = decltype(cc)::value;
-    f32x4 l1[2], d1[2], ln[2], dn[2];
-    fetch(st, 1, l1, d1);
-    if (st + 1 < nst) fetch(st + 1, 0, ln, dn);
-    const HK_L uint8_t* Qs = BUF ? Q1 : Q0;
-    const HK_L uint8_t* Os = BUF ? O1 : O0;
-    const int64_t nxt = COPY ? stage_origin<QST>(st + 1, nst, Sq) : 0;
-    f32x4 s0[2], p0[2], s1[2], p1[2];
-    u32x4 pa0, da0, pa1, da1;
-    sdp(cc, Qs, Os, s0, p0, Qb + nxt * qss, qss, BUF ? Q0 : Q1, qlo);
-    __builtin_amdgcn_sched_barrier(0);
-    sdp(cc, Qs + QHALF * ROWB, Os + QHALF * ROWB, s1, p1, Ob + nxt * oss, oss, BUF ? O0 : O1, olo);
-    pds(s0, p0, nl, dl, pa0, da0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int i = 0; i < 4 * DCH; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i < 3 * DCH) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (COPY && i < IPW) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    if (more) {
+      nl[0] = nn[0], nl[1] = nn[1], dl[0] = dn[0], dl[1] = dn[1];
     }
-    __builtin_amdgcn_sched_barrier(0);
-    dvdk(Qs, Os, pa0, da0);
-    pds(s1, p1, l1, d1, pa1, da1);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int i = 0; i < NDT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      if (i < NDT - 2) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 48 / NDT, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    dvdk(Qs + QHALF * ROWB, Os + QHALF * ROWB, pa1, da1);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) nl[t] = ln[t], dl[t] = dn[t];
-    if constexpr (COPY) __syncthreads();
+    if constexpr (HALF == 1 && COPY) __syncthreads();
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   if (nst == 1) {
-    stage(I0(), std::false_type(), 0);  // rows of half 1 past Sq get lse = +inf: P = dS = 0
+    half_stage(I0(), I0(), std::false_type(), 0);
+    if (Sq > QHALF) half_stage(I0(), I1(), std::false_type(), 0);
     __syncthreads();
   } else {
     for (int st = 0; st < nst; st += 2) {
-      stage(I0(), std::true_type(), st);
-      if (st + 1 < nst) stage(I1(), std::true_type(), st + 1);
+      half_stage(I0(), I0(), std::true_type(), st);
+      half_stage(I0(), I1(), std::true_type(), st);
+      if (st + 1 < nst) {
+        half_stage(I1(), I0(), std::true_type(), st + 1);
+        half_stage(I1(), I1(), std::true_type(), st + 1);
+      }
     }
   }
 
