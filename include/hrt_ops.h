@@ -53,6 +53,22 @@ typedef struct hrt_copy_args {
   int64_t src_strides[HRT_MAX_DIMS];
 } hrt_copy_args;
 
+/* "cat_rows16" — torch.cat of up to HRT_CAT_MAX_PARTS same-dtype contiguous parts in one launch (the
+ * reference copies each part with its own kernel: csrc/ops_rows.cpp:272-332).  Tensors are viewed as rows
+ * of bytes: part p as [outer, row_bytes[p]], out as [outer, out_row_bytes]; part p fills byte columns
+ * [col[p], col[p] + row_bytes[p]) of every out row, the parts in column order and adjacent (col[p + 1] =
+ * col[p] + row_bytes[p]).  Pointers, row_bytes, col and out_row_bytes are multiples of 16 bytes and
+ * row_bytes[p] > 0.  More parts: one launch per group of HRT_CAT_MAX_PARTS. */
+#define HRT_CAT_MAX_PARTS 8
+typedef struct hrt_cat_args {
+  uint64_t out;
+  uint64_t src[HRT_CAT_MAX_PARTS];
+  int64_t row_bytes[HRT_CAT_MAX_PARTS];
+  int64_t col[HRT_CAT_MAX_PARTS];
+  int64_t outer, out_row_bytes;
+  int32_t nparts, pad;
+} hrt_cat_args;
+
 /* "ew_fill" — dst[i] = value over a strided index space; value_bits holds the element's bit pattern in
  * its low bytes (dtype selects the element size).  Replaces `try_fill` (csrc/ops_ew.cpp:382-392). */
 typedef struct hrt_fill_args {

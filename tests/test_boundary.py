@@ -54,7 +54,7 @@ def test_runtime_reports_errors_without_a_device():
 
 
 KERNELS = (
-    ["add_f32", "ew_copy", "ew_fill", "ew_map", "reduce_sum"]
+    ["add_f32", "ew_copy", "ew_fill", "ew_map", "reduce_sum", "cat_rows16"]
     + [f"{op}_{k}" for op in ("im2col", "col2im", "upsample_nearest_fwd", "upsample_nearest_bwd", "gn_fwd", "gn_bwd")
        for k in ("f32", "bf16", "f16")]
     + [f"dq8_{k}" for k in ("f32", "bf16", "f16")]
@@ -122,6 +122,7 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
 
     structs = {
         "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs, "hrt_ew_args": abi.EwArgs, "hrt_reduce_args": abi.ReduceArgs,
+        "hrt_cat_args": abi.CatArgs,
         "hrt_im2col_args": abi.Im2colArgs, "hrt_upsample_args": abi.UpsampleArgs, "hrt_gn_args": abi.GnArgs,
         "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_mm_reduce_args": abi.MmReduceArgs,
         "hrt_attn_args": abi.AttnArgs,

@@ -7,6 +7,8 @@ their in-order second pass (run-to-run identical bits), empty, 0-dim and 8-dimen
 dtype, the DiT bias gradient at full size, and cat with mixed float dtypes, integer parts and views.
 """
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -17,6 +19,7 @@ from vkutil import bits
 pytestmark = pytest.mark.gpu
 
 import torch_vulkan  # noqa: E402
+from torch_vulkan import abi  # noqa: E402
 
 dev = torch.device("vk")
 DTYPES = [torch.float32, torch.bfloat16, torch.float16]
@@ -197,3 +200,39 @@ def test_cat_mixed_dtypes_ints_and_views():
     out = torch.cat([xd[:, ::2], xd[:, 1:4].transpose(1, 2).transpose(1, 2), xd[:, :1]], 1)
     assert torch.equal(out.cpu(), torch.cat([x[:, ::2], x[:, 1:4], x[:, :1]], 1))
     no_fallback("aten::cat")
+
+
+# ---- cat in one launch ("cat_rows16": same-dtype contiguous parts, rows of whole 16-byte chunks) -------------
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.int64])
+@pytest.mark.parametrize("shapes,dim", [
+    ([(64, 256), (64, 128), (64, 8)], 1),
+    ([(4, 16, 32)] * 3, 0),
+    ([(2, 8, 16), (2, 0, 16), (2, 24, 16)], 1),  # the empty part is skipped
+    ([(16, 64)] * 11, 1),                         # two launches: 8 parts, then 3
+    ([(1024, 2048)] * 3, 1),                      # the benchmark shape
+])
+def test_cat_one_launch(dt, shapes, dim):
+    parts = [(torch.arange(math.prod(sh), dtype=torch.int64) * 3 + 1000 * i).reshape(sh).to(dt) for i, sh in enumerate(shapes)]
+    out = torch.cat([p.to(dev) for p in parts], dim)
+    assert torch.equal(out.cpu(), torch.cat(parts, dim))
+    no_fallback("aten::cat")
+
+
+def test_cat_rows16_c_abi_and_checks():
+    """The kernel through the C ABI: parts land at their byte columns; non-adjacent parts are rejected."""
+    rt = abi.Runtime()
+    a, b = rnd((32, 24), seed=1), rnd((32, 40), seed=2)
+    ad, bd = a.to(dev), b.to(dev)
+    out = torch.zeros(32, 64, device=dev)
+    A = abi.CatArgs()
+    A.out, A.outer, A.out_row_bytes, A.nparts = out.data_ptr(), 32, 64 * 4, 2
+    A.src[0], A.src[1] = ad.data_ptr(), bd.data_ptr()
+    A.row_bytes[0], A.row_bytes[1] = 24 * 4, 40 * 4
+    A.col[0], A.col[1] = 0, 24 * 4
+    rt.dispatch("cat_rows16", A)
+    rt.synchronize()
+    assert torch.equal(out.cpu(), torch.cat([a, b], 1))
+    A.col[1] = 32 * 4
+    with pytest.raises(RuntimeError, match="adjacent"):
+        rt.dispatch("cat_rows16", A)
+    rt.synchronize()

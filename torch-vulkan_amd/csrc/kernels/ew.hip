@@ -294,5 +294,47 @@ bool launch_fill(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
 }
 HRT_REGISTER("ew_fill", hrt_fill_args, launch_fill);
 
+// ---- cat: all parts in one launch --------------------------------------------------------------------------
+// One 16-byte chunk per lane: out row r, byte column cb in [col[0], col[n-1] + row_bytes[n-1]); the part
+// holding cb is the last one starting at or before it (selected with constant indices, so the argument
+// arrays stay in scalar registers).
+__global__ __launch_bounds__(256) void cat_rows16_k(hrt_cat_args a, int64_t span16, int64_t n16) {
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= n16) return;
+  const int64_t r = j / span16, cb = a.col[0] + (j - r * span16) * 16;
+  uint64_t sp = a.src[0];
+  int64_t rb = a.row_bytes[0], c0 = a.col[0];
+#pragma unroll
+  for (int k = 1; k < HRT_CAT_MAX_PARTS; ++k)
+    if (k < a.nparts && a.col[k] <= cb) {
+      sp = a.src[k];
+      rb = a.row_bytes[k];
+      c0 = a.col[k];
+    }
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)((const uint8_t*)sp + r * rb + (cb - c0)));
+  __builtin_nontemporal_store(v, (u32x4*)((uint8_t*)a.out + r * a.out_row_bytes + cb));
+}
+
+bool launch_cat(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
+  const auto& a = *static_cast<const hrt_cat_args*>(p);
+  if (a.nparts < 1 || a.nparts > HRT_CAT_MAX_PARTS || a.outer < 0) return ctx.fail("cat: 1..8 parts, outer >= 0");
+  if (a.out % 16 || a.out_row_bytes % 16 || a.out_row_bytes <= 0) return ctx.fail("cat: out rows of 16-byte chunks");
+  for (int k = 0; k < a.nparts; ++k) {
+    if (a.src[k] % 16 || a.row_bytes[k] <= 0 || a.row_bytes[k] % 16 || a.col[k] % 16 || a.col[k] < 0)
+      return ctx.fail("cat: parts of whole 16-byte chunks");
+    if (k > 0 && a.col[k] != a.col[k - 1] + a.row_bytes[k - 1]) return ctx.fail("cat: parts must be adjacent");
+  }
+  const int64_t end = a.col[a.nparts - 1] + a.row_bytes[a.nparts - 1];
+  if (end > a.out_row_bytes) return ctx.fail("cat: parts exceed the out row");
+  if (!ctx.check(a.out, (uint64_t)(a.outer * a.out_row_bytes), "out")) return false;
+  for (int k = 0; k < a.nparts; ++k)
+    if (!ctx.check(a.src[k], (uint64_t)(a.outer * a.row_bytes[k]), "src")) return false;
+  const int64_t span16 = (end - a.col[0]) / 16, n16 = a.outer * span16;
+  if (n16 == 0) return true;
+  hipLaunchKernelGGL(cat_rows16_k, dim3((uint32_t)cdiv(n16, 256)), dim3(256), 0, ctx.stream, a, span16, n16);
+  return hrt::launch_ok(hipGetLastError(), ctx, "cat_rows16");
+}
+HRT_REGISTER("cat_rows16", hrt_cat_args, launch_cat);
+
 }  // namespace
 }  // namespace hk

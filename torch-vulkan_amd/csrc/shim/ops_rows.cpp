@@ -259,6 +259,41 @@ at::Tensor k_mean(const at::Tensor& self, std::optional<at::ScalarType> dtype) {
 // The output is allocated on the device and every part is copied into its slice by the strided
 // copy/cast kernel.  Parts of float kinds may differ in dtype (PyTorch's result type); other dtypes must
 // all be the same.  1-D empty parts are skipped (PyTorch's legacy rule, as the reference does).
+// Same-dtype contiguous parts whose rows (the elements from `dim` on) are whole 16-byte chunks: one
+// "cat_rows16" launch per 8 parts instead of one copy per part.
+bool cat_one_launch(const at::Tensor& out, const std::vector<at::Tensor>& parts, int64_t dim) {
+  const int64_t es = (int64_t)out.element_size();
+  int64_t outer = 1, inner = 1;
+  for (int64_t d = 0; d < dim; ++d) outer *= out.size(d);
+  for (int64_t d = dim + 1; d < out.dim(); ++d) inner *= out.size(d);
+  const int64_t orow = out.size(dim) * inner * es;
+  if (outer == 0 || orow == 0 || orow % 16 || reinterpret_cast<uintptr_t>(out.data_ptr()) % 16) return false;
+  std::vector<const at::Tensor*> use;
+  for (const auto& t : parts) {
+    if (t.size(dim) == 0) continue;
+    if (t.scalar_type() != out.scalar_type() || !t.is_contiguous() || (t.size(dim) * inner * es) % 16 ||
+        reinterpret_cast<uintptr_t>(t.data_ptr()) % 16)
+      return false;
+    use.push_back(&t);
+  }
+  int64_t col = 0;
+  for (size_t g = 0; g < use.size(); g += HRT_CAT_MAX_PARTS) {
+    hrt_cat_args A{};
+    A.out = (uint64_t)out.data_ptr();
+    A.outer = outer;
+    A.out_row_bytes = orow;
+    for (size_t k = g; k < use.size() && k < g + HRT_CAT_MAX_PARTS; ++k) {
+      const int i = A.nparts++;
+      A.src[i] = (uint64_t)use[k]->data_ptr();
+      A.row_bytes[i] = use[k]->size(dim) * inner * es;
+      A.col[i] = col;
+      col += A.row_bytes[i];
+    }
+    launch("cat_rows16", A);
+  }
+  return true;
+}
+
 at::Tensor k_cat(const at::ITensorListRef& tensors, int64_t dim) {
   std::vector<at::Tensor> parts;
   bool ok = true, all_float = true, same = true;
@@ -290,10 +325,12 @@ at::Tensor k_cat(const at::ITensorListRef& tensors, int64_t dim) {
       }
       if (ok) {
         at::Tensor out = at::empty(sizes, parts[0].options().dtype(odt));
-        int64_t off = 0;
-        for (const auto& t : parts) {
-          if (t.size(dim) > 0) out.narrow(dim, off, t.size(dim)).copy_(t);
-          off += t.size(dim);
+        if (!cat_one_launch(out, parts, dim)) {
+          int64_t off = 0;
+          for (const auto& t : parts) {
+            if (t.size(dim) > 0) out.narrow(dim, off, t.size(dim)).copy_(t);
+            off += t.size(dim);
+          }
         }
         count_kernel("aten::cat");
         return out;

@@ -53,6 +53,14 @@ class ReduceArgs(ctypes.Structure):
                 ("reduce_mask", u32), ("div", f32), ("pad", u32), ("sizes", i64 * MAX_DIMS), ("strides", i64 * MAX_DIMS)]
 
 
+CAT_MAX_PARTS = 8
+
+
+class CatArgs(ctypes.Structure):
+    _fields_ = [("out", u64), ("src", u64 * CAT_MAX_PARTS), ("row_bytes", i64 * CAT_MAX_PARTS), ("col", i64 * CAT_MAX_PARTS),
+                ("outer", i64), ("out_row_bytes", i64), ("nparts", i32), ("pad", i32)]
+
+
 class Im2colArgs(ctypes.Structure):
     _fields_ = [("x", u64), ("cols", u64)] + [(n, i64) for n in ("N", "C", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW", "PH", "PW")]
 
