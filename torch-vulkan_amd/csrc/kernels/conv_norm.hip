@@ -2,10 +2,10 @@
 // upsampling and its backward, and group_norm forward and backward.  Reference: csrc/ops_conv.cpp:31-221,
 // csrc/ops_norm.cpp:27-142 with vkrt/shaders/im2col.comp.in, upsample.comp.in, gn.comp.in.
 //
-// conv2d runs as im2col followed by the MFMA GEMM (the product dominates; the unfolding is a streaming
-// write of the column matrix, coalesced along the output pixels).  col2im is a gather: each input pixel
-// adds the KH*KW column entries it fed, in a fixed order, so the input gradient is deterministic without
-// atomics.  group_norm's statistics are fp32 partial sums over chunks of each group (a group of a VAE
+// conv2d runs as im2col followed by the MFMA GEMM (the product dominates; the unfolding stages the input
+// rows of a block of output rows in LDS once and streams the column matrix out in 16-byte stores).  col2im
+// is a gather: each input pixel adds the KH*KW column entries it fed, in a fixed order, so the input
+// gradient is deterministic without atomics.  group_norm's statistics are fp32 partial sums over chunks of each group (a group of a VAE
 // layer spans up to millions of elements, so one workgroup per group would leave the GPU idle), each
 // shifted by the chunk's first element and merged with Chan's formula in a fixed order; applying the
 // normalisation and the backward's per-channel sums stream the tensor with coalesced loads.
