@@ -657,43 +657,50 @@ __global__ __launch_bounds__(256) void gn_bwd_sums_k(hrt_gn_args a) {
   }
 }
 
-// Per (n, g): c2 and c3 of dx = rstd*w*g + c2*x + c3, into ws[2*N*C + 2*ng + {0, 1}].
-template <typename T>
-__global__ __launch_bounds__(256) void gn_bwd_coef_k(hrt_gn_args a) {
-  const int64_t ng = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (ng >= a.N * a.G) return;
-  const int64_t Cg = a.C / a.G, n = ng / a.G, g = ng % a.G;
-  const HK_G float* ws = gcptr<float>(a.ws);
-  float dsg = 0.0f, dbg = 0.0f;
-  for (int64_t j = 0; j < Cg; ++j) {
-    const int64_t c = g * Cg + j;
-    const float w = a.w ? ldf<T>(a.w, c) : 1.0f;
-    dsg += ws[n * a.C + c] * w;
-    dbg += ws[a.N * a.C + n * a.C + c] * w;
-  }
-  const float mean = ldf<T>(a.mean, ng), rstd = ldf<T>(a.rstd, ng);
-  const float s = 1.0f / (float)(Cg * a.HW);
-  const float c2 = (dbg * mean - dsg) * rstd * rstd * rstd * s;
-  const float c3 = -c2 * mean - dbg * rstd * s;
-  gptr<float>(a.ws)[2 * a.N * a.C + 2 * ng] = c2;
-  gptr<float>(a.ws)[2 * a.N * a.C + 2 * ng + 1] = c3;
-}
-
-// grid (cdiv(HW / V, 256), N*C): dx = rstd*w*g + c2*x + c3.
+// grid (cdiv(HW / V, 256), N*C): dx = rstd*w*g + c2*x + c3.  c2 and c3 of the channel's group are formed
+// by wave 0 from the per-channel sums (lane j takes channels j, j + 64, .. of the group, then a butterfly
+// sum; a + b == b + a, so every lane, and every workgroup of the group, gets the same bits) while the
+// workgroup's g and x loads are in flight.
 template <typename T, int V>
 __global__ __launch_bounds__(256) void gn_bwd_dx_k(hrt_gn_args a) {
+  __shared__ float cc[2];
   const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
-  if (e >= a.HW) return;
-  const int64_t nc = blockIdx.y, n = nc / a.C, c = nc % a.C, ng = n * a.G + c / (a.C / a.G);
-  const HK_G float* ws = gcptr<float>(a.ws) + 2 * a.N * a.C + 2 * ng;
-  const float c1 = ldf<T>(a.rstd, ng) * (a.w ? ldf<T>(a.w, c) : 1.0f), c2 = ws[0], c3 = ws[1];
+  const int64_t nc = blockIdx.y, n = nc / a.C, c = nc % a.C, Cg = a.C / a.G, g = c / Cg, ng = n * a.G + g;
+  const bool live = e < a.HW;
   const int64_t i = nc * a.HW + e;
-  float g[V], x[V];
-  ldn<T, V>(a.g, i, g);
-  ldn<T, V>(a.x, i, x);
+  float gv[V], xv[V];
+  if (live) {
+    ldn<T, V>(a.g, i, gv);
+    ldn<T, V>(a.x, i, xv);
+  }
+  if (threadIdx.x < 64) {
+    const HK_G float* ws = gcptr<float>(a.ws);
+    float dsg = 0.0f, dbg = 0.0f;
+    for (int64_t j = threadIdx.x; j < Cg; j += 64) {
+      const int64_t cj = g * Cg + j;
+      const float w = a.w ? ldf<T>(a.w, cj) : 1.0f;
+      dsg += ws[n * a.C + cj] * w;
+      dbg += ws[a.N * a.C + n * a.C + cj] * w;
+    }
 #pragma unroll
-  for (int j = 0; j < V; ++j) g[j] = c1 * g[j] + c2 * x[j] + c3;
-  stn<T, V>(a.dx, i, g);
+    for (int m = 1; m < 64; m <<= 1) {
+      dsg += __shfl_xor(dsg, m, 64);
+      dbg += __shfl_xor(dbg, m, 64);
+    }
+    if (threadIdx.x == 0) {
+      const float mean = ldf<T>(a.mean, ng), rstd = ldf<T>(a.rstd, ng);
+      const float s = 1.0f / (float)(Cg * a.HW);
+      const float c2 = (dbg * mean - dsg) * rstd * rstd * rstd * s;
+      cc[0] = c2;
+      cc[1] = -c2 * mean - dbg * rstd * s;
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  const float c1 = ldf<T>(a.rstd, ng) * (a.w ? ldf<T>(a.w, c) : 1.0f), c2 = cc[0], c3 = cc[1];
+#pragma unroll
+  for (int j = 0; j < V; ++j) gv[j] = c1 * gv[j] + c2 * xv[j] + c3;
+  stn<T, V>(a.dx, i, gv);
 }
 
 // Thread per channel: dw[c] = sum_n (ds - db*mean)*rstd, db[c] = sum_n db, n in order.
@@ -763,7 +770,6 @@ bool launch_gn_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (vec) hipLaunchKernelGGL((gn_bwd_sums_k<T, V>), dim3((uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
   else hipLaunchKernelGGL((gn_bwd_sums_k<T, 1>), dim3((uint32_t)(a.N * a.C)), dim3(256), 0, ctx.stream, a);
   if (a.dx) {
-    hipLaunchKernelGGL(gn_bwd_coef_k<T>, dim3((uint32_t)cdiv(a.N * a.G, 256)), dim3(256), 0, ctx.stream, a);
     const dim3 g((uint32_t)cdiv(vec ? a.HW / V : a.HW, 256), (uint32_t)(a.N * a.C));
     if (vec) hipLaunchKernelGGL((gn_bwd_dx_k<T, V>), g, dim3(256), 0, ctx.stream, a);
     else hipLaunchKernelGGL((gn_bwd_dx_k<T, 1>), g, dim3(256), 0, ctx.stream, a);
