@@ -256,6 +256,20 @@ static inline int64_t hrt_ln_chunks(int64_t rows) {
   return (rows + r - 1) / r;
 }
 
+/* hrt_ln_bwd_noalloc — "ln_bwd_{dt}" followed by "ln_wgrad_{dt}" (dx, dw, db of layer_norm) without any
+ * allocation.  No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code recorded into a HIP graph, tight serving loops, harnesses that forbid hipMalloc).  The caller
+ * passes inputs and outputs as for "ln_bwd_{dt}" with ws = 0; the per-chunk partial sums of dw / db go to a
+ * file-scope device array of HRT_LN_SCRATCH_BYTES that the library holds on each GPU until the process
+ * ends.  Its size bounds the problem: hrt_ln_chunks(rows) * 2 * D * 4 bytes must fit (rows * D up to about
+ * 4 Mi elements, e.g. [1024, 2048] or [2048, 2048]) whenever dw or db is requested; larger calls fail with
+ * an error and queue nothing.  dx alone needs no scratch and has no such limit.  Every call writes the
+ * partial sums before reading them, so nothing needs clearing; calls on the runtime's one stream run in
+ * order, but work that overlaps on one GPU (a recorded graph replayed beside another call) shares the array
+ * and races.  dtype: HRT_F32, HRT_BF16 or HRT_F16.  0 = queued, -1 = error (hrt_last_error). */
+#define HRT_LN_SCRATCH_BYTES (8u << 20)
+int hrt_ln_bwd_noalloc(const hrt_ln_args* args, int32_t dtype);
+
 /* "dq8_{f32,bf16,f16}" — weight-only int8 dequant (vkrt/shaders/dq8.comp.in:39-62, closed form
  * torch_vulkan/__init__.py:203-205): out[r, c] = round_dt(float(q[r, c]) * float(scale[r, c / 64])).
  * q: int8 [rows, cols] contiguous; scale: bf16 [rows, nblocks] contiguous, nblocks = ceil(cols / 64);

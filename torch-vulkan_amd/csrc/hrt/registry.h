@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -17,12 +18,17 @@ namespace hrt {
 
 struct LaunchCtx {
   hipStream_t stream = nullptr;
+  int device = 0;
   std::string error;
   // True when [addr, addr + bytes) lies in one live block; otherwise records an error naming `what`.
   bool (*in_bounds)(uint64_t addr, uint64_t bytes, std::string* err) = nullptr;
+  // A device range the launcher owns outside the allocator (a file-scope __device__ scratch array);
+  // operands inside it pass check() without an allocator lookup.
+  uint64_t own_lo = 0, own_hi = 0;
 
   bool check(uint64_t addr, uint64_t bytes, const char* what) {
     if (bytes == 0) return true;
+    if (addr >= own_lo && addr < own_hi && bytes <= own_hi - addr) return true;
     std::string e;
     if (addr == 0 || !in_bounds(addr, bytes, &e)) {
       error = std::string("operand '") + what + "': " + (addr == 0 ? std::string("null address") : e);
@@ -54,9 +60,23 @@ struct KernelRegistrar {
   }
 };
 
+// Per-device set-up that hrt_init runs once, with the selected device current (for instance resolving
+// the address of a file-scope __device__ array).  Returns false and sets *err on failure.
+using DeviceInitFn = bool (*)(int device, std::string* err);
+std::vector<DeviceInitFn>& device_init_table();
+struct DeviceInitRegistrar {
+  explicit DeviceInitRegistrar(DeviceInitFn fn) { device_init_table().push_back(fn); }
+};
+
+// For entry points other than hrt_dispatch: runs `fn` under the runtime lock with a LaunchCtx on the
+// runtime stream.  Returns 0, or -1 with the last error set to "<what>: <ctx.error>" (also when
+// hrt_init has not run).
+int run_launch(const char* what, const std::function<bool(LaunchCtx&)>& fn);
+
 #define HRT_CAT2(a, b) a##b
 #define HRT_CAT(a, b) HRT_CAT2(a, b)
 #define HRT_REGISTER(name, ArgsT, fn) static ::hrt::KernelRegistrar HRT_CAT(hrt_reg_, __COUNTER__)(name, sizeof(ArgsT), fn)
+#define HRT_REGISTER_DEVICE_INIT(fn) static ::hrt::DeviceInitRegistrar HRT_CAT(hrt_dinit_, __COUNTER__)(fn)
 #define HRT_REGISTER_RAW(name, ArgsT, fn) \
   static ::hrt::KernelRegistrar HRT_CAT(hrt_reg_, __COUNTER__)(name, sizeof(ArgsT), fn, true)
 

@@ -30,6 +30,11 @@ std::vector<KernelEntry>& kernel_table() {
   return t;
 }
 
+std::vector<DeviceInitFn>& device_init_table() {
+  static std::vector<DeviceInitFn> t;
+  return t;
+}
+
 namespace {
 
 std::mutex g_err_mu;
@@ -187,6 +192,13 @@ int init_runtime() {
     dev = (int)v;
   }
   if ((e = hipSetDevice(dev)) != hipSuccess) return hip_fail("hipSetDevice", e);
+  for (DeviceInitFn fn : device_init_table()) {  // per-device set-up of the kernel sources, device current
+    std::string err;
+    if (!fn(dev, &err)) {
+      set_error("device set-up: " + err);
+      return -1;
+    }
+  }
   hipDeviceProp_t prop;
   if ((e = hipGetDeviceProperties(&prop, dev)) != hipSuccess) return hip_fail("hipGetDeviceProperties", e);
   rt->device = dev;
@@ -272,6 +284,26 @@ void release_pinned(Runtime* rt, bool all) {
 }
 
 }  // namespace
+
+int run_launch(const char* what, const std::function<bool(LaunchCtx&)>& fn) {
+  Runtime* rt = rt_or_error();
+  if (!rt) return -1;
+  uint64_t t0 = now_ns();
+  std::lock_guard<std::mutex> l(rt->mu);
+  LaunchCtx ctx;
+  ctx.stream = rt->stream;
+  ctx.device = rt->device;
+  ctx.in_bounds = &in_bounds_locked;
+  if (!fn(ctx)) {
+    if (ctx.error.rfind("operand", 0) == 0) g_validation_errors++;
+    set_error(std::string(what) + ": " + ctx.error);
+    return -1;
+  }
+  g_stats[0] += now_ns() - t0;
+  g_stats[1]++;
+  return 0;
+}
+
 }  // namespace hrt
 
 using namespace hrt;
@@ -577,6 +609,7 @@ int hrt_dispatch(uint32_t kernel, const void* args, uint32_t len, uint32_t gx, u
   std::lock_guard<std::mutex> l(rt->mu);
   LaunchCtx ctx;
   ctx.stream = rt->stream;
+  ctx.device = rt->device;
   ctx.in_bounds = &in_bounds_locked;
   const bool prof = rt->profile && !rt->backing.capturing;
   if (prof) (void)hipEventRecord(rt->prof_ev[0], rt->stream);

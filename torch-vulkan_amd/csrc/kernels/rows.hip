@@ -661,6 +661,52 @@ bool launch_ln_wgrad(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   return hrt::launch_ok(hipGetLastError(), ctx, "ln_wgrad");
 }
 
+// ---- allocation-free layer_norm backward (hrt_ln_bwd_noalloc) -------------------------------------------
+// The weight-gradient partial sums go to this array instead of a caller workspace.  Host code never uses
+// its name as an address: the device address is resolved once per device at hrt_init (device current)
+// and kept in ln_scratch_addr.
+static __device__ __align__(256) float scratch[HRT_LN_SCRATCH_BYTES / sizeof(float)];
+constexpr int kMaxDevices = 64;
+uint64_t ln_scratch_addr[kMaxDevices] = {};
+
+bool ln_scratch_setup(int device, std::string* err) {
+  if (device < 0 || device >= kMaxDevices) {
+    *err = "device index " + std::to_string(device) + " out of range for the layer_norm scratch table";
+    return false;
+  }
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr) {
+    (void)hipGetLastError();
+    *err = std::string("hipGetSymbolAddress(layer_norm scratch): ") + hipGetErrorString(e);
+    return false;
+  }
+  ln_scratch_addr[device] = reinterpret_cast<uint64_t>(p);
+  return true;
+}
+HRT_REGISTER_DEVICE_INIT(ln_scratch_setup);
+
+template <typename T>
+bool ln_bwd_into_scratch(hrt_ln_args a, hrt::LaunchCtx& ctx) {
+  static const uint32_t no_grid[3] = {0, 0, 0};
+  const bool wgrad = (a.dw || a.db) && a.rows > 0;
+  if (wgrad) {
+    const uint64_t cap = HRT_LN_SCRATCH_BYTES, per_chunk = 2 * (uint64_t)a.D * sizeof(float);
+    const uint64_t chunks = (uint64_t)hrt_ln_chunks(a.rows);
+    if (per_chunk > cap || chunks > cap / per_chunk)
+      return ctx.fail("rows " + std::to_string(a.rows) + " x D " + std::to_string(a.D) + " needs " +
+                      std::to_string(chunks) + " x " + std::to_string(per_chunk) +
+                      " bytes of weight-gradient partial sums; the scratch array holds " + std::to_string(cap));
+    const uint64_t base = ln_scratch_addr[ctx.device];
+    if (!base) return ctx.fail("the scratch array is not set up on this device");
+    ctx.own_lo = base;
+    ctx.own_hi = base + cap;
+    a.ws = base;
+  }
+  if (!launch_ln_bwd<T>(&a, no_grid, ctx)) return false;
+  return !wgrad || launch_ln_wgrad<T>(&a, no_grid, ctx);
+}
+
 HRT_REGISTER("softmax_fwd_f32", hrt_softmax_args, launch_softmax_fwd<F32>);
 HRT_REGISTER("softmax_fwd_bf16", hrt_softmax_args, launch_softmax_fwd<BF16>);
 HRT_REGISTER("softmax_fwd_f16", hrt_softmax_args, launch_softmax_fwd<F16>);
@@ -679,3 +725,18 @@ HRT_REGISTER("ln_wgrad_f16", hrt_ln_args, launch_ln_wgrad<F16>);
 
 }  // namespace
 }  // namespace hk
+
+extern "C" int hrt_ln_bwd_noalloc(const hrt_ln_args* args, int32_t dtype) {
+  using namespace hk;
+  return hrt::run_launch("hrt_ln_bwd_noalloc", [&](hrt::LaunchCtx& ctx) {
+    if (!args) return ctx.fail("null argument block");
+    if (args->ws) return ctx.fail("ws must be 0: the partial sums live in the library's scratch array");
+    if (args->rows < 0 || args->D <= 0) return ctx.fail("bad shape");
+    switch (dtype) {
+      case HRT_F32: return ln_bwd_into_scratch<F32>(*args, ctx);
+      case HRT_BF16: return ln_bwd_into_scratch<BF16>(*args, ctx);
+      case HRT_F16: return ln_bwd_into_scratch<F16>(*args, ctx);
+      default: return ctx.fail("dtype must be HRT_F32, HRT_BF16 or HRT_F16");
+    }
+  });
+}

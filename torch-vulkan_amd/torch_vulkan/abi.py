@@ -127,6 +127,9 @@ def ln_chunks(rows):
     return (rows + 3) // 4
 
 
+LN_SCRATCH_BYTES = 8 << 20  # HRT_LN_SCRATCH_BYTES (include/hrt_ops.h)
+
+
 class Runtime:
     """The hrt library with typed entry points; one per process (the runtime is a process singleton)."""
 
@@ -172,6 +175,7 @@ class Runtime:
             "hrt_graph_launch": (ctypes.c_int, [i64]),
             "hrt_graph_destroy": (ctypes.c_int, [i64]),
             "hrt_reduce_workspace": (i64, [vp]),
+            "hrt_ln_bwd_noalloc": (ctypes.c_int, [vp, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -217,6 +221,10 @@ class Runtime:
         rc = self.lib.hrt_dispatch_batch(b[0], b[1], b[2], b[3])
         if rc != 0:
             raise RuntimeError(f"hrt_dispatch_batch failed at launch {-rc - 1}: {self.last_error()}")
+
+    def ln_bwd_noalloc(self, args, dtype):
+        """hrt_ln_bwd_noalloc: layer_norm backward with the partial sums in the library's scratch array."""
+        self.check(self.lib.hrt_ln_bwd_noalloc(ctypes.byref(args), dtype), "hrt_ln_bwd_noalloc")
 
     def synchronize(self):
         self.check(self.lib.hrt_synchronize(), "hrt_synchronize")
