@@ -6,12 +6,13 @@ benchmark shape), in algorithmic TFLOP/s: 4*B*H*S^2*D forward + 2.5x that backwa
 step (the convention of the reference's tools/bench_attention.py:39).  A step is the hot path's three
 kernels (forward, dQ with the delta pass folded in, dK/dV) over one batch already resident in HBM, queued
 through the hrt C ABI exactly as the PyTorch shim queues them, directly on the runtime's stream, and timed
-with HIP events on that stream.  The same JSON line carries the other benchmark workloads
-(GEMMs, softmax, layer_norm, int8 dequant, the fused int8 linear, attention at S=4096), each as absolute
-TFLOP/s or GB/s and as a fraction of MI355X's published peak, the roofline object of the step's dominant
-kernel (its HBM traffic from the rocprofv3 counter summary in profiles/, when present), the PyTorch-level
-step time, and the CPU baseline: the oracle's float64 restatement of the same fwd+bwd timed on this host
-(plus, for reference, torch's CPU aten SDPA, which is what the reference runs on CPU).
+with HIP events on that stream.  The roofline object belongs to the step's dominant kernel; its duration
+comes from the same direct step repeated with an event after every kernel, its HBM traffic from the
+rocprofv3 counter summary in profiles/.  The same JSON line carries the step through the PyTorch operator
+path (F.scaled_dot_product_attention + autograd, host work included), the other benchmark workloads (GEMMs,
+softmax, layer_norm, int8 dequant, the fused int8 linear, attention at S=4096, ...) as absolute TFLOP/s or
+GB/s and as a fraction of MI355X's published peaks, and the CPU baseline: the reference's CPU path (torch
+CPU aten) at the full configuration, with the other configurations and the oracle's float64 port beside it.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--skip-cpu] [--only-attn]
        python bench.py --profile {fwd,dq,dkdv,copy,gemm,gemm1024,dq8,softmax,ln,dequant,dit} [--steps K]
@@ -30,8 +31,11 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "torch-vulkan_amd"))
 
 METRIC = "bf16 TFLOP/s flash-attn fwd+bwd (S1024,H16,D128) & GEMM; % of MFMA/HBM peak"
-PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0}  # MI355X published dense matrix peak
-PEAK_GBS = 8000.0  # MI355X HBM3E
+# MI355X dense bf16/f16 matrix peak: 256 CUs x 4096 flop/clock/CU x 2.4 GHz peak engine clock = 2516.6 TFLOP/s
+# (AMD's published "2.5 PFLOP/s" dense figure; the 2:1-sparsity figures are never used here).  Every frac field
+# of this file divides by this one constant.
+PEAK_BF16_TFLOPS = 256 * 4096 * 2.4e9 / 1e12
+PEAK_GBS = 8000.0  # MI355X HBM3E, published 8 TB/s
 
 
 def parse():
@@ -207,13 +211,15 @@ class Bench:
         return step, kernels, keep, names
 
     def attn_headline(self):
-        """K timed steps of fwd+bwd at B1 H16 S1024 D128 bf16, plus per-kernel durations."""
+        """K timed steps of fwd+bwd at B1 H16 S1024 D128 bf16 (the headline), then each of the step's kernels
+        K times back to back, queued directly on the runtime stream like the step (one hrt_dispatch_batch
+        call, no Python between launches) between two events: its average launch duration, from which the
+        roofline's achieved rate is taken.  (An event recorded between every two kernels would cost ~6 us of
+        idle time per event on this runtime and inflate each kernel's time.)"""
         rt, args = self.rt, self.args
         B, H, S, D = 1, 16, 1024, 128
         step, kernels, keep, names = self.attn_setup(B, H, S, D)
         fwd_f, bwd_f = attn_flops(B, H, S, S, D)
-        # the steps are queued directly on the runtime stream, as the shim queues them (replaying the step as
-        # a 3-node HIP graph costs ~10 us more per step on this runtime: each graph launch carries a fixed cost)
         for _ in range(args.warmup):
             step()
         rt.synchronize()
@@ -223,34 +229,24 @@ class Bench:
         rt.event_record(1)
         rt.synchronize()
         ms = rt.elapsed_ms(0, 1) / args.steps
-        gid = rt.graph(step)
-        try:
-            rt.graph_launch(gid)
-            rt.synchronize()
-            rt.event_record(0)
-            for _ in range(args.steps):
-                rt.graph_launch(gid)
-            rt.event_record(1)
-            rt.synchronize()
-            self.graph_step_ms = rt.elapsed_ms(0, 1) / args.steps
-        finally:
-            rt.graph_destroy(gid)
-        # per-kernel average launch durations (20 back-to-back launches each)
-        per = {n: self.time_graph(kernels[n], 20) for n in ("fwd", "dq", "dkdv")}
+        order = ("fwd", "dq", "dkdv")  # the step's own order
+        per = {k: self.time_direct(kernels[k], args.steps, launches=1) for k in order}
+        self.kernel_sum_ms = sum(per.values())
         unit = 2.0 * B * H * S * S * D  # one S x S x D product
         # S, dP are shared by dK/dV; dQ's S and dP are recomputation, and its delta pass is memory work
         algo = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 1 * unit}
         kstats = {}
-        for n, t in per.items():
-            e = {"kernel": names[n], "avg_us": round(t * 1e3, 3), "algo_tflop": algo[n] / 1e12}
-            e["tflops"] = round(algo[n] / (t * 1e-3) / 1e12, 2)
-            e["frac_of_bf16_peak"] = round(e["tflops"] / PEAK_TFLOPS["bf16"], 4)
-            kstats[n] = e
-        dom = max(("fwd", "dkdv", "dq"), key=lambda n: per[n])
+        for k, t in per.items():
+            e = {"kernel": names[k], "avg_us": round(t * 1e3, 3), "algo_tflop": algo[k] / 1e12}
+            e["tflops"] = round(algo[k] / (t * 1e-3) / 1e12, 2)
+            e["frac_of_bf16_peak"] = round(e["tflops"] / PEAK_BF16_TFLOPS, 4)
+            kstats[k] = e
+        dom = max(order, key=lambda k: per[k])
         ach = algo[dom] / (per[dom] * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_TFLOPS["bf16"], 4), "traffic": load_traffic(names[dom]), "kernel": names[dom],
-                "algo_flop_per_launch": algo[dom], "avg_launch_us": round(per[dom] * 1e3, 3)}
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": round(PEAK_BF16_TFLOPS, 1), "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic(names[dom]), "kernel": names[dom],
+                "algo_flop_per_launch": algo[dom], "avg_launch_us": round(per[dom] * 1e3, 3),
+                "timing": f"{args.steps} back-to-back direct launches between two events on the runtime stream"}
         del keep
         return ms, (fwd_f + bwd_f) / (ms * 1e-3) / 1e12, kstats, roof
 
@@ -287,7 +283,7 @@ class Bench:
         per = {n: round(self.time_graph(kernels[n], 5) * 1e3, 2) for n in ("fwd", "dkdv", "dq")}
         del keep
         return {"ms": round(t, 4), "tflops": round((f + b) / (t * 1e-3) / 1e12, 2), "timing": how,
-                "frac_of_bf16_peak": round((f + b) / (t * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4), "kernel_us": per}
+                "frac_of_bf16_peak": round((f + b) / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "kernel_us": per}
 
     # ---- GEMM --------------------------------------------------------------------------------------
     def gemm(self, M, K, N, layout, bias=False):
@@ -311,7 +307,7 @@ class Bench:
         t, how = self.time_best(lambda i: self.rt.dispatch("mm_mfma_bf16", m), 10)
         fl = 2.0 * M * N * K
         return {"shape": f"{M}x{K}x{N}", "layout": layout, "bias": bias, "avg_us": round(t * 1e3, 2), "timing": how,
-                "tflops": round(fl / (t * 1e-3) / 1e12, 2), "frac_of_bf16_peak": round(fl / (t * 1e-3) / 1e12 / 2500.0, 4)}
+                "tflops": round(fl / (t * 1e-3) / 1e12, 2), "frac_of_bf16_peak": round(fl / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
 
     def mm_ops(self, A, B, C, bias=None, alpha=1.0, beta=0.0, ws=None):
         """Argument blocks for C = alpha * A @ B + beta * bias on 2-D views (any strides), the way the shim
@@ -387,7 +383,7 @@ class Bench:
         tb, _ = self.time_best(lambda i: run(base_ops), 3)
         del keep
         return {"ms": round(t, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 2),
-                "frac_of_bf16_peak": round(flops / (t * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4),
+                "frac_of_bf16_peak": round(flops / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                 "flop": flops, "base_gemms_ms": round(tb, 4), "lora_ms": round(t - tb, 4), "timing": how,
                 "launches": len(ops)}
 
@@ -409,7 +405,7 @@ class Bench:
         t, how = self.time_best(lambda i: self.rt.dispatch("mm_dq8_bf16", a), 10)
         fl = 2.0 * M * N * K
         return {"M": M, "avg_us": round(t * 1e3, 2), "tflops": round(fl / (t * 1e-3) / 1e12, 2), "timing": how,
-                "frac_of_bf16_peak": round(fl / (t * 1e-3) / 1e12 / 2500.0, 4)}
+                "frac_of_bf16_peak": round(fl / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
 
     # ---- bandwidth kernels: rotate over > 512 MB so the 256 MB MALL cannot serve them ------------
     def bw(self, name, nbytes, sets, make_args, kernels):
@@ -739,10 +735,16 @@ class Bench:
         self.rt.synchronize()
 
     def cpu_baseline(self):
-        """The oracle (the float64 numpy restatement the parity tests check against) running the headline
-        fwd + delta + bwd on a bounded sample (2 of the 16 heads), timed on this host with the BLAS threads
-        numpy uses; plus torch's CPU aten SDPA fwd+bwd in bf16 on the same sample for reference (what the
-        reference itself runs on CPU)."""
+        """The reference's CPU path: torch's CPU aten operators, which are what the reference runs for anything
+        its device does not take and what its tests compare against (tests/test_fused_attention.py,
+        tests/test_mm.py, tests/test_rows.py, tests/test_dequant_int8.py), timed on this host with torch's
+        thread pool.  `value` is the headline: F.scaled_dot_product_attention forward + backward in bf16 at the
+        full [1,16,1024,128] configuration, in the same algorithmic TFLOP/s as the GPU step (the convention of
+        tools/bench_attention.py:39-41).  `configs` times the other benchmark configurations the same way
+        (GEMMs in TFLOP/s; softmax, layer_norm and dequant in GB/s of algorithmic bytes, as
+        tools/bench_dequant_int8.py:28-29 counts them).  `oracle_port` is the float64 numpy restatement the
+        parity tests check against, on 2 of the 16 heads.  Each figure is the median of at least 5 runs after
+        one untimed run, within a time budget."""
         import numpy as np
         import torch
         import torch.nn.functional as F
@@ -750,55 +752,96 @@ class Bench:
         sys.path.insert(0, REPO)
         import oracle
 
-        B, H, S, D = 1, 2, 1024, 128
-        g = torch.Generator().manual_seed(0)
-        q, k, v, do = (torch.randn((B, H, S, D), generator=g).to(torch.bfloat16) for _ in range(4))
-        qa, ka, va, ga = (t.double().numpy() for t in (q, k, v, do))
-        sc = 1.0 / np.sqrt(D)
-
-        def port():
-            out, lse = oracle.attention_fwd(qa, ka, va, sc)
-            oracle.attention_bwd(qa, ka, va, ga, lse, oracle.attention_delta(out, ga), sc)
-
-        def aten():
-            qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
-            F.scaled_dot_product_attention(qq, kk, vv).backward(do)
-
-        def median_time(fn, budget):
+        def median_time(fn, budget, at_least=5, at_most=200):
             fn()
             times = []
             t_end = time.perf_counter() + budget
-            while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 100):
+            while len(times) < at_least or (time.perf_counter() < t_end and len(times) < at_most):
                 t0 = time.perf_counter()
                 fn()
                 times.append(time.perf_counter() - t0)
             return statistics.median(times), len(times)
 
-        f, b = attn_flops(B, H, S, S, D)
-        t_port, n_port = median_time(port, self.args.cpu_seconds)
-        t_aten, n_aten = median_time(aten, min(self.args.cpu_seconds, 5.0))
-        threads = None
-        try:
-            from threadpoolctl import threadpool_info
-
-            threads = max((i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"), default=None)
-        except Exception:
-            pass
         model = ""
         try:
             with open("/proc/cpuinfo") as fh:
                 model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), "")
         except OSError:
             pass
-        return {"value": round((f + b) / t_port / 1e12, 5), "unit": "TFLOP/s", "cores": threads or os.cpu_count(),
-                "kind": "port", "ms_per_sample": round(t_port * 1e3, 1),
-                "sample": f"oracle.attention_fwd + attention_delta + attention_bwd (numpy float64) on [1,2,1024,128] "
-                          f"bf16-valued inputs = 2 of the 16 heads of the headline step (TFLOP/s is per-sample work / "
-                          f"time, the same rate as the full step), median of {n_port} runs, {model}",
-                "torch_cpu_aten": {"value": round((f + b) / t_aten / 1e12, 5), "unit": "TFLOP/s",
-                                   "cores": torch.get_num_threads(), "ms_per_sample": round(t_aten * 1e3, 1),
-                                   "sample": f"torch {torch.__version__} F.scaled_dot_product_attention fwd+bwd bf16 "
-                                             f"on the same sample, median of {n_aten} runs"}}
+        threads = torch.get_num_threads()
+        gen = torch.Generator().manual_seed(0)
+        bf = torch.bfloat16
+
+        # headline: SDPA fwd + bwd, bf16, the full configuration
+        B, H, S, D = 1, 16, 1024, 128
+        q, k, v, do = (torch.randn((B, H, S, D), generator=gen).to(bf) for _ in range(4))
+
+        def aten():
+            qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+            F.scaled_dot_product_attention(qq, kk, vv).backward(do)
+
+        f, b = attn_flops(B, H, S, S, D)
+        t_aten, n_aten = median_time(aten, self.args.cpu_seconds * 0.6)
+
+        # the oracle port on 2 heads (float64 numpy)
+        Hs = 2
+        qa, ka, va, ga = (t[:, :Hs].double().numpy() for t in (q, k, v, do))
+        sc = 1.0 / np.sqrt(D)
+
+        def port():
+            out, lse = oracle.attention_fwd(qa, ka, va, sc)
+            oracle.attention_bwd(qa, ka, va, ga, lse, oracle.attention_delta(out, ga), sc)
+
+        fp, bp = attn_flops(B, Hs, S, S, D)
+        t_port, n_port = median_time(port, self.args.cpu_seconds * 0.1, at_least=3)
+
+        # the other benchmark configurations
+        budget = self.args.cpu_seconds * 0.3 / 7
+        cfg = {}
+
+        def rate(name, fn, work, unit, sample):
+            t, n = median_time(fn, budget)
+            scale = 1e12 if unit == "TFLOP/s" else 1e9
+            cfg[name] = {"value": round(work / t / scale, 3), "unit": unit, "ms": round(t * 1e3, 3),
+                         "sample": f"{sample}, median of {n} runs"}
+
+        A, Bm, bias = (torch.randn(s_, generator=gen).to(bf) for s_ in ((1024, 1024), (1024, 1024), (1024,)))
+        rate("addmm_1024_bias_bf16", lambda: torch.addmm(bias, A, Bm), 2.0 * 1024 ** 3, "TFLOP/s",
+             "torch.addmm(bias[1024], A[1024,1024], B[1024,1024]) bf16")
+        X, W = torch.randn((1024, 2048), generator=gen).to(bf), torch.randn((8192, 2048), generator=gen).to(bf)
+        rate("mm_1024x2048x8192_nt_bf16", lambda: X @ W.t(), 2.0 * 1024 * 2048 * 8192, "TFLOP/s",
+             "X[1024,2048] @ W[8192,2048]^T bf16 (F.linear layout)")
+        xs = torch.randn((16384, 1024), generator=gen) * 2
+        ys = torch.softmax(xs, -1)
+        gs = torch.randn((16384, 1024), generator=gen)
+        n4 = 16384 * 1024 * 4
+        rate("softmax_fwd_f32_16384x1024", lambda: torch._softmax(xs, -1, False), 2 * n4, "GB/s", "aten::_softmax fp32")
+        rate("softmax_bwd_f32_16384x1024", lambda: torch._softmax_backward_data(gs, ys, -1, torch.float32), 3 * n4, "GB/s",
+             "aten::_softmax_backward_data fp32")
+        xl, gl = (torch.randn((1024, 2048), generator=gen).to(bf) for _ in range(2))
+        wl, bl = (torch.randn((2048,), generator=gen).to(bf) for _ in range(2))
+        _, ml, rl = torch.native_layer_norm(xl, [2048], wl, bl, 1e-5)
+        R_, D_ = 1024, 2048
+        rate("layer_norm_fwd_bf16_1024x2048", lambda: torch.native_layer_norm(xl, [2048], wl, bl, 1e-5),
+             2 * R_ * D_ * 2 + 2 * D_ * 2 + 2 * R_ * 4, "GB/s", "aten::native_layer_norm bf16 with weight and bias")
+        rate("layer_norm_bwd_bf16_1024x2048",
+             lambda: torch.ops.aten.native_layer_norm_backward(gl, xl, [2048], ml, rl, wl, bl, [True, True, True]),
+             3 * R_ * D_ * 2 + D_ * 2 + 2 * R_ * 4 + 2 * D_ * 2, "GB/s", "aten::native_layer_norm_backward bf16 (dx, dw, db)")
+        qi = torch.randint(-127, 128, (8192, 2048), generator=gen, dtype=torch.int8)
+        si = (torch.rand((8192, 32), generator=gen) * 0.019 + 0.001).to(bf)
+        rate("dequant_int8_8192x2048_bf16", lambda: (qi.float() * si.float().repeat_interleave(64, 1)[:, :2048]).to(bf),
+             8192 * 2048 + 8192 * 32 * 2 + 8192 * 2048 * 2, "GB/s",
+             "the reference's CPU closed form (torch_vulkan/__init__.py:203-205)")
+        return {"value": round((f + b) / t_aten / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+                "ms_per_sample": round(t_aten * 1e3, 2),
+                "sample": f"torch {torch.__version__} CPU aten F.scaled_dot_product_attention forward + backward, bf16, "
+                          f"the full [1,16,1024,128] configuration (the reference's CPU path), median of {n_aten} runs "
+                          f"on {threads} threads, {model}",
+                "configs": cfg,
+                "oracle_port": {"value": round((fp + bp) / t_port / 1e12, 5), "unit": "TFLOP/s",
+                                "ms_per_sample": round(t_port * 1e3, 1),
+                                "sample": f"oracle.attention_fwd + attention_delta + attention_bwd (numpy float64) on "
+                                          f"2 of the 16 heads, median of {n_port} runs"}}
 
 
 def main():
@@ -824,10 +867,10 @@ def main():
         "config": {"workload": "flash-attention fwd+bwd, B=1 H=16 S=1024 D=128 bf16, non-causal, scale 1/sqrt(128) "
                                "(benchmark configs[1]+[2]); one step = fwd, dQ (+delta), dK/dV kernels",
                    "B": 1, "H": 16, "S": 1024, "D": 128, "parallelism": "single GPU"},
-        "frac_of_bf16_peak": round(tflops / PEAK_TFLOPS["bf16"], 4),
+        "frac_of_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
         "roofline": roof,
         "attn_kernels": kstats,
-        "ms_per_step_graph_replay": round(bench.graph_step_ms, 5),
+        "ms_sum_of_kernel_averages": round(bench.kernel_sum_ms, 5),
     }
     if not args.only_attn:
         line["attn_torch_path"] = bench.attn_torch_step()

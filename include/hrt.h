@@ -153,7 +153,7 @@ size_t hrt_profile_dump(char* buf, size_t cap);
 uint32_t hrt_coop_caps(void);
 
 /* ---- Timing on the runtime's stream (no counterpart in csrc/vkrt.h) --------------------------------
- * Record HIP event `slot` (0..15) on the runtime stream, and read the elapsed milliseconds between two
+ * Record HIP event `slot` (0..1023) on the runtime stream, and read the elapsed milliseconds between two
  * recorded slots (waits for the later one).  Used by bench.py so that kernel time is measured on the
  * stream the kernels actually run on.  0 / value >= 0 = ok, -1 = error. */
 int hrt_event_record(uint32_t slot);

@@ -88,7 +88,8 @@ struct Runtime {
   bool profile = false;
   std::map<std::string, std::pair<uint64_t, uint64_t>> prof;  // name -> (ns, count)
   hipEvent_t prof_ev[2] = {nullptr, nullptr};
-  hipEvent_t slots[16] = {};
+  static constexpr uint32_t kSlots = 1024;  // timing events (hrt_event_record)
+  hipEvent_t slots[kSlots] = {};
   std::vector<hipGraphExec_t> graphs;
   // Asynchronous uploads run on their own stream (default priority) so they overlap kernels.
   hipStream_t copy_stream = nullptr;
@@ -720,8 +721,8 @@ uint32_t hrt_coop_caps(void) {
 int hrt_event_record(uint32_t slot) {
   Runtime* rt = rt_or_error();
   if (!rt) return -1;
-  if (slot >= 16) {
-    set_error("hrt_event_record: slot must be < 16");
+  if (slot >= Runtime::kSlots) {
+    set_error("hrt_event_record: slot must be < 1024");
     return -1;
   }
   std::lock_guard<std::mutex> l(rt->mu);
@@ -735,7 +736,7 @@ int hrt_event_record(uint32_t slot) {
 float hrt_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot) {
   Runtime* rt = rt_or_error();
   if (!rt) return -1.f;
-  if (start_slot >= 16 || end_slot >= 16 || !rt->slots[start_slot] || !rt->slots[end_slot]) {
+  if (start_slot >= Runtime::kSlots || end_slot >= Runtime::kSlots || !rt->slots[start_slot] || !rt->slots[end_slot]) {
     set_error("hrt_event_elapsed_ms: slot not recorded");
     return -1.f;
   }
