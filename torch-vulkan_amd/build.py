@@ -47,13 +47,17 @@ HRT_SOURCES = [
     "kernels/attn_f32.hip",
 ]
 SHIM_SOURCES = [
-    "shim/shim.cpp",
-    "shim/ops_mm.cpp",
-    "shim/ops_attn.cpp",
-    "shim/ops_rows.cpp",
-    "shim/ops_quant.cpp",
-    "shim/ops_ew.cpp",
-    "shim/ops_conv.cpp",
+    "shim/device.cpp",
+    "shim/fallback.cpp",
+    "shim/bindings.cpp",
+    "shim/autocast.cpp",
+    "shim/op_gemm.cpp",
+    "shim/op_attention.cpp",
+    "shim/op_rows.cpp",
+    "shim/op_reduce.cpp",
+    "shim/op_quant.cpp",
+    "shim/op_ew.cpp",
+    "shim/op_image.cpp",
 ]
 
 

@@ -56,7 +56,7 @@ bool merge_dims(c10::IntArrayRef sizes, c10::IntArrayRef s0, c10::IntArrayRef s1
 }  // namespace
 
 bool ew_copy(const at::Tensor& dst, const at::Tensor& src) {
-  if (!is_vk(dst) || !is_vk(src) || dst.sizes() != src.sizes()) return false;
+  if (!on_vk(dst) || !on_vk(src) || dst.sizes() != src.sizes()) return false;
   if (dst.numel() == 0) return true;
   hrt_copy_args A{};
   const int dc = float_code(dst.scalar_type()), sc = float_code(src.scalar_type());
@@ -69,15 +69,15 @@ bool ew_copy(const at::Tensor& dst, const at::Tensor& src) {
     return false;
   }
   if (!merge_dims(dst.sizes(), dst.strides(), src.strides(), &A.ndim, A.sizes, A.dst_strides, A.src_strides)) return false;
-  A.dst = addr_of(dst);
-  A.src = addr_of(src);
-  launch("ew_copy", A);
-  count_kernel("aten::copy_");
+  A.dst = dptr(dst);
+  A.src = dptr(src);
+  queue("ew_copy", A);
+  note_gpu("aten::copy_");
   return true;
 }
 
 bool ew_fill(const at::Tensor& dst, const at::Scalar& v) {
-  if (!is_vk(dst)) return false;
+  if (!on_vk(dst)) return false;
   if (dst.numel() == 0) return true;
   uint64_t bits = 0;
   switch (dst.scalar_type()) {
@@ -122,9 +122,9 @@ bool ew_fill(const at::Tensor& dst, const at::Scalar& v) {
   if (A.dtype < 0) return false;
   int64_t dummy[HRT_MAX_DIMS];
   if (!merge_dims(dst.sizes(), dst.strides(), dst.strides(), &A.ndim, A.sizes, A.strides, dummy)) return false;
-  A.dst = addr_of(dst);
+  A.dst = dptr(dst);
   A.value_bits = bits;
-  launch("ew_fill", A);
+  queue("ew_fill", A);
   return true;
 }
 
@@ -139,10 +139,10 @@ bool ew_fill(const at::Tensor& dst, const at::Scalar& v) {
 // and the in-place forms of the unary ops are registered too.
 namespace {
 
-using vkt::addr_of;
-using vkt::count_kernel;
+using vkt::dptr;
+using vkt::note_gpu;
 using vkt::float_code;
-using vkt::is_vk;
+using vkt::on_vk;
 
 bool is_float(const at::Tensor& t) { return float_code(t.scalar_type()) >= 0; }
 
@@ -202,18 +202,18 @@ bool run_ew(int op, const at::Tensor& out, const at::Tensor* a, const at::Tensor
   A.ndim = m;
   if (out.numel() == 0) return true;
   A.op = op;
-  A.out = addr_of(out);
+  A.out = dptr(out);
   A.out_dtype = float_code(out.scalar_type());
-  A.a = a ? addr_of(*a) : 0;
+  A.a = a ? dptr(*a) : 0;
   A.a_dtype = a ? float_code(a->scalar_type()) : HRT_F32;
-  A.b = b ? addr_of(*b) : 0;
+  A.b = b ? dptr(*b) : 0;
   A.b_dtype = b ? float_code(b->scalar_type()) : HRT_F32;
-  A.c = c ? addr_of(*c) : 0;
+  A.c = c ? dptr(*c) : 0;
   A.c_dtype = c ? (c->scalar_type() == at::kBool ? HRT_RAW8 : float_code(c->scalar_type())) : HRT_F32;
   A.s0 = s0;
   A.s1 = s1;
-  vkt::launch("ew_map", A);
-  count_kernel(aten_name);
+  vkt::queue("ew_map", A);
+  note_gpu(aten_name);
   return true;
 }
 
@@ -235,7 +235,7 @@ enum class Bin { Add, Sub, Mul, Div };
 // form alpha * value.
 std::optional<at::Tensor> try_scalar(Bin op, const at::Tensor& t, const at::Scalar& v, const at::Scalar& alpha,
                                      bool scalar_left, at::Tensor* self, const char* aten_name) {
-  if (!is_vk(t) || !is_float(t) || v.isComplex() || alpha.isComplex()) return std::nullopt;
+  if (!on_vk(t) || !is_float(t) || v.isComplex() || alpha.isComplex()) return std::nullopt;
   const float fv = v.to<float>(), fa = alpha.to<float>();
   int code;
   float s0, s1 = 0.f;
@@ -268,7 +268,7 @@ std::optional<at::Tensor> try_scalar(Bin op, const at::Tensor& t, const at::Scal
 // Reference: try_binary, csrc/ops_ew.cpp:146-239.
 std::optional<at::Tensor> try_binary(Bin op, const at::Tensor& a, const at::Tensor& b, const at::Scalar& alpha,
                                      at::Tensor* self, const char* aten_name) {
-  if (is_vk(a) && is_vk(b)) {
+  if (on_vk(a) && on_vk(b)) {
     if (!is_float(a) || !is_float(b) || alpha.isComplex()) return std::nullopt;
     const at::ScalarType rt = at::result_type(a, b);
     if (float_code(rt) < 0) return std::nullopt;
@@ -292,11 +292,11 @@ std::optional<at::Tensor> try_binary(Bin op, const at::Tensor& a, const at::Tens
     if (!run_ew(code, out, &ca, &cb, nullptr, alpha.to<float>(), 0.f, aten_name)) return std::nullopt;
     return out;
   }
-  if (is_vk(a) && host_scalar(b)) {
+  if (on_vk(a) && host_scalar(b)) {
     if (at::result_type(a, b) != a.scalar_type()) return std::nullopt;
     return try_scalar(op, a, b.item(), alpha, false, self, aten_name);
   }
-  if (!self && host_scalar(a) && is_vk(b)) {
+  if (!self && host_scalar(a) && on_vk(b)) {
     if (at::result_type(a, b) != b.scalar_type()) return std::nullopt;
     return try_scalar(op, b, a.item(), alpha, true, nullptr, aten_name);
   }
@@ -306,37 +306,37 @@ std::optional<at::Tensor> try_binary(Bin op, const at::Tensor& a, const at::Tens
 #define VKT_EW_BINARY(NAME, OP, ATEN)                                                                  \
   at::Tensor NAME##_Tensor(const at::Tensor& a, const at::Tensor& b, const at::Scalar& alpha) {          \
     if (auto r = try_binary(OP, a, b, alpha, nullptr, ATEN ".Tensor")) return *r;                        \
-    return VKT_FALLBACK(NAME##_Tensor, a, b, alpha);                                                     \
+    return VKT_CPU(NAME##_Tensor, a, b, alpha);                                                     \
   }                                                                                                      \
   at::Tensor& NAME##__Tensor(at::Tensor& self, const at::Tensor& b, const at::Scalar& alpha) {           \
     if (try_binary(OP, self, b, alpha, &self, ATEN "_.Tensor")) return self;                             \
-    return VKT_FALLBACK(NAME##__Tensor, self, b, alpha);                                                 \
+    return VKT_CPU(NAME##__Tensor, self, b, alpha);                                                 \
   }                                                                                                      \
   at::Tensor NAME##_Scalar(const at::Tensor& a, const at::Scalar& b, const at::Scalar& alpha) {          \
     if (auto r = try_scalar(OP, a, b, alpha, false, nullptr, ATEN ".Scalar")) return *r;                 \
-    return VKT_FALLBACK(NAME##_Scalar, a, b, alpha);                                                     \
+    return VKT_CPU(NAME##_Scalar, a, b, alpha);                                                     \
   }                                                                                                      \
   at::Tensor& NAME##__Scalar(at::Tensor& self, const at::Scalar& b, const at::Scalar& alpha) {           \
     if (try_scalar(OP, self, b, alpha, false, &self, ATEN "_.Scalar")) return self;                      \
-    return VKT_FALLBACK(NAME##__Scalar, self, b, alpha);                                                 \
+    return VKT_CPU(NAME##__Scalar, self, b, alpha);                                                 \
   }
 
 #define VKT_EW_BINARY_NOALPHA(NAME, OP, ATEN)                                                          \
   at::Tensor NAME##_Tensor(const at::Tensor& a, const at::Tensor& b) {                                   \
     if (auto r = try_binary(OP, a, b, 1.0, nullptr, ATEN ".Tensor")) return *r;                          \
-    return VKT_FALLBACK(NAME##_Tensor, a, b);                                                            \
+    return VKT_CPU(NAME##_Tensor, a, b);                                                            \
   }                                                                                                      \
   at::Tensor& NAME##__Tensor(at::Tensor& self, const at::Tensor& b) {                                    \
     if (try_binary(OP, self, b, 1.0, &self, ATEN "_.Tensor")) return self;                               \
-    return VKT_FALLBACK(NAME##__Tensor, self, b);                                                        \
+    return VKT_CPU(NAME##__Tensor, self, b);                                                        \
   }                                                                                                      \
   at::Tensor NAME##_Scalar(const at::Tensor& a, const at::Scalar& b) {                                   \
     if (auto r = try_scalar(OP, a, b, 1.0, false, nullptr, ATEN ".Scalar")) return *r;                   \
-    return VKT_FALLBACK(NAME##_Scalar, a, b);                                                            \
+    return VKT_CPU(NAME##_Scalar, a, b);                                                            \
   }                                                                                                      \
   at::Tensor& NAME##__Scalar(at::Tensor& self, const at::Scalar& b) {                                    \
     if (try_scalar(OP, self, b, 1.0, false, &self, ATEN "_.Scalar")) return self;                        \
-    return VKT_FALLBACK(NAME##__Scalar, self, b);                                                        \
+    return VKT_CPU(NAME##__Scalar, self, b);                                                        \
   }
 
 VKT_EW_BINARY(add, Bin::Add, "aten::add")
@@ -346,7 +346,7 @@ VKT_EW_BINARY_NOALPHA(div, Bin::Div, "aten::div")
 
 // ---- unary (reference: try_unary and its users, csrc/ops_ew.cpp:283-334) ------------------------------
 std::optional<at::Tensor> try_unary(int code, const at::Tensor& a, float s0, at::Tensor* self, const char* aten_name) {
-  if (!is_vk(a) || !is_float(a)) return std::nullopt;
+  if (!on_vk(a) || !is_float(a)) return std::nullopt;
   if (self) {
     check_inplace(*self, {});
     if (!run_ew(code, *self, self, nullptr, nullptr, s0, 0.f, aten_name)) return std::nullopt;
@@ -360,11 +360,11 @@ std::optional<at::Tensor> try_unary(int code, const at::Tensor& a, float s0, at:
 #define VKT_EW_UNARY(NAME, CODE)                                                                       \
   at::Tensor k_##NAME(const at::Tensor& a) {                                                             \
     if (auto r = try_unary(CODE, a, 0.f, nullptr, "aten::" #NAME)) return *r;                            \
-    return VKT_FALLBACK(NAME, a);                                                                        \
+    return VKT_CPU(NAME, a);                                                                        \
   }                                                                                                      \
   at::Tensor& k_##NAME##_(at::Tensor& self) {                                                            \
     if (try_unary(CODE, self, 0.f, &self, "aten::" #NAME "_")) return self;                              \
-    return VKT_FALLBACK(NAME##_, self);                                                                  \
+    return VKT_CPU(NAME##_, self);                                                                  \
   }
 
 VKT_EW_UNARY(neg, HRT_EW_NEG)
@@ -384,11 +384,11 @@ bool real_scalar(const at::Scalar& s) { return s.isFloatingPoint() || s.isIntegr
 at::Tensor k_pow_Tensor_Scalar(const at::Tensor& a, const at::Scalar& e) {
   if (real_scalar(e))
     if (auto r = try_unary(HRT_EW_POW_S, a, e.to<float>(), nullptr, "aten::pow.Tensor_Scalar")) return *r;
-  return VKT_FALLBACK(pow_Tensor_Scalar, a, e);
+  return VKT_CPU(pow_Tensor_Scalar, a, e);
 }
 at::Tensor& k_pow__Scalar(at::Tensor& self, const at::Scalar& e) {
   if (real_scalar(e) && try_unary(HRT_EW_POW_S, self, e.to<float>(), &self, "aten::pow_.Scalar")) return self;
-  return VKT_FALLBACK(pow__Scalar, self, e);
+  return VKT_CPU(pow__Scalar, self, e);
 }
 
 int gelu_code(c10::string_view approximate, bool backward) {
@@ -401,17 +401,17 @@ at::Tensor k_gelu(const at::Tensor& a, c10::string_view approximate) {
   const int code = gelu_code(approximate, false);
   if (code >= 0)
     if (auto r = try_unary(code, a, 0.f, nullptr, "aten::gelu")) return *r;
-  return VKT_FALLBACK(gelu, a, approximate);
+  return VKT_CPU(gelu, a, approximate);
 }
 at::Tensor& k_gelu_(at::Tensor& self, c10::string_view approximate) {
   const int code = gelu_code(approximate, false);
   if (code >= 0 && try_unary(code, self, 0.f, &self, "aten::gelu_")) return self;
-  return VKT_FALLBACK(gelu_, self, approximate);
+  return VKT_CPU(gelu_, self, approximate);
 }
 
 // ---- activation backward (grad, input) (reference: csrc/ops_ew.cpp:336-372) ---------------------------
 std::optional<at::Tensor> try_backward(int code, const at::Tensor& g, const at::Tensor& x, const char* aten_name) {
-  if (!is_vk(g) || !is_vk(x) || !is_float(g) || g.scalar_type() != x.scalar_type()) return std::nullopt;
+  if (!on_vk(g) || !on_vk(x) || !is_float(g) || g.scalar_type() != x.scalar_type()) return std::nullopt;
   std::vector<int64_t> sizes;
   try {
     sizes = at::infer_size(g.sizes(), x.sizes());
@@ -425,18 +425,18 @@ std::optional<at::Tensor> try_backward(int code, const at::Tensor& g, const at::
 
 at::Tensor k_silu_backward(const at::Tensor& g, const at::Tensor& x) {
   if (auto r = try_backward(HRT_EW_SILU_BWD, g, x, "aten::silu_backward")) return *r;
-  return VKT_FALLBACK(silu_backward, g, x);
+  return VKT_CPU(silu_backward, g, x);
 }
 at::Tensor k_gelu_backward(const at::Tensor& g, const at::Tensor& x, c10::string_view approximate) {
   const int code = gelu_code(approximate, true);
   if (code >= 0)
     if (auto r = try_backward(code, g, x, "aten::gelu_backward")) return *r;
-  return VKT_FALLBACK(gelu_backward, g, x, approximate);
+  return VKT_CPU(gelu_backward, g, x, approximate);
 }
 
 // ---- where (reference: csrc/ops_ew.cpp:374-392) --------------------------------------------------------
 at::Tensor k_where_self(const at::Tensor& cond, const at::Tensor& a, const at::Tensor& b) {
-  if (is_vk(cond) && is_vk(a) && is_vk(b) && cond.scalar_type() == at::kBool && is_float(a) && is_float(b)) {
+  if (on_vk(cond) && on_vk(a) && on_vk(b) && cond.scalar_type() == at::kBool && is_float(a) && is_float(b)) {
     const at::ScalarType rt = at::result_type(a, b);
     std::vector<int64_t> sizes;
     bool ok = float_code(rt) >= 0;
@@ -451,13 +451,13 @@ at::Tensor k_where_self(const at::Tensor& cond, const at::Tensor& a, const at::T
       if (run_ew(HRT_EW_WHERE, out, &ca, &cb, &cond, 0.f, 0.f, "aten::where.self")) return out;
     }
   }
-  return VKT_FALLBACK(where_self, cond, a, b);
+  return VKT_CPU(where_self, cond, a, b);
 }
 
 // ---- optimizer forms: addcmul(_), addcdiv(_), lerp(_).Scalar (reference: csrc/ops_ew.cpp:394-455) -------
 std::optional<at::Tensor> try_ternary(int code, const at::Tensor& a, const at::Tensor& b, const at::Tensor* c,
                                       const at::Scalar& s, at::Tensor* self, const char* aten_name) {
-  if (!is_vk(a) || !is_vk(b) || (c && !is_vk(*c)) || !is_float(a) || s.isComplex()) return std::nullopt;
+  if (!on_vk(a) || !on_vk(b) || (c && !on_vk(*c)) || !is_float(a) || s.isComplex()) return std::nullopt;
   if (b.scalar_type() != a.scalar_type() || (c && c->scalar_type() != a.scalar_type())) return std::nullopt;
   std::vector<int64_t> sizes;
   try {
@@ -481,27 +481,27 @@ std::optional<at::Tensor> try_ternary(int code, const at::Tensor& a, const at::T
 
 at::Tensor k_addcmul(const at::Tensor& self, const at::Tensor& t1, const at::Tensor& t2, const at::Scalar& value) {
   if (auto r = try_ternary(HRT_EW_ADDCMUL, self, t1, &t2, value, nullptr, "aten::addcmul")) return *r;
-  return VKT_FALLBACK(addcmul, self, t1, t2, value);
+  return VKT_CPU(addcmul, self, t1, t2, value);
 }
 at::Tensor& k_addcmul_(at::Tensor& self, const at::Tensor& t1, const at::Tensor& t2, const at::Scalar& value) {
   if (try_ternary(HRT_EW_ADDCMUL, self, t1, &t2, value, &self, "aten::addcmul_")) return self;
-  return VKT_FALLBACK(addcmul_, self, t1, t2, value);
+  return VKT_CPU(addcmul_, self, t1, t2, value);
 }
 at::Tensor k_addcdiv(const at::Tensor& self, const at::Tensor& t1, const at::Tensor& t2, const at::Scalar& value) {
   if (auto r = try_ternary(HRT_EW_ADDCDIV, self, t1, &t2, value, nullptr, "aten::addcdiv")) return *r;
-  return VKT_FALLBACK(addcdiv, self, t1, t2, value);
+  return VKT_CPU(addcdiv, self, t1, t2, value);
 }
 at::Tensor& k_addcdiv_(at::Tensor& self, const at::Tensor& t1, const at::Tensor& t2, const at::Scalar& value) {
   if (try_ternary(HRT_EW_ADDCDIV, self, t1, &t2, value, &self, "aten::addcdiv_")) return self;
-  return VKT_FALLBACK(addcdiv_, self, t1, t2, value);
+  return VKT_CPU(addcdiv_, self, t1, t2, value);
 }
 at::Tensor k_lerp_Scalar(const at::Tensor& self, const at::Tensor& end, const at::Scalar& weight) {
   if (auto r = try_ternary(HRT_EW_LERP_S, self, end, nullptr, weight, nullptr, "aten::lerp.Scalar")) return *r;
-  return VKT_FALLBACK(lerp_Scalar, self, end, weight);
+  return VKT_CPU(lerp_Scalar, self, end, weight);
 }
 at::Tensor& k_lerp__Scalar(at::Tensor& self, const at::Tensor& end, const at::Scalar& weight) {
   if (try_ternary(HRT_EW_LERP_S, self, end, nullptr, weight, &self, "aten::lerp_.Scalar")) return self;
-  return VKT_FALLBACK(lerp__Scalar, self, end, weight);
+  return VKT_CPU(lerp__Scalar, self, end, weight);
 }
 
 }  // namespace

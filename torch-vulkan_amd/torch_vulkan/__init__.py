@@ -154,8 +154,21 @@ def set_rng_state(new_state, device="vk") -> None:
     return None
 
 
+# Names of the runtime counters (include/hrt.h, hrt_stat) as stats() reports them: (key, index, scale).
+_RUNTIME_COUNTERS = (
+    ("dispatch_s", 0, 1e-9), ("dispatch_n", 1, 1.0), ("transfer_s", 2, 1e-9), ("transfer_n", 3, 1.0),
+    ("pipeline_create_s", 4, 1e-9), ("upload_MB", 5, 1.0 / 2**20), ("download_MB", 6, 1.0 / 2**20),
+    ("gpu_wait_s", 7, 1e-9),
+)
+
+
 def stats() -> dict:
-    return dict(_C.stats())
+    """Host-side runtime counters: time spent queueing kernels and in transfers, their counts, kernel-table
+    set-up time, bytes moved, time waiting for the GPU, and the time spent in CPU fallbacks."""
+    raw = _C.runtime_counters()
+    out = {key: raw[i] * scale for key, i, scale in _RUNTIME_COUNTERS}
+    out["fallback_s"] = sum(fallback_time_by_op().values())
+    return out
 
 
 def fallback_time_by_op() -> dict:
@@ -163,28 +176,30 @@ def fallback_time_by_op() -> dict:
 
 
 def profile() -> str:
-    """Per-kernel GPU time ("name\\tms\\tcount" lines) when HRT_PROFILE=1 was set at start-up."""
+    """Per-kernel GPU time ("name\tms\tcount" lines) when HRT_PROFILE=1 was set at start-up."""
     return _C.profile()
 
 
-def _print_stats_at_exit():
-    st = stats()
-    print("\n[torch_vulkan stats] " + ", ".join(f"{k}={v:.3f}" for k, v in st.items()))
-    top = sorted(fallback_time_by_op().items(), key=lambda kv: -kv[1])[:8]
-    print("[torch_vulkan stats] top fallback time: " + ", ".join(f"{k}={v:.2f}s" for k, v in top))
-    if os.environ.get("HRT_PROFILE"):
-        rows = [r.split("\t") for r in profile().splitlines()]
-        total = sum(float(r[1]) for r in rows) or 1.0
-        print(f"[torch_vulkan profile] GPU time {total:.1f} ms")
-        for name, ms, n in rows[:18]:
-            print(f"[torch_vulkan profile] {name:34s} {float(ms):9.1f} ms {float(ms) / total * 100:5.1f}%  x{n}")
-    print("[torch_vulkan stats] top kernels: " + str(sorted(kernel_counts().items(), key=lambda kv: -kv[1])[:8]))
+def _report_at_exit():
+    """VKT_STATS=1 / HRT_PROFILE=1: a summary of where the time went, printed when the process ends."""
+    lines = ["runtime " + " ".join(f"{k}={v:.3g}" for k, v in stats().items())]
+    slow = sorted(fallback_time_by_op().items(), key=lambda kv: kv[1], reverse=True)
+    if slow:
+        lines.append("CPU fallbacks by time " + " ".join(f"{k}={v:.3g}s" for k, v in slow[:8]))
+    busy = sorted(kernel_counts().items(), key=lambda kv: kv[1], reverse=True)
+    lines.append("GPU operators by count " + " ".join(f"{k}={n}" for k, n in busy[:8]))
+    prof = [row.split("\t") for row in profile().splitlines() if row]
+    if prof:
+        total = sum(float(r[1]) for r in prof) or 1.0
+        lines.append(f"kernel time {total:.1f} ms")
+        lines += [f"  {name:34s} {float(ms):9.1f} ms {100 * float(ms) / total:5.1f}%  x{n}" for name, ms, n in prof[:18]]
+    print("\n".join("[torch_vulkan] " + l for l in lines))
 
 
 if os.environ.get("VKT_STATS") or os.environ.get("HRT_PROFILE"):
     import atexit
 
-    atexit.register(_print_stats_at_exit)
+    atexit.register(_report_at_exit)
 
 
 def coop_caps() -> int:
@@ -250,7 +265,7 @@ def dequant_int8_linear(x, q, scale, bias=None):
 
 
 def event_record(slot: int) -> None:
-    """Record HIP event `slot` (0..15) on the runtime's stream (the stream every vk kernel runs on)."""
+    """Record HIP event `slot` (0..1023) on the runtime's stream (the stream every vk kernel runs on)."""
     _C.event_record(int(slot))
 
 
