@@ -193,7 +193,8 @@ typedef struct hrt_mm_dq8_args {
 /* Fused scaled-dot-product attention, non-causal, no mask, D <= 128 (vkrt/shaders/attn.comp.in:1-14,
  * attn_coop.comp.in:1-9).  q: [B, H, Sq, D], k, v: [B, H, Sk, D] views given by (batch, head, seq)
  * element strides, d contiguous.  Outputs o / o32 / dq / dk / dv are [B, S, H, D]-contiguous (PyTorch
- * returns them permuted to [B, H, S, D], csrc/ops_attn.cpp:159-162); lse and delta are fp32 [B, H, Sq].
+ * returns them permuted to [B, H, S, D], csrc/ops_attn.cpp:159-162; dq / dk / dv may instead follow the
+ * inputs' layout, HRT_ATTN_GRAD_LIKE_INPUT); lse and delta are fp32 [B, H, Sq].
  *
  *  "attn_fwd_{dt}":   o = softmax(scale * q k^T) v (rounded to dt), lse = rowwise logsumexp (fp32),
  *                     o32 = the unrounded fp32 o when o32 != 0.
@@ -209,6 +210,11 @@ typedef struct hrt_mm_dq8_args {
  * counterpart in the reference, which always launches the delta pass on its own (csrc/ops_attn.cpp:240-248):
  * it saves a launch and a second read of dO. */
 #define HRT_ATTN_DQ_DELTA 2u
+/* "attn_dq_{dt}" / "attn_dkdv_{dt}" with this flag write dq, dk, dv in the layout of q, k, v (the element
+ * strides q_sb/q_sh/q_ss, k_*, v_* with d contiguous) instead of [B, S, H, D]-contiguous.  No counterpart
+ * in the reference: PyTorch's autograd copies a leaf's gradient into the leaf's own layout, so gradients
+ * in the input's layout cost nothing there; the caller must give q, k, v non-overlapping dense layouts. */
+#define HRT_ATTN_GRAD_LIKE_INPUT 4u
 typedef struct hrt_attn_args {
   uint64_t q, k, v;
   uint64_t o, lse, o32;

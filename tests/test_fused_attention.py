@@ -218,3 +218,45 @@ def test_baseline_s1024_h16_d128_bf16():
 
 def test_baseline_s4096_h16_d128_bf16():
     baseline_check(4096, 2)  # heads are independent: two of the sixteen heads against the oracle
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd", "expanded_kv"])
+def test_gradients_take_the_input_layout(layout):
+    """dq, dk, dv are written in the layout of q, k, v when those are dense (HRT_ATTN_GRAD_LIKE_INPUT), so
+    autograd stores them as they are; non-dense inputs (a key/value shared across heads by expand) get the
+    [B,S,H,D] layout.  Values against the oracle either way."""
+    B, H, S, D, dt = 2, 4, 96, 64, torch.bfloat16
+    g = uniform((B, H, S, D), dt, 24)
+    if layout == "bhsd":
+        q, k, v = (uniform((B, H, S, D), dt, s) for s in (21, 22, 23))
+        qv, kv, vv = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+        leaves, used = (qv, kv, vv), (qv, kv, vv)
+    elif layout == "bshd":
+        qb, kb, vb = (uniform((B, S, H, D), dt, s) for s in (21, 22, 23))
+        q, k, v = (t.transpose(1, 2) for t in (qb, kb, vb))
+        leaves = tuple(t.to(dev).requires_grad_(True) for t in (qb, kb, vb))
+        used = tuple(t.transpose(1, 2) for t in leaves)
+    else:
+        q = uniform((B, H, S, D), dt, 21)
+        k1, v1 = uniform((B, 1, S, D), dt, 22), uniform((B, 1, S, D), dt, 23)
+        k, v = k1.expand(B, H, S, D), v1.expand(B, H, S, D)
+        leaves = tuple(t.to(dev).requires_grad_(True) for t in (q, k1, v1))
+        used = (leaves[0], leaves[1].expand(B, H, S, D), leaves[2].expand(B, H, S, D))
+    ro, _, rq, rk, rv = oracle_all(q, k, v, g)
+    o = F.scaled_dot_product_attention(*used)
+    gd = g.to(dev)
+    torch_vulkan.reset_fallback_counts()
+    o.backward(gd)
+    kc = torch_vulkan.kernel_counts()
+    if layout == "expanded_kv":  # autograd sums the per-head gradients of the shared key / value
+        rk, rv = rk.sum(axis=1, keepdims=True), rv.sum(axis=1, keepdims=True)
+    for name, leaf, ref in (("dq", leaves[0], rq), ("dk", leaves[1], rk), ("dv", leaves[2], rv)):
+        assert leaf.grad.stride() == leaf.stride(), (name, leaf.grad.stride(), leaf.stride())
+        got = f64(leaf.grad)
+        if layout == "bshd":
+            got = got.transpose(0, 2, 1, 3)
+        e = oracle.rel_l2(got, ref)
+        assert e < REL[dt], f"{name} {layout}: rel-L2 {e}"
+    if layout != "expanded_kv":  # the gradients reach the leaves without a layout copy
+        assert kc.get("aten::copy_", 0) == 0, kc
+    assert oracle.rel_l2(f64(o), ro) < REL[dt]

@@ -43,8 +43,12 @@ bool attn_check(const hrt_attn_args& a, bool fwd, bool dkdv, bool dq, uint64_t e
   if (dkdv || dq) {
     if (!ctx.check(a.dout, hrt::span_bytes(4, qs, dst, elem), "dout") || !ctx.check(a.delta, rows_q * 4, "delta")) return false;
   }
-  if (dkdv && (!ctx.check(a.dk, rows_k * a.D * elem, "dk") || !ctx.check(a.dv, rows_k * a.D * elem, "dv"))) return false;
-  if (dq && !ctx.check(a.dq, rows_q * a.D * elem, "dq")) return false;
+  const bool like_input = (a.flags & HRT_ATTN_GRAD_LIKE_INPUT) != 0;
+  const uint64_t dk_bytes = like_input ? hrt::span_bytes(4, ks, kst, elem) : rows_k * a.D * elem;
+  const uint64_t dv_bytes = like_input ? hrt::span_bytes(4, ks, vst, elem) : rows_k * a.D * elem;
+  const uint64_t dq_bytes = like_input ? hrt::span_bytes(4, qs, qst, elem) : rows_q * a.D * elem;
+  if (dkdv && (!ctx.check(a.dk, dk_bytes, "dk") || !ctx.check(a.dv, dv_bytes, "dv"))) return false;
+  if (dq && !ctx.check(a.dq, dq_bytes, "dq")) return false;
   return true;
 }
 
@@ -257,9 +261,8 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(hrt_attn_args p, int nkb) 
     for (int e = 0; e < 16; ++e) {
       const int64_t kk = kb * 64 + kg * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
       if (kk < Sk && d < D) {
-        const int64_t off = ((b * Sk + kk) * p.H + hh) * D + d;
-        dK[off] = T::from_f32((dk[n][e] + xch[n * 32 + e]) * p.scale);
-        dV[off] = T::from_f32(dv[n][e] + xch[n * 32 + 16 + e]);
+        dK[grad_row(p, b, hh, kk, Sk, p.k_sb, p.k_sh, p.k_ss) + d] = T::from_f32((dk[n][e] + xch[n * 32 + e]) * p.scale);
+        dV[grad_row(p, b, hh, kk, Sk, p.v_sb, p.v_sh, p.v_ss) + d] = T::from_f32(dv[n][e] + xch[n * 32 + 16 + e]);
       }
     }
   }
@@ -391,7 +394,8 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(hrt_attn_args p, int nqb) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int64_t qq = qb * 64 + qg * 32 + 8 * (e >> 2) + 4 * hl + (e & 3);
-      if (qq < Sq && d < D) dQ[((b * Sq + qq) * p.H + hh) * D + d] = T::from_f32((acc[n][e] + xch[n * 16 + e]) * p.scale);
+      if (qq < Sq && d < D)
+        dQ[grad_row(p, b, hh, qq, Sq, p.q_sb, p.q_sh, p.q_ss) + d] = T::from_f32((acc[n][e] + xch[n * 16 + e]) * p.scale);
     }
   }
 }
@@ -636,7 +640,7 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(area + qq * 36 + c4);
       const int64_t qrow = qb * 64 + g * 32 + qq;
       if (qrow < Sq)
-        *reinterpret_cast<HK_G u32x2*>(gptr<uint16_t>(p.dq) + ((b * Sq + qrow) * p.H + hh) * p.D + N * 32 + c4) =
+        *reinterpret_cast<HK_G u32x2*>(gptr<uint16_t>(p.dq) + grad_row(p, b, hh, qrow, Sq, p.q_sb, p.q_sh, p.q_ss) + N * 32 + c4) =
             u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
     }
   };
@@ -873,6 +877,7 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) tr[phys(4 * g4 + i, 16 * dt + l16)] = acc[dt][i];
   const uint64_t dst_base = qh == 0 ? p.dk : p.dv;
+  const int64_t g_sb = qh == 0 ? p.k_sb : p.v_sb, g_sh = qh == 0 ? p.k_sh : p.v_sh, g_ss = qh == 0 ? p.k_ss : p.v_ss;
 #pragma unroll
   for (int ps = 0; ps < 16 * LPR / 64; ++ps) {
     const int r = ps * (64 / LPR) + lane / LPR, c8 = (lane % LPR) * 8;
@@ -880,7 +885,7 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
     const f32x4 y = *reinterpret_cast<const f32x4*>(tr + phys(r, c8) + 4);
     const int64_t kk = kb * 64 + kg * 16 + r;
     if (kk < Sk)
-      *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + ((b * Sk + kk) * p.H + hh) * p.D + c8) =
+      *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + grad_row(p, b, hh, kk, Sk, g_sb, g_sh, g_ss) + c8) =
           u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
   }
 }

@@ -142,8 +142,8 @@ __global__ __launch_bounds__(64) void attn_dkdv_fma(hrt_attn_args p, int nkb) {
     }
   }
   if (key >= Sk) return;
-  S* dK = reinterpret_cast<S*>(p.dk) + ((b * Sk + key) * p.H + hh) * D;
-  S* dV = reinterpret_cast<S*>(p.dv) + ((b * Sk + key) * p.H + hh) * D;
+  S* dK = reinterpret_cast<S*>(p.dk) + grad_row(p, b, hh, key, Sk, p.k_sb, p.k_sh, p.k_ss);
+  S* dV = reinterpret_cast<S*>(p.dv) + grad_row(p, b, hh, key, Sk, p.v_sb, p.v_sh, p.v_ss);
 #pragma unroll
   for (int d = 0; d < DP; ++d)
     if (d < D) {
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(64) void attn_dq_fma(hrt_attn_args p, int nqb) {
     }
   }
   if (!qv) return;
-  S* dQ = reinterpret_cast<S*>(p.dq) + ((b * Sq + q) * p.H + hh) * D;
+  S* dQ = reinterpret_cast<S*>(p.dq) + grad_row(p, b, hh, q, Sq, p.q_sb, p.q_sh, p.q_ss);
 #pragma unroll
   for (int d = 0; d < DP; ++d)
     if (d < D) dQ[d] = T::from_f32(dq[d] * p.scale);

@@ -140,4 +140,11 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Element offset of row (b, h, s) of a gradient output (dq, dk or dv) whose matching input has strides
+// (sb, sh, ss): that layout with HRT_ATTN_GRAD_LIKE_INPUT, else [B, S, H, D]-contiguous over S rows.
+__device__ __forceinline__ int64_t grad_row(const hrt_attn_args& p, int64_t b, int64_t h, int64_t s, int64_t S, int64_t sb,
+                                            int64_t sh, int64_t ss) {
+  return (p.flags & HRT_ATTN_GRAD_LIKE_INPUT) ? b * sb + h * sh + s * ss : ((b * S + s) * p.H + h) * p.D;
+}
+
 }  // namespace hk

@@ -183,6 +183,16 @@ BwdOut k_sdpa_bwd(const at::Tensor& grad_out, const at::Tensor& query, const at:
     A.o = dptr(o_rows);
   }
 
+  // Gradients take their input's layout when q, k and v are all dense (autograd then keeps them as they
+  // are; a [B, S, H, D] gradient of a [B, H, S, D]-contiguous leaf would be copied into the leaf's layout),
+  // else [B, S, H, D]-contiguous memory viewed as [B, H, S, D].
+  const bool like_input = q.is_non_overlapping_and_dense() && k.is_non_overlapping_and_dense() &&
+                          v.is_non_overlapping_and_dense();
+  auto grad_for = [&](const at::Tensor& in, int64_t S) {
+    return like_input ? at::empty_strided(in.sizes(), in.strides(), in.options()) : bshd(d, S, in.options());
+  };
+  if (like_input) A.flags |= HRT_ATTN_GRAD_LIKE_INPUT;
+
   // Order: delta (inside the matrix-core dQ kernel, HRT_ATTN_DQ_DELTA, or as its own pass), dQ, dK/dV.
   const bool fold_delta = need[0] && matrix_cores(dt);
   if (!fold_delta) {
@@ -191,7 +201,7 @@ BwdOut k_sdpa_bwd(const at::Tensor& grad_out, const at::Tensor& query, const at:
   }
   at::Tensor dq, dk, dv;
   if (need[0]) {
-    dq = bshd(d, d.Sq, q.options());
+    dq = grad_for(q, d.Sq);
     hrt_attn_args Q = A;
     Q.dq = dptr(dq);
     if (fold_delta) Q.flags |= HRT_ATTN_DQ_DELTA;
@@ -199,10 +209,8 @@ BwdOut k_sdpa_bwd(const at::Tensor& grad_out, const at::Tensor& query, const at:
     note_gpu(kBwdOp);
   }
   if (need[1] || need[2]) {
-    // dK and dV share one allocation: [2, B, Sk, H, D]
-    const at::Tensor kv = at::empty({2, d.B, d.Sk, d.H, d.D}, q.options());
-    dk = kv.select(0, 0).transpose(1, 2);
-    dv = kv.select(0, 1).transpose(1, 2);
+    dk = grad_for(k, d.Sk);
+    dv = grad_for(v, d.Sk);
     hrt_attn_args KV = A;
     KV.dk = dptr(dk);
     KV.dv = dptr(dv);

@@ -16,6 +16,7 @@ F32, BF16, F16, RAW8, RAW16, RAW32, RAW64 = range(7)
 ATTN_O_F32 = 1
 MM_F32_OUT = 1  # hrt_mm_args.flags: fp32 output (split-K partials)
 ATTN_DQ_DELTA = 2
+ATTN_GRAD_LIKE_INPUT = 4  # hrt_attn_args.flags: dq, dk, dv in the layout of q, k, v
 
 u64, i64, i32, u32, f32 = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float
 
