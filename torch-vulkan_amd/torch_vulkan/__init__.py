@@ -282,6 +282,17 @@ def reset_fallback_counts() -> None:
     _C.reset_counts()
 
 
+def set_inline_backward(on: bool = True) -> None:
+    """Run autograd's backward on the calling thread (PyTorch's thread-local
+    torch.autograd.set_multithreading_enabled(False)), for the thread that calls this.  PyTorch otherwise
+    hands the work of every non-CPU device to a per-device worker thread and waits for it; the vk device
+    has one stream, so that thread adds only a cross-thread handoff: on MI355X a backward() call costs
+    ~49 us of host time on vk that way against ~24 us inline, which left the GPU idle in short steps.
+    Gradients are the same either way.  Applied to the importing thread at import; VKT_THREADED_BACKWARD=1
+    keeps PyTorch's default."""
+    torch._C._set_multithreading_enabled(not on)
+
+
 def _register():
     # Keep nn.Parameter identity when modules move to vk (optimizers built before .to() keep working).
     torch.__future__.set_swap_module_params_on_conversion(True)
@@ -316,6 +327,8 @@ def _register():
 
 
 _register()
+if not os.environ.get("VKT_THREADED_BACKWARD"):
+    set_inline_backward(True)
 
 
 def set_coop_range(lo: int = 0, hi: int = 2**64 - 1, kind: int = 0) -> None:
