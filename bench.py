@@ -339,10 +339,19 @@ class Bench:
         if bias is not None and beta != 0.0:
             bsm, bsn = (0, bias.stride(0)) if bias.dim() == 1 else (bias.stride(0), bias.stride(1))
             m.bias, m.bias_sm, m.bias_sn, m.has_bias = bias.data_ptr(), bsm, bsn, 1
-        tiles = -(-M // 64) * -(-N // 64)
-        S = 1
-        while K % 64 == 0 and min(M, N) <= 64 and tiles * S * 2 <= 256 and (K // 64) % (S * 2) == 0 and K // (S * 2) >= 128:
-            S *= 2
+        S = 1  # the shim's K-split rule (op_gemm.cpp: k_splits)
+        if K % 64 == 0 and min(M, N) <= 64:
+            tiles = -(-M // 64) * -(-N // 64)
+            while tiles * S * 2 <= 256 and (K // 64) % (S * 2) == 0 and K // (S * 2) >= 128:
+                S *= 2
+        elif K % 64 == 0:
+            tiles = max((M // 128) * (N // 256) if M % 128 == 0 and N % 256 == 0 else 0,
+                        (M // 256) * (N // 128) if M % 256 == 0 and N % 128 == 0 else 0)
+            if 0 < tiles < 192:
+                while tiles * S < 192 and K % (64 * 2 * S) == 0 and K // (2 * S) >= 1536:
+                    S *= 2
+                if tiles * S < 192:
+                    S = 1
         if S == 1:
             return [("mm_mfma_bf16", m)]
         assert ws is not None and ws.numel() >= S * M * N, "split-K workspace too small"
@@ -366,7 +375,7 @@ class Bench:
         torch = self.torch
         bf, M, r = torch.bfloat16, 1024, 16
         layers = [(2048, 6144), (2048, 2048), (2048, 8192), (8192, 2048)]
-        ws = torch.empty(8 * 8192 * 16 * 2, dtype=torch.float32, device=self.dev)  # >= S * M * N of every split product
+        ws = torch.empty(4 * 1024 * 2048, dtype=torch.float32, device=self.dev)  # >= S * M * N of every split product
         ops, base_ops, keep, flops, base_flops = [], [], [], 0.0, 0.0
         for li, (fin, fout) in enumerate(layers):
             x = self.randn((M, fin), bf, 100 + li)
@@ -382,7 +391,7 @@ class Bench:
             dh = torch.empty((M, r), dtype=bf, device=self.dev)
             dA = torch.empty((r, fin), dtype=bf, device=self.dev)
             keep += [x, W, b, A, Bl, g, y, h, dx, dB, dh, dA]
-            base = [self.mm_ops(x, W.t(), y, b, 1.0, 1.0), self.mm_ops(g, W, dx)]
+            base = [self.mm_ops(x, W.t(), y, b, 1.0, 1.0, ws=ws), self.mm_ops(g, W, dx, ws=ws)]
             lora = [self.mm_ops(x, A.t(), h, ws=ws), self.mm_ops(h, Bl.t(), y, y, 1.0, 1.0),
                     self.mm_ops(g.t(), h, dB, ws=ws), self.mm_ops(g, Bl, dh, ws=ws), self.mm_ops(dh.t(), x, dA, ws=ws),
                     self.mm_ops(dh, A, dx, dx, 1.0, 1.0)]

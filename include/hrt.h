@@ -28,8 +28,10 @@
 extern "C" {
 #endif
 
-/* Initialise the runtime (idempotent): select the device (env HRT_DEVICE, default 0), create the
- * stream, register the kernels.  0 = ok, -1 = error.  Replaces `vkrt_init` (csrc/vkrt.h:7). */
+/* Initialise the runtime (idempotent): select the device (env HRT_DEVICE: an index, or a case-insensitive
+ * substring of a device name, the lowest-numbered match winning; default 0; no match is an error that
+ * lists the devices), create the stream, register the kernels.  0 = ok, -1 = error.  Replaces `vkrt_init`
+ * (csrc/vkrt.h:7). */
 int hrt_init(void);
 
 /* Copy the last error message into buf (NUL-terminated, at most cap bytes) and return its full

@@ -64,3 +64,25 @@ def test_linear_with_lora_forward_backward(name, fin, fout):
     assert rel(Ad.grad, dA_ref) <= 1e-2
     assert rel(xd.grad[rows], dx_ref) <= 1e-2
     assert "aten::mm" not in torch_vulkan.fallback_counts()
+
+
+def test_first_pass_with_zero_lora_b():
+    """BASELINE config 4's first pass: B is zero-initialised, so the LoRA branch adds exactly 0 (the output
+    equals the base linear bit for bit) and dA = (g B)^T x is exactly 0, while dB = g^T h is not."""
+    M, fin, fout = 1024, 2048, 2048
+    x = randn((M, fin), bf, 61)
+    W = randn((fout, fin), bf, 62, 0.02)
+    b = randn((fout,), bf, 63, 0.02)
+    A = randn((RANK, fin), bf, 64, 0.02)
+    g = randn((M, fout), bf, 65)
+    xd = x.to(dev)
+    Ad = A.to(dev).requires_grad_(True)
+    Bd = torch.zeros((fout, RANK), dtype=bf, device=dev).requires_grad_(True)
+    h = torch.nn.functional.linear(xd, Ad)
+    base = torch.nn.functional.linear(xd, W.to(dev), b.to(dev))
+    y = base + torch.nn.functional.linear(h, Bd)
+    y.backward(g.to(dev))
+    assert torch.equal(y.detach().cpu(), base.cpu())
+    assert not Ad.grad.cpu().any()
+    x64, A64, g64 = f64(x), f64(A), f64(g)
+    assert rel(Bd.grad, g64.T @ rb(x64 @ A64.T)) <= 1e-2

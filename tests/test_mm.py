@@ -273,3 +273,24 @@ def test_baseline_gemm_1024x2048x8192(layout):
         ref = oracle.gemm(f64(a), f64(w).T)
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
     check(out, ref, torch.bfloat16, K)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False)])
+@pytest.mark.parametrize("m,k,n", [(1024, 8192, 2048), (1024, 6144, 2048), (512, 6144, 2048), (1024, 2048, 2048)])
+def test_wide_split_k_on_large_tiles(m, k, n, ta, tb, dt):
+    """Products whose 128 x 256 tiles alone give fewer than 192 workgroups (the DiT stack's 1024 x 2048
+    outputs) split K over the fast kernel's large tiles with fp32 partials (HRT_MM_F32_OUT) and the ordered
+    mm_reduce: against the oracle with bias, alpha and beta, and bit-identical run to run."""
+    a = randn((k, m) if ta else (m, k), dt, 51)
+    b = randn((n, k) if tb else (k, n), dt, 52)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), dt, 53)
+    out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.5)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.5)
+    check(out, ref, dt, k)
+    assert oracle.rel_l2(f64(out), ref) <= (1e-2 if dt == torch.bfloat16 else 4e-3)
+    again = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.5)
+    assert torch.equal(out.cpu(), again.cpu())
+    no_fallback("aten::addmm")

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cctype>
 #include <atomic>
 #include <chrono>
 #include <cstdio>
@@ -177,20 +178,43 @@ int init_runtime() {
     set_error(std::string("no HIP device available: ") + (e != hipSuccess ? hipGetErrorString(e) : "0 devices"));
     return -1;
   }
+  // HRT_DEVICE: a device index, or a case-insensitive substring of a device's name ("name (arch)"), the
+  // lowest-numbered match winning (the reference's VKRT_DEVICE rule, vkrt/src/lib.rs:241-262); anything
+  // else fails with the list of devices.
+  auto display_name = [](int i) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, i) != hipSuccess) {
+      (void)hipGetLastError();
+      return std::string("?");
+    }
+    return std::string(p.name) + " (" + p.gcnArchName + ")";
+  };
+  auto lower = [](std::string t) {
+    for (char& c : t) c = (char)std::tolower((unsigned char)c);
+    return t;
+  };
   int dev = 0;
-  if (dev_env && dev_env[0]) {
+  std::string sel = dev_env ? dev_env : "";
+  while (!sel.empty() && std::isspace((unsigned char)sel.back())) sel.pop_back();
+  while (!sel.empty() && std::isspace((unsigned char)sel.front())) sel.erase(sel.begin());
+  if (!sel.empty()) {
+    int found = -1;
     char* end = nullptr;
-    long v = std::strtol(dev_env, &end, 10);
-    if (end == dev_env || *end != '\0' || v < 0 || v >= count) {
+    const long v = std::strtol(sel.c_str(), &end, 10);
+    if (end != sel.c_str() && *end == '\0') {
+      if (v >= 0 && v < count) found = (int)v;
+    } else {
+      const std::string key = lower(sel);
+      for (int i = 0; i < count && found < 0; ++i)
+        if (lower(display_name(i)).find(key) != std::string::npos) found = i;
+    }
+    if (found < 0) {
       std::string names;
-      for (int i = 0; i < count; ++i) {
-        hipDeviceProp_t p;
-        if (hipGetDeviceProperties(&p, i) == hipSuccess) names += "\n  " + std::to_string(i) + ": " + p.name;
-      }
-      set_error(std::string("HRT_DEVICE='") + dev_env + "' does not name a device; available:" + names);
+      for (int i = 0; i < count; ++i) names += "\n  " + std::to_string(i) + ": " + display_name(i);
+      set_error("HRT_DEVICE='" + sel + "' does not name a device; available:" + names);
       return -1;
     }
-    dev = (int)v;
+    dev = found;
   }
   if ((e = hipSetDevice(dev)) != hipSuccess) return hip_fail("hipSetDevice", e);
   for (DeviceInitFn fn : device_init_table()) {  // per-device set-up of the kernel sources, device current

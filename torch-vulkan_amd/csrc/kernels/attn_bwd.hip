@@ -546,9 +546,10 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
   }
 
   // COPY: stage st + 1 is copied into the other buffers while stage st computes, the copies placed between
-  // the MFMAs of S^T / dP^T (the buffers' previous readers passed the last barrier).  With more than one
-  // stage the copies are branch-free (stage_origin: the last, ragged stage is the window ending at Sk,
-  // its keys before the stage masked; copies past the end repeat the last stage into a buffer nobody reads).
+  // the MFMAs of S^T / dP^T (the buffers' previous readers passed the last barrier); the last, ragged stage
+  // is the window ending at Sk (stage_origin), its keys before the stage masked.  The last stage runs
+  // without copies: the tiles are reused as scratch by the merge below, and a copy landing there late has
+  // been seen to corrupt LDS written after the closing barrier.
   constexpr int IPW = KST2 * NCH / 64 / NW;
   auto stage = [&](auto bc, auto cc, int st) {
     constexpr int BUF = decltype(bc)::value;
@@ -593,13 +594,20 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
       }
     __syncthreads();
   };
-  if (nst == 1) {
-    stage(std::integral_constant<int, 0>(), std::false_type(), 0);
+  // Pairs of copying stages, the last one or two peeled into straight-line code (the loop body holds one
+  // variant per buffer, which keeps the D = 128 kernel within its 256 registers).
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  int st = 0;
+  for (; st + 2 < nst; st += 2) {
+    stage(B0(), std::true_type(), st);
+    stage(B1(), std::true_type(), st + 1);
+  }
+  if (st + 1 < nst) {
+    stage(B0(), std::true_type(), st);
+    stage(B1(), std::false_type(), st + 1);
   } else {
-    for (int st = 0; st < nst; st += 2) {
-      stage(std::integral_constant<int, 0>(), std::true_type(), st);
-      if (st + 1 < nst) stage(std::integral_constant<int, 1>(), std::true_type(), st + 1);
-    }
+    stage(B0(), std::false_type(), st);
   }
 
   // ---- sum the four key quarters: piece (g, n) = d block n of group g, finished by wavefront (g, k = n)
@@ -831,20 +839,30 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  if (nst == 1) {
-    half_stage(I0(), I0(), std::false_type(), 0);
-    if (Sq > QHALF) half_stage(I0(), I1(), std::false_type(), 0);
-    __syncthreads();
-  } else {
-    for (int st = 0; st < nst; st += 2) {
-      half_stage(I0(), I0(), std::true_type(), st);
-      half_stage(I0(), I1(), std::true_type(), st);
-      if (st + 1 < nst) {
-        half_stage(I1(), I0(), std::true_type(), st + 1);
-        half_stage(I1(), I1(), std::true_type(), st + 1);
-      }
-    }
+  // The last stage runs without copies (no stage follows; the tiles are reused as scratch below, and a copy
+  // landing there late has been seen to corrupt LDS written after the closing barrier), then one barrier.
+  // Pairs of copying stages run in the loop, the last one or two are peeled into straight-line code (one
+  // variant per buffer in the loop body keeps the D = 128 kernel within its 256 registers).
+  auto full = [&](auto bc, int st) {
+    half_stage(bc, I0(), std::true_type(), st);
+    half_stage(bc, I1(), std::true_type(), st);
+  };
+  auto last = [&](auto bc, int st) {
+    half_stage(bc, I0(), std::false_type(), st);
+    if (nst > 1 || Sq > QHALF) half_stage(bc, I1(), std::false_type(), st);
+  };
+  int st = 0;
+  for (; st + 2 < nst; st += 2) {
+    full(I0(), st);
+    full(I1(), st + 1);
   }
+  if (st + 1 < nst) {
+    full(I0(), st);
+    last(I1(), st + 1);
+  } else {
+    last(I0(), st);
+  }
+  __syncthreads();
 
   // ---- sum the two query halves through tile k's area: slot 0 takes wave (k, 1)'s dK partials, slot 1 wave
   // (k, 0)'s dV partials (16 bytes per lane and d tile); each wave then reuses its own slot to transpose its

@@ -341,18 +341,22 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
   // interleaved by sched_group_barrier); then O += V(st)^T P(st); then S(st+1) is masked and the running
   // max updated.  K(st) sits in buffer st & 1 and is read one iteration before V(st); the copies go into
   // the buffers the previous iteration finished reading and the closing barrier makes them visible.
-  // COPY = false: single-stage sequences (no copies, no next stage).
+  // MODE 2: both copies (st + 2 < nst); 1: V(st+1) only (st + 2 == nst); 0: the last stage, or a single-
+  // stage sequence: no copies and no next stage.  No copy is ever issued for a stage past the end: the
+  // tiles are reused as scratch by the merge below, and a copy landing there late has been seen to corrupt
+  // LDS written after the closing barrier.
   constexpr int IPW = KST * NCH / 64 / NW;  // copy instructions per tile and wavefront
-  auto stage = [&](auto bc, auto cc, int st, f32x16& s, f32x16& sn) {
+  auto stage = [&](auto bc, auto mc, int st, f32x16& s, f32x16& sn) {
     constexpr int BUF = decltype(bc)::value;
-    constexpr bool COPY = decltype(cc)::value;
+    constexpr int MODE = decltype(mc)::value;
+    constexpr bool COPY = MODE > 0;            // there is a next stage
+    constexpr int NK = MODE == 2 ? IPW : 0;    // K copies of this stage
     const float nm = m == -INFINITY ? 0.f : -m;
     if constexpr (COPY) {
       const HK_G uint8_t* ksrc = Kb + stage_origin<KST>(st + 2, nst, Sk) * kss;
       const HK_G uint8_t* vsrc = Vb + stage_origin<KST>(st + 1, nst, Sk) * vss;
-      // S(st+1) (in the last iteration unused; its tile holds valid data) with this iteration's copies
-      // placed after its MFMAs, one per MFMA, then P(st); the VALU work of P(st) is interleaved with the
-      // MFMAs by sched_group_barrier
+      // S(st+1) with this iteration's copies placed after its MFMAs, one per MFMA, then P(st); the VALU
+      // work of P(st) is interleaved with the MFMAs by sched_group_barrier
       const HK_L uint8_t* Kt = BUF ? K0 : K1;
       u32x4 kfr[2 * DCH];
 #pragma unroll
@@ -361,8 +365,8 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 #pragma unroll
       for (int ks = 0; ks < 2 * DCH; ++ks) {
         sn = Mfma32<T>::mac(kfr[ks], qf[ks], sn);
-        if (ks < IPW) dma_tile_part<NCH, KST, NW>(ksrc, kss, BUF ? K1 : K0, wave, klo, ks);
-        else if (ks < 2 * IPW) dma_tile_part<NCH, KST, NW>(vsrc, vss, BUF ? V0 : V1, wave, vlo, ks - IPW);
+        if (ks < NK) dma_tile_part<NCH, KST, NW>(ksrc, kss, BUF ? K1 : K0, wave, klo, ks);
+        else if (ks < NK + IPW) dma_tile_part<NCH, KST, NW>(vsrc, vss, BUF ? V0 : V1, wave, vlo, ks - NK);
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -374,7 +378,7 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 #pragma unroll
       for (int i = 0; i < 2 * DCH; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (i < 2 * IPW) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+        if (i < NK + IPW) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 48 / (2 * DCH), 0);
       }
     } else {
@@ -408,13 +412,27 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
   f32x16 sa = qk(K0), sb;
   mask_and_max(sa, 0);
   __syncthreads();  // every wave is done with K(0) and Q before they are copied over
-  if (nst == 1) {
-    stage(std::integral_constant<int, 0>(), std::false_type(), 0, sa, sb);
+  using M2 = std::integral_constant<int, 2>;
+  using M1 = std::integral_constant<int, 1>;
+  using M0 = std::integral_constant<int, 0>;
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  // Pairs of full-copy stages, then the last one to three stages peeled into straight-line code (the loop
+  // body holds one variant per buffer, which keeps the D = 128 kernel within its 256 registers).
+  int st = 0;
+  for (; st + 3 < nst; st += 2) {
+    stage(B0(), M2(), st, sa, sb);
+    stage(B1(), M2(), st + 1, sb, sa);
+  }
+  if (st + 2 < nst) {
+    stage(B0(), M2(), st, sa, sb);
+    stage(B1(), M1(), st + 1, sb, sa);
+    stage(B0(), M0(), st + 2, sa, sb);
+  } else if (st + 1 < nst) {
+    stage(B0(), M1(), st, sa, sb);
+    stage(B1(), M0(), st + 1, sb, sa);
   } else {
-    for (int st = 0; st < nst; st += 2) {
-      stage(std::integral_constant<int, 0>(), std::true_type(), st, sa, sb);
-      if (st + 1 < nst) stage(std::integral_constant<int, 1>(), std::true_type(), st + 1, sb, sa);
-    }
+    stage(B0(), M0(), st, sa, sb);
   }
 
   // ---- merge the four key quarters of each query group.  Piece (g, n) = d block n of group g, finished by

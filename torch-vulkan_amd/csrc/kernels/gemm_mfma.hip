@@ -354,10 +354,11 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 // the MFMAs then read exactly as a copied B tile.  The step barrier also waits for these LDS writes.
 constexpr int GBK = 64;
 
-template <typename T, int BM, int BN, int WM, int WN, bool ATR, bool BTR, bool DQ8, int RING = 3>
+template <typename T, int BM, int BN, int WM, int WN, bool ATR, bool BTR, bool DQ8, int RING = 3, bool F32OUT = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args p, int tiles_m, int tiles_n,
                                                                    uint64_t dq_scale, int64_t dq_nblocks) {
   static_assert(!DQ8 || !BTR, "int8 B is staged as [n][k] rows");
+  static_assert(!(DQ8 && F32OUT), "the fused int8 linear writes its own dtype");
   static_assert(RING == 3 || (RING == 2 && !DQ8), "three-buffer ring, or two buffers for the plain GEMM");
   constexpr int WNN = BN / WN;         // wavefronts along n
   constexpr int NW = (BM / WM) * WNN;  // wavefronts
@@ -538,8 +539,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   }
 
   // K step kt: MFMAs from buffer kt % 3, copies of step min(kt + 2, nk - 1) into buffer (kt + 2) % 3 (read
-  // by step kt - 1, whose readers all passed the previous barrier) placed after the first MFMAs; steps
-  // past the end re-copy the last step into a buffer nobody reads again.  Before the barrier that ends
+  // by step kt - 1, whose readers all passed the previous barrier) placed after the first MFMAs; no copy is
+  // issued for steps past the end.  Before the barrier that ends
   // the step each wavefront waits for its copies of the previous step only, so step kt + 1's buffer is
   // complete after the barrier while the copies of step kt + 2 stay in flight.  DQ8: B tiles alternate
   // (kt % 2), int8 step min(kt + 3, nk - 1) is copied into int8 buffer kt % 3 (converted during step
@@ -556,6 +557,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
     const HK_L uint8_t* Bt = DQ8 ? bbuf(bq) : bbuf(bc);
     const int kq = DQ8 ? (kt + 3 < nk ? kt + 3 : nk - 1) : kn;
     const HK_G uint8_t* bn = Bb + kq * bstep;
+    // No copies past the last K step: the ring buffers they would fill are the epilogue's staging areas.
+    // (DQ8: A runs AHEAD = 2 steps ahead, the int8 tiles 3.)
+    const bool more_a = kt + AHEAD < nk, more_b = DQ8 ? kt + 3 < nk : more_a;
     float sv[CPT];
     if constexpr (DQ8) {
 #pragma unroll
@@ -577,21 +581,30 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
       for (int q = 0; q < 4; ++q) {
         const int c = kk * 4 + q;
         if (c < IPA) {
-          dma_tile_part<A_NCH, A_ROWS, NW>(an, ass, abuf(std::integral_constant<int, NXT>()), wave, alo, c);
+          if (more_a) dma_tile_part<A_NCH, A_ROWS, NW>(an, ass, abuf(std::integral_constant<int, NXT>()), wave, alo, c);
         } else if constexpr (!DQ8) {
-          if (c < IPA + IPB)
+          if (c < IPA + IPB && more_b)
             dma_tile_part<B_NCH, B_ROWS, NW>(bn, bss, bbuf(std::integral_constant<int, NXT>()), wave, blo, c - IPA);
         } else {
-          if (c < IPA + IPQ) dma_tile_part<4, BN, NW>(bn, bss, qbuf(std::integral_constant<int, BUF>()), wave, blo, c - IPA);
+          if (c < IPA + IPQ && more_b)
+            dma_tile_part<4, BN, NW>(bn, bss, qbuf(std::integral_constant<int, BUF>()), wave, blo, c - IPA);
         }
       }
       if constexpr (DQ8) {
         if (kk == 1) dq_convert(qbuf(std::integral_constant<int, (BUF + 1) % 3>()), bbuf(std::integral_constant<int, BB ^ 1>()), sv);
       }
     }
-    if constexpr (DQ8) barrier_keep_vm_lds<IPA + IPQ>();
-    else if constexpr (RING == 3) barrier_keep_vm<IPA + IPB>();
-    else __syncthreads();  // the next step's copies, issued in this one, have landed everywhere
+    // each wavefront lets exactly the copies it issued in this step stay in flight
+    if constexpr (DQ8) {
+      if (more_b) barrier_keep_vm_lds<IPA + IPQ>();
+      else if (more_a) barrier_keep_vm_lds<IPA>();
+      else barrier_keep_vm_lds<0>();
+    } else if constexpr (RING == 3) {
+      if (more_a) barrier_keep_vm<IPA + IPB>();
+      else barrier_keep_vm<0>();
+    } else {
+      __syncthreads();  // the next step's copies, issued in this one, have landed everywhere
+    }
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -639,6 +652,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   const bool has_bias = p.has_bias != 0;
   const HK_G uint16_t* bias = gcptr<uint16_t>(p.bias) + bz * p.bias_sb;
   HK_G uint16_t* C = gptr<uint16_t>(p.c) + bz * p.c_sb;
+  HK_G float* C32 = gptr<float>(p.c) + bz * p.c_sb;  // F32OUT: unrounded fp32 results (split-K partials)
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int64_t gn = n0 + wn * WN + j * 32 + l32;
@@ -667,8 +681,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
       const int r = ps * 16 + (lane >> 2), c8 = (lane & 3) * 8;
       const f32x4 x = *reinterpret_cast<const f32x4*>(area + r * RS + c8);
       const f32x4 y = *reinterpret_cast<const f32x4*>(area + r * RS + c8 + 4);
-      *reinterpret_cast<HK_G u32x4*>(C + (m0 + wm * WM + r) * p.c_sm + n0 + wn * WN + j * 32 + c8) =
-          u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+      const int64_t off = (m0 + wm * WM + r) * p.c_sm + n0 + wn * WN + j * 32 + c8;
+      if constexpr (F32OUT) {
+        *reinterpret_cast<HK_G f32x4*>(C32 + off) = x;
+        *reinterpret_cast<HK_G f32x4*>(C32 + off + 4) = y;
+      } else {
+        *reinterpret_cast<HK_G u32x4*>(C + off) =
+            u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+      }
     }
   }
 }
@@ -691,17 +711,17 @@ bool mm_dma_ok(const hrt_mm_args& a, int BM, int BN, bool& atr, bool& btr) {
   return (atr ? a.a_sk : a.a_sm) * 2 * (arows + 1) < lim && (btr ? a.b_sk : a.b_sn) * 2 * (brows + 1) < lim;
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int RING = 3>
+template <typename T, int BM, int BN, int WM, int WN, int RING = 3, bool F32OUT = false>
 bool queue_dma(const hrt_mm_args& a, hipStream_t s) {
   bool atr = false, btr = false;
   if (!mm_dma_ok(a, BM, BN, atr, btr)) return false;
   const int tm = (int)(a.M / BM), tn = (int)(a.N / BN);
   const dim3 g((uint32_t)((int64_t)tm * tn * a.batch)), blk((BM / WM) * (BN / WN) * 64);
   const uint64_t ns = 0;
-  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
-  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, true, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
-  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
-  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, true, false, RING>), g, blk, 0, s, a, tm, tn, ns, 0);
+  if (!atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, false, false, RING, F32OUT>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else if (!atr && btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, false, true, false, RING, F32OUT>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else if (atr && !btr) hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, false, false, RING, F32OUT>), g, blk, 0, s, a, tm, tn, ns, 0);
+  else hipLaunchKernelGGL((mm_dma<T, BM, BN, WM, WN, true, true, false, RING, F32OUT>), g, blk, 0, s, a, tm, tn, ns, 0);
   return true;
 }
 
@@ -788,6 +808,11 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!f32out && a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128, 64, 64>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (!f32out && a.batch * (a.M / 64) * (a.N / 64) >= 128 && queue_dma<T, 64, 64, 32, 32>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
+  // fp32 partials of a split-K product whose slices (the batch) fill the GPU with the large tiles
+  if (f32out && a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256, 64, 64, 3, true>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
+  if (f32out && a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128, 64, 64, 3, true>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (am == GATHER || bm == GATHER) {
     dispatch_gather<T>(a, am, bm, ctx.stream);

@@ -114,15 +114,32 @@ std::optional<Plan> plan(const at::Tensor& a, const at::Tensor& b, const at::Ten
   return p;
 }
 
-// K-split factor for a matrix-core product too narrow to fill the GPU with 64 x 64 output tiles: doubles
-// while the grid stays within one workgroup per CU (256) and every slice keeps >= 128 of K in whole
-// 64-element steps.  1 = no split.  Unbatched products only (the slices use the batch dimension).
+// K-split factor of a matrix-core product (1 = no split; unbatched products only, the slices use the batch
+// dimension; K in whole 64-element steps):
+//  * narrow products, one 64-wide output tile across (min(M, N) <= 64: rank-16 LoRA factors): S doubles
+//    while the grid of 64 x 64 tiles stays within one workgroup per CU (256) and every slice keeps >= 128
+//    of K;
+//  * wide products whose 128 x 256 (or 256 x 128) tiles alone give fewer than 192 workgroups (1024 x 2048
+//    outputs: 64), which would otherwise fall to 64 x 64 tiles that copy three times the bytes per flop:
+//    S doubles until S x tiles >= 192, keeping >= 1536 of K per slice; the slices then run on the large
+//    tiles.  The fp32 partials cost a write and a read of S x M x N x 4 bytes (32 MB at 1024 x 2048, S = 4),
+//    which only long slices repay: measured at 1024 x 2048 outputs, S = 4 takes 51-52 us against 58-65 at
+//    K = 8192 and 44 against 47 at K = 6144, but 29.5 against 17-19 at K = 2048 (S = 2 loses everywhere:
+//    128 large tiles are too few).  S stays 1 when no split reaches 192 workgroups.
 int64_t k_splits(const Plan& p) {
-  if (p.batched || p.K % 64 != 0 || std::min(p.M, p.N) > 64) return 1;
-  const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64), steps = p.K / 64;
+  if (p.batched || p.K % 64 != 0) return 1;
   int64_t s = 1;
-  while (tiles * (2 * s) <= 256 && steps % (2 * s) == 0 && p.K / (2 * s) >= 128) s *= 2;
-  return s;
+  if (std::min(p.M, p.N) <= 64) {
+    const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64), steps = p.K / 64;
+    while (tiles * (2 * s) <= 256 && steps % (2 * s) == 0 && p.K / (2 * s) >= 128) s *= 2;
+    return s;
+  }
+  const int64_t wide = (p.M % 128 == 0 && p.N % 256 == 0) ? (p.M / 128) * (p.N / 256) : 0;
+  const int64_t tall = (p.M % 256 == 0 && p.N % 128 == 0) ? (p.M / 256) * (p.N / 128) : 0;
+  const int64_t tiles = std::max(wide, tall);
+  if (tiles == 0 || tiles >= 192) return 1;
+  while (tiles * s < 192 && p.K % (64 * 2 * s) == 0 && p.K / (2 * s) >= 1536) s *= 2;
+  return tiles * s >= 192 ? s : 1;
 }
 
 // The split product: slice s of K goes to batch entry s of the matrix-core kernel, which writes unrounded
