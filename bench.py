@@ -230,6 +230,12 @@ class Bench:
         rt, args, torch = self.rt, self.args, self.torch
         B, H, S, D = 1, 16, 1024, 128
         step, kernels, keep, names = self.attn_setup(B, H, S, D)
+        # the operator path's inputs are made here, before any timing: drawing them on the CPU takes tens of
+        # milliseconds, and a GPU left idle that long drops its clock, which the W warm-up steps of a short
+        # run do not recover (20 timed steps read 55-70 us per step that way, against 54-55 in steady state)
+        bf = torch.bfloat16
+        qb, kb, vb, gb = (self.randn((B, S, H, D), bf, s) for s in (1, 2, 3, 4))
+        gt = gb.transpose(1, 2)
         fwd_f, bwd_f = attn_flops(B, H, S, S, D)
         order = ("fwd", "dq", "dkdv")
         reps = max(args.steps, 200)
@@ -248,9 +254,6 @@ class Bench:
         del keep
 
         # the operator path
-        bf = torch.bfloat16
-        qb, kb, vb, gb = (self.randn((B, S, H, D), bf, s) for s in (1, 2, 3, 4))
-        gt = gb.transpose(1, 2)
 
         def op_step():
             q, k, v = (t.transpose(1, 2).detach().requires_grad_(True) for t in (qb, kb, vb))
@@ -485,12 +488,15 @@ class Bench:
             a.x, a.g, a.mean, a.rstd, a.w, a.dx, a.ws, a.dw, a.db, a.rows, a.D = (
                 xs[i].data_ptr(), gs[i].data_ptr(), mu.data_ptr(), rs.data_ptr(), w.data_ptr(), dxs[i].data_ptr(),
                 ws.data_ptr(), dw.data_ptr(), db.data_ptr(), R, D)
-            return [a, a]
+            return [a]
 
         fwd_b = 2 * R * D * 2 + 2 * D * 2 + 2 * R * 4
         bwd_b = 3 * R * D * 2 + D * 2 + 2 * R * 4 + 2 * D * 2
-        return {"fwd": self.bw("ln_fwd", fwd_b, sets, fa, ["ln_fwd_bf16"]),
-                "bwd": self.bw("ln_bwd", bwd_b, sets, ba, ["ln_bwd_bf16", "ln_wgrad_bf16"])}
+        fwd = self.bw("ln_fwd", fwd_b, sets, fa, ["ln_fwd_bf16"])
+        bwd = self.bw("ln_bwd", bwd_b, sets, ba, ["ln_bwd_bf16"])  # dx, then dw and db (two kernels)
+        fwd["copy_floor"] = self.copy_floor(R * D * 2, R * D * 2, sets)
+        bwd["copy_floor"] = self.copy_floor(2 * R * D * 2, R * D * 2, sets)
+        return {"fwd": fwd, "bwd": bwd}
 
     def dequant(self):
         torch, abi = self.torch, self.abi
@@ -507,7 +513,29 @@ class Bench:
             a.q, a.scale, a.out, a.rows, a.cols, a.nblocks = qs[i].data_ptr(), ss[i].data_ptr(), outs[i].data_ptr(), R, C, C // 64
             return [a]
 
-        return self.bw("dq8", R * C + R * (C // 64) * 2 + R * C * 2, sets, mk, ["dq8_bf16"])
+        nbytes = R * C + R * (C // 64) * 2 + R * C * 2
+        out = self.bw("dq8", nbytes, sets, mk, ["dq8_bf16"])
+        out["copy_floor"] = self.copy_floor(R * C + R * (C // 64) * 2, R * C * 2, sets)
+        return out
+
+    def copy_floor(self, read_bytes, write_bytes, sets):
+        """The runtime's own device copy (ew_copy, 16 bytes per lane) moving the same total bytes as a
+        bandwidth kernel (half read, half written), timed the same way and rotating over as many buffers: the
+        practical floor that kernel is compared with, launch cost included."""
+        torch, abi = self.torch, self.abi
+        n = (read_bytes + write_bytes) // 2 // 16 * 4  # fp32 elements, whole 16-byte chunks
+        srcs = [torch.empty(n, dtype=torch.float32, device=self.dev).fill_(1.0) for _ in range(sets)]
+        dsts = [torch.empty_like(x) for x in srcs]
+
+        def mk(i):
+            a = abi.CopyArgs()
+            a.dst, a.src, a.ndim, a.dst_dtype, a.src_dtype = dsts[i].data_ptr(), srcs[i].data_ptr(), 1, 0, 0
+            a.sizes[0], a.dst_strides[0], a.src_strides[0] = n, 1, 1
+            return [a]
+
+        r = self.bw("ew_copy", 2 * n * 4, sets, mk, ["ew_copy"])
+        r["read_bytes"] = r["write_bytes"] = n * 4
+        return r
 
     def elementwise(self):
         """ew_map at the shapes of the LoRA/DiT training step: the MLP activation forward and backward

@@ -244,7 +244,9 @@ typedef struct hrt_softmax_args {
  *                   y = (x-mean)*rstd*w + b   (w, b optional = 0); mean, rstd fp32 [rows].
  *  "ln_bwd_{dt}":   dx = rstd*(gw - mean(gw) - xhat*mean(gw*xhat)), gw = g*w, xhat = (x-mean)*rstd
  *                   (dx optional); when ws != 0 also writes per-chunk partial sums of g*xhat and g to
- *                   ws = fp32 [hrt_ln_chunks(rows)][2][D].
+ *                   ws = fp32 [hrt_ln_chunks(rows)][2][D], and when dw or db is also given, queues the
+ *                   "ln_wgrad_{dt}" reduction of them right behind (one call for dx, dw and db).  dw / db
+ *                   without ws is an error.
  *  "ln_wgrad_{dt}": dw[d] = sum over chunks of ws[c][0][d], db[d] = sum of ws[c][1][d] (each optional). */
 typedef struct hrt_ln_args {
   uint64_t x, y, mean, rstd, w, b;
@@ -262,7 +264,8 @@ static inline int64_t hrt_ln_chunks(int64_t rows) {
   return (rows + r - 1) / r;
 }
 
-/* hrt_ln_bwd_noalloc — "ln_bwd_{dt}" followed by "ln_wgrad_{dt}" (dx, dw, db of layer_norm) without any
+/* hrt_ln_bwd_noalloc — "ln_bwd_{dt}" with dw / db (dx, dw, db of layer_norm, as "ln_bwd_{dt}" followed by
+ * "ln_wgrad_{dt}" computes them) without any
  * allocation.  No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code recorded into a HIP graph, tight serving loops, harnesses that forbid hipMalloc).  The caller
  * passes inputs and outputs as for "ln_bwd_{dt}" with ws = 0; the per-chunk partial sums of dw / db go to a

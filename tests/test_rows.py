@@ -168,3 +168,61 @@ def test_layer_norm_baseline_shape_bf16_1024x2048():
     assert oracle.rel_l2(f64(xd.grad), dx) <= 1e-2
     assert oracle.rel_l2(f64(wd.grad), dw) <= 1e-2
     assert oracle.rel_l2(f64(bd.grad), db) <= 1e-2
+
+
+def _ln_bwd_args(x, g, w, mean, rstd, dx, dw, db, ws):
+    from torch_vulkan import abi
+    a = abi.LnArgs()
+    a.x, a.g, a.mean, a.rstd = x.data_ptr(), g.data_ptr(), mean.data_ptr(), rstd.data_ptr()
+    a.w = w.data_ptr() if w is not None else 0
+    a.dx = dx.data_ptr() if dx is not None else 0
+    a.dw = dw.data_ptr() if dw is not None else 0
+    a.db = db.data_ptr() if db is not None else 0
+    a.ws, a.rows, a.D, a.eps = ws, x.shape[0], x.shape[1], 1e-5
+    return a
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,D,affine", [(1024, 2048, True), (1021, 2048, True), (37, 512, False), (13, 1000, True),
+                                           (2, 4096, True), (300, 200, True)])
+def test_layer_norm_backward_one_call_matches_two(dt, rows, D, affine):
+    """"ln_bwd" given dw / db also reduces the partial sums (one call for dx, dw, db, as the shim queues it);
+    it must give the bits of "ln_bwd" followed by "ln_wgrad", on ragged row counts, rows off the full-chunk
+    path and without affine parameters, and two calls in a row on different inputs must each see their own
+    partial sums."""
+    from torch_vulkan import abi
+    rt = abi.Runtime()
+    kind = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dt]
+    chunks = abi.ln_chunks(rows)
+    outs = []
+    for seed in (5, 6):
+        gen = torch.Generator().manual_seed(seed * 1000 + rows)
+        x = (torch.randn(rows, D, generator=gen) * 1.5 + 0.2).to(dt).to(dev)
+        g = torch.randn(rows, D, generator=gen).to(dt).to(dev)
+        w = torch.randn(D, generator=gen).to(dt).to(dev) if affine else None
+        b = torch.randn(D, generator=gen).to(dt).to(dev) if affine else None
+        _, mean, rstd = torch.native_layer_norm(x, [D], w, b, 1e-5)
+        mean, rstd = mean.contiguous(), rstd.contiguous()
+        res = {}
+        for mode in ("one", "two"):
+            dx = torch.empty_like(x)
+            dw = torch.empty(D, dtype=dt, device=dev)
+            db = torch.empty(D, dtype=dt, device=dev)
+            ws = torch.empty(chunks * 2 * D, dtype=torch.float32, device=dev)
+            if mode == "one":
+                rt.dispatch(f"ln_bwd_{kind}", _ln_bwd_args(x, g, w, mean, rstd, dx, dw, db, ws.data_ptr()))
+            else:
+                rt.dispatch(f"ln_bwd_{kind}", _ln_bwd_args(x, g, w, mean, rstd, dx, None, None, ws.data_ptr()))
+                rt.dispatch(f"ln_wgrad_{kind}", _ln_bwd_args(x, g, w, mean, rstd, None, dw, db, ws.data_ptr()))
+            res[mode] = [t.cpu() for t in (dx, dw, db)]
+        for a_, b_ in zip(res["one"], res["two"]):
+            assert torch.equal(a_.view(torch.int16 if a_.element_size() == 2 else torch.int32),
+                               b_.view(torch.int16 if b_.element_size() == 2 else torch.int32))
+        # and against float64: dw = sum(g * xhat), db = sum(g)
+        xh = (f64(x) - f64(mean).reshape(-1, 1)) * f64(rstd).reshape(-1, 1)
+        gd = f64(g)
+        tol = 1e-5 if dt == torch.float32 else 1e-2
+        assert oracle.rel_l2(f64(res["one"][1]), (gd * xh).sum(0)) <= tol
+        assert oracle.rel_l2(f64(res["one"][2]), gd.sum(0)) <= tol
+        outs.append(res["one"])
+    assert not torch.equal(outs[0][1], outs[1][1])  # the two calls saw different inputs

@@ -45,6 +45,26 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
   return u >> 16;
 }
 
+// Eight floats to bf16 with the hardware's round-to-nearest-even (v_cvt_pk_bf16_f32), which equals
+// f32_to_bf16_bits for every non-NaN input; a NaN keeps its sign and payload there, so the caller uses this
+// only when it knows the values hold no NaN (bf16_pack8_checked).
+__device__ __forceinline__ u32x4 bf16_pack8_hw(const float* v) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bf16x2 h = {(__bf16)v[2 * i], (__bf16)v[2 * i + 1]};
+    r[i] = __builtin_bit_cast(uint32_t, h);
+  }
+  return r;
+}
+__device__ __forceinline__ u32x4 bf16_pack8_sw(const float* v) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = f32_to_bf16_bits(v[2 * i]) | (f32_to_bf16_bits(v[2 * i + 1]) << 16);
+  return r;
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   union {
     uint16_t u;
@@ -103,6 +123,24 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+// The same sum without LDS round trips: DPP quad swaps (lane ^ 1, lane ^ 2), the half-row and row mirrors
+// (after the quad steps each quad, then each half-row, holds one value, so a mirror pairs it with the other
+// half), then the gfx950 16- and 32-lane swaps.  Each step adds a pair of values in both of its lanes, so
+// every lane ends with the same bits.  About 20 VALU cycles against ~6 LDS latencies for wave_sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -8,6 +8,7 @@
 // 256-thread workgroup.  Rows that are too long for registers, misaligned, or softmaxes over a
 // non-innermost dimension take a generic multi-pass path.
 #include <cmath>
+#include <type_traits>
 
 #include "../hrt/registry.h"
 #include "device_common.h"
@@ -311,7 +312,33 @@ bool launch_softmax_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
 }
 
 // ================================ layer_norm ============================================================
-template <typename T, int NV, bool FULL>
+// Packs NV chunks of V outputs into 16-byte vectors of T.  bf16 goes through the hardware conversion
+// (bf16_pack8_hw), which rounds like the contract except for NaN: a NaN among the lane's values makes their
+// sum NaN, and then the lane packs with the contract's rounding instead (every NaN -> 0x7FC0).
+template <typename T, int NV, int V>
+__device__ __forceinline__ void pack_chunks(float (&v)[NV][V], u32x4 (&out)[NV]) {
+  if constexpr (std::is_same<T, BF16>::value) {
+    float t = 0.f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c)
+#pragma unroll
+      for (int e = 0; e < V; ++e) t += v[c][e];
+    if (t == t) {
+#pragma unroll
+      for (int c = 0; c < NV; ++c) out[c] = bf16_pack8_hw(v[c]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < NV; ++c) out[c] = bf16_pack8_sw(v[c]);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NV; ++c) out[c] = Vec<T>::pack(v[c]);
+  }
+}
+
+// Forward, register path: one wavefront per row (4 rows per workgroup), the row in registers.  HW / HB:
+// weight / bias present (compile-time, so the per-element work has no selects).
+template <typename T, int NV, bool FULL, bool HW, bool HB>
 __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __restrict__ x,
                                                   typename T::storage* __restrict__ y, float* __restrict__ mean_out,
                                                   float* __restrict__ rstd_out, const typename T::storage* __restrict__ w,
@@ -319,36 +346,47 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
                                                   float eps) {
   constexpr int V = Vec<T>::N;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int64_t row0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool live = row0 < rows;
+  const int64_t row = live ? row0 : rows - 1;  // a row past the end loads the last row and stores nothing
+  // x, w and b of every chunk requested before the first use, with no branch between the loads (a branch
+  // there made the compiler wait for the first chunk's loads before issuing the next: two round trips to
+  // HBM instead of one).  Lanes past the row load its last vector and do not use it.
   float v[NV][V];
-  float s = 0.f;
-  // x, w and b all requested before the reductions (w, b are shared by every row: cached loads)
   u32x4 rx[NV], rw[NV], rb[NV];
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if ((FULL || col < D)) {
-      rx[c] = rd_nt(x + row * D + col);
-      if (w) rw[c] = rd(w + col);
-      if (b) rb[c] = rd(b + col);
-    }
+    const int64_t cl = FULL || col < D ? col : D - V;
+    rx[c] = rd_nt(x + row * D + cl);
+    if constexpr (HW) rw[c] = rd(w + cl);  // shared by every row: cached
+    if constexpr (HB) rb[c] = rd(b + cl);
   }
+  // x passes through an empty asm that also uses w and b, right after the loads: without it the compiler
+  // sinks the w and b loads to their first use, after the two reductions, where they cost a second round
+  // trip.  The row sum needs all of x anyway, so waiting for everything here costs nothing.
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    if constexpr (HW && HB) asm volatile("" : "+v"(rx[c]) : "v"(rw[c]), "v"(rb[c]));
+    else if constexpr (HW) asm volatile("" : "+v"(rx[c]) : "v"(rw[c]));
+    else if constexpr (HB) asm volatile("" : "+v"(rx[c]) : "v"(rb[c]));
+  }
+  float s = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if ((FULL || col < D)) {
-      Vec<T>::unpack(rx[c], v[c]);
+    Vec<T>::unpack(rx[c], v[c]);
+    if (FULL || col < D) {
 #pragma unroll
       for (int e = 0; e < V; ++e) s += v[c][e];
     }
   }
-  const float mean = wave_sum(s) / (float)D;
+  const float mean = wave_sum_dpp(s) / (float)D;
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if ((FULL || col < D)) {
+    if (FULL || col < D) {
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         const float d = v[c][e] - mean;
@@ -356,28 +394,35 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
       }
     }
   }
-  const float var = wave_sum(q) / (float)D;
+  const float var = wave_sum_dpp(q) / (float)D;
   const float rstd = 1.f / sqrtf(var + eps);
+  // y = ((x - mean) * rstd) * w + b, the product and sum as one fma
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
-    const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if ((FULL || col < D)) {
-      float wv[V], bv[V];
-      if (w) Vec<T>::unpack(rw[c], wv);
-      if (b) Vec<T>::unpack(rb[c], bv);
+    float wv[V], bv[V];
+    if constexpr (HW) Vec<T>::unpack(rw[c], wv);
+    if constexpr (HB) Vec<T>::unpack(rb[c], bv);
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        float o = (v[c][e] - mean) * rstd;
-        if (w) o *= wv[e];
-        if (b) o += bv[e];
-        v[c][e] = o;
-      }
-      wr_nt(y + row * D + col, Vec<T>::pack(v[c]));
+    for (int e = 0; e < V; ++e) {
+      const float t = (v[c][e] - mean) * rstd;
+      if constexpr (HW && HB) v[c][e] = fmaf(t, wv[e], bv[e]);
+      else if constexpr (HW) v[c][e] = t * wv[e];
+      else if constexpr (HB) v[c][e] = t + bv[e];
+      else v[c][e] = t;
     }
   }
-  if (lane == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
+  u32x4 out[NV];
+  pack_chunks<T>(v, out);
+  if (live) {
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+      const int64_t col = (int64_t)(c * 64 + lane) * V;
+      if (FULL || col < D) wr_nt(y + row * D + col, out[c]);
+    }
+    if (lane == 0) {
+      mean_out[row] = mean;
+      rstd_out[row] = rstd;
+    }
   }
 }
 
@@ -410,78 +455,83 @@ __global__ __launch_bounds__(256) void ln_fwd_row(const typename T::storage* __r
   }
 }
 
-// Backward, register path: workgroup = one chunk of 4 rows, one wavefront per row.  dx per row; the
-// per-column partial sums of g*xhat and g of the 4 rows are combined through LDS (every wavefront stores
-// its row, then each thread sums the 4 rows of its columns) and written as one ws row pair per chunk.
-template <typename T, int NV, bool FULL>
-__global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __restrict__ x,
-                                                  const typename T::storage* __restrict__ g,
-                                                  const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
-                                                  const typename T::storage* __restrict__ w,
-                                                  typename T::storage* __restrict__ dx, float* __restrict__ ws, int64_t rows,
-                                                  int64_t D) {
+// Backward, register path: one chunk of 4 rows per workgroup, one wavefront per row.  dx per row; with ws,
+// the chunk's column sums of g*xhat and g (its 4 rows added through LDS: every wavefront stores its row,
+// then each thread sums the 4 rows of its columns) as ws row pair `chunk`.  HW: weight present.
+template <typename T, int NV, bool FULL, bool HW>
+__device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restrict__ x, const typename T::storage* __restrict__ g,
+                                             const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+                                             const typename T::storage* __restrict__ w, typename T::storage* __restrict__ dx,
+                                             float* __restrict__ ws, int64_t rows, int64_t D, int64_t chunk, float* part) {
   constexpr int V = Vec<T>::N;
-  extern __shared__ float part[];  // [4 rows][D] when ws != nullptr
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  const bool live = row < rows;
+  const int64_t row0 = chunk * 4 + wave;
+  const bool live = row0 < rows;
+  const int64_t row = live ? row0 : rows - 1;  // a row past the end loads the last row; its terms are zeroed
+  // every load issued before the first use, with no branch between them, and pinned there by the empty asm
+  // (as in ln_fwd_reg); lanes past the row load its last vector and do not use it
   float xh[NV][V], gv[NV][V];
-  float s1 = 0.f, s2 = 0.f, mean = 0.f, rstd = 0.f;
   u32x4 rx[NV], rg[NV], rw[NV];
+  float mean = mean_in[row], rstd = rstd_in[row];
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (live && (FULL || col < D)) {
-      rx[c] = rd_nt(x + row * D + col);
-      rg[c] = rd_nt(g + row * D + col);
-      if (w) rw[c] = rd(w + col);
-    }
+    const int64_t cl = FULL || col < D ? col : D - V;
+    rx[c] = rd_nt(x + row * D + cl);
+    rg[c] = rd_nt(g + row * D + cl);
+    if constexpr (HW) rw[c] = rd(w + cl);
   }
-  if (live) {
-    mean = mean_in[row];
-    rstd = rstd_in[row];
+  asm volatile("" : "+v"(mean), "+v"(rstd));
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    if constexpr (HW) asm volatile("" : "+v"(rx[c]), "+v"(rg[c]) : "v"(rw[c]));
+    else asm volatile("" : "+v"(rx[c]), "+v"(rg[c]));
   }
+  float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
-    if (live && (FULL || col < D)) {
-      float wv[V];
-      Vec<T>::unpack(rx[c], xh[c]);
-      Vec<T>::unpack(rg[c], gv[c]);
-      if (w) Vec<T>::unpack(rw[c], wv);
+    const bool ok = live && (FULL || col < D);
+    float wv[V];
+    Vec<T>::unpack(rx[c], xh[c]);
+    Vec<T>::unpack(rg[c], gv[c]);
+    if constexpr (HW) Vec<T>::unpack(rw[c], wv);
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        xh[c][e] = (xh[c][e] - mean) * rstd;
-        const float gw = w ? gv[c][e] * wv[e] : gv[c][e];
-        s1 += gw;
-        s2 += gw * xh[c][e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < V; ++e) xh[c][e] = gv[c][e] = 0.f;
+    for (int e = 0; e < V; ++e) {
+      xh[c][e] = ok ? (xh[c][e] - mean) * rstd : 0.f;
+      gv[c][e] = ok ? gv[c][e] : 0.f;
+      const float gw = HW ? gv[c][e] * wv[e] : gv[c][e];
+      s1 += gw;
+      s2 += gw * xh[c][e];
     }
   }
-  s1 = wave_sum(s1) / (float)D;
-  s2 = wave_sum(s2) / (float)D;
-  if (dx && live) {
+  s1 = wave_sum_dpp(s1) / (float)D;
+  s2 = wave_sum_dpp(s2) / (float)D;
+  if (dx) {
+    float o[NV][V];
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
-      const int64_t col = (int64_t)(c * 64 + lane) * V;
-      if ((FULL || col < D)) {
-        float wv[V], o[V];
-        if (w) Vec<T>::unpack(rw[c], wv);
+      float wv[V];
+      if constexpr (HW) Vec<T>::unpack(rw[c], wv);
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const float gw = w ? gv[c][e] * wv[e] : gv[c][e];
-          o[e] = rstd * (gw - s1 - xh[c][e] * s2);
-        }
-        wr_nt(dx + row * D + col, Vec<T>::pack(o));
+      for (int e = 0; e < V; ++e) {
+        const float gw = HW ? gv[c][e] * wv[e] : gv[c][e];
+        o[c][e] = rstd * (gw - s1 - xh[c][e] * s2);
+      }
+    }
+    u32x4 out[NV];
+    pack_chunks<T>(o, out);
+    if (live) {
+#pragma unroll
+      for (int c = 0; c < NV; ++c) {
+        const int64_t col = (int64_t)(c * 64 + lane) * V;
+        if (FULL || col < D) wr_nt(dx + row * D + col, out[c]);
       }
     }
   }
   if (!ws) return;  // uniform across the workgroup: no barrier below is skipped by only some waves
-  // rows past the end hold zeros (xh = gv = 0 above)
-  float* out = ws + (int64_t)blockIdx.x * 2 * D;
+  // rows past the end and lanes past the row hold zeros (xh = gv = 0 above)
+  float* out = ws + chunk * 2 * D;
 #pragma unroll
   for (int qn = 0; qn < 2; ++qn) {  // qn = 0: g * xhat, 1: g
     if (qn) __syncthreads();         // the previous quantity's sums have been read
@@ -503,6 +553,50 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
       *reinterpret_cast<f32x4*>(out + qn * D + i) = (r0 + r1) + (r2 + r3);
     }
   }
+}
+
+template <typename T, int NV, bool FULL, bool HW>
+__global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __restrict__ x,
+                                                  const typename T::storage* __restrict__ g,
+                                                  const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+                                                  const typename T::storage* __restrict__ w,
+                                                  typename T::storage* __restrict__ dx, float* __restrict__ ws, int64_t rows,
+                                                  int64_t D) {
+  extern __shared__ float part[];  // [4 rows][D] when ws != nullptr
+  ln_bwd_chunk<T, NV, FULL, HW>(x, g, mean_in, rstd_in, w, dx, ws, rows, D, blockIdx.x, part);
+}
+
+// Sum over chunks of one column of the per-chunk partial sums (src = the column's value in chunk 0, stride
+// = floats between chunks).  Chunk group k of NG takes chunks k, k + NG, ...: eight running sums filled in
+// chunk order (sixteen loads in flight per round), then added in a fixed tree, so the result does not
+// depend on timing.
+template <int NG>
+__device__ __forceinline__ float chunk_column_sum(const float* __restrict__ src, int64_t stride, int64_t chunks, int k) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t c = k;
+  for (; c + 15 * NG < chunks; c += 16 * NG) {  // two rounds of eight at once, added in the same order
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = src[(c + NG * u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += v[u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += v[8 + u];
+  }
+  for (; c + 7 * NG < chunks; c += 8 * NG) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += src[(c + NG * u) * stride];
+  }
+  for (int u = 0; c < chunks; c += NG, ++u) acc[u & 7] += src[c * stride];
+  return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+// The 16 chunk groups' sums of one column (sp[k * W]) added in a fixed tree.
+template <int W>
+__device__ __forceinline__ float combine_groups16(const float* sp) {
+  float t[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) t[k] = sp[(2 * k) * W] + sp[(2 * k + 1) * W];
+  return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
 }
 
 // Backward, generic path: workgroup per chunk of 4 rows; ws accumulated in place (each thread owns its
@@ -551,39 +645,22 @@ __global__ __launch_bounds__(256) void ln_bwd_row(const typename T::storage* __r
   }
 }
 
-// dw[d] = sum_c ws[c][0][d], db[d] = sum_c ws[c][1][d]: workgroup (column block of 64, quantity) with
-// 16 chunk groups of 64 threads (chunk group k takes chunks k, k + 16, ..); each thread keeps 8 loads in
-// flight (independent partial sums), and the groups are combined in a fixed tree order, so the result
-// does not depend on timing.  16 groups leave two rounds of loads per thread at 256 chunks.
+// dw[d] = sum_c ws[c][0][d], db[d] = sum_c ws[c][1][d]: workgroup (column block of 64, quantity) with 16
+// chunk groups of 64 threads, each column summed by chunk_column_sum and the groups combined in a fixed
+// tree, so the result does not depend on timing.
 template <typename T>
 __global__ __launch_bounds__(1024) void ln_wgrad_reduce(const float* __restrict__ ws, typename T::storage* __restrict__ dw,
                                                         typename T::storage* __restrict__ db, int64_t chunks, int64_t D) {
   constexpr int NG = 16;
-  __shared__ float sp[NG][64];
+  __shared__ float sp[NG * 64];
   const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int qn = blockIdx.y;  // 0: dw, 1: db
   typename T::storage* dst = qn ? db : dw;
   if (!dst) return;  // uniform over the workgroup
   const int64_t col = (int64_t)blockIdx.x * 64 + cl;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (col < D) {
-    const float* src = ws + qn * D + col;
-    int64_t c = grp;
-    for (; c + 7 * NG < chunks; c += 8 * NG) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] += src[(c + NG * u) * 2 * D];
-    }
-    for (int u = 0; c < chunks; c += NG, ++u) acc[u & 7] += src[c * 2 * D];
-  }
-  sp[grp][cl] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  sp[grp * 64 + cl] = col < D ? chunk_column_sum<NG>(ws + qn * D + col, 2 * D, chunks, grp) : 0.f;
   __syncthreads();
-  if (grp == 0 && col < D) {
-    float t[NG / 2];
-#pragma unroll
-    for (int k = 0; k < NG / 2; ++k) t[k] = sp[2 * k][cl] + sp[2 * k + 1][cl];
-    const float s = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
-    dst[col] = T::from_f32(s);
-  }
+  if (grp == 0 && col < D) dst[col] = T::from_f32(combine_groups16<64>(sp + cl));
 }
 
 template <typename T>
@@ -603,16 +680,36 @@ bool launch_ln_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int nv = reg_nv<T>(a.D, {a.x, a.y, a.w, a.b});
   const auto full_row = [&](int v) { return a.D == (int64_t)v * 64 * Vec<T>::N; };  // rows fill every chunk: no column guards
   const dim3 g4((uint32_t)cdiv(a.rows, 4));
+  // one instantiation per (chunks per lane, full rows, weight present, bias present)
+  auto go = [&](auto nvc, auto fullc, auto hwc, auto hbc) {
+    hipLaunchKernelGGL((ln_fwd_reg<T, decltype(nvc)::value, decltype(fullc)::value, decltype(hwc)::value, decltype(hbc)::value>),
+                       g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps);
+  };
+  auto by_affine = [&](auto nvc, auto fullc) {
+    using Y = std::true_type;
+    using N = std::false_type;
+    if (w && b) go(nvc, fullc, Y(), Y());
+    else if (w) go(nvc, fullc, Y(), N());
+    else if (b) go(nvc, fullc, N(), Y());
+    else go(nvc, fullc, N(), N());
+  };
+  auto by_full = [&](auto nvc) {
+    if (full_row(decltype(nvc)::value)) by_affine(nvc, std::true_type());
+    else by_affine(nvc, std::false_type());
+  };
   switch (nv) {
-    case 1: if (full_row(1)) hipLaunchKernelGGL((ln_fwd_reg<T, 1, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 1, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
-    case 2: if (full_row(2)) hipLaunchKernelGGL((ln_fwd_reg<T, 2, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 2, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
-    case 4: if (full_row(4)) hipLaunchKernelGGL((ln_fwd_reg<T, 4, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 4, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
-    case 8: if (full_row(8)) hipLaunchKernelGGL((ln_fwd_reg<T, 8, true>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); else hipLaunchKernelGGL((ln_fwd_reg<T, 8, false>), g4, dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.rows, a.D, a.eps); break;
+    case 1: by_full(std::integral_constant<int, 1>()); break;
+    case 2: by_full(std::integral_constant<int, 2>()); break;
+    case 4: by_full(std::integral_constant<int, 4>()); break;
+    case 8: by_full(std::integral_constant<int, 8>()); break;
     default:
       hipLaunchKernelGGL(ln_fwd_row<T>, dim3((uint32_t)a.rows), dim3(256), 0, ctx.stream, x, y, mu, rs, w, b, a.D, a.eps);
   }
   return hrt::launch_ok(hipGetLastError(), ctx, "ln_fwd");
 }
+
+template <typename T>
+bool launch_ln_wgrad(const void* p, const uint32_t*, hrt::LaunchCtx& ctx);
 
 template <typename T>
 bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
@@ -623,9 +720,12 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   using S = typename T::storage;
   const uint64_t bytes = (uint64_t)(a.rows * a.D) * sizeof(S);
   const int64_t chunks = hrt_ln_chunks(a.rows);
+  const bool wgrad = a.ws && (a.dw || a.db);
+  if ((a.dw || a.db) && !a.ws) return ctx.fail("dw / db need the partial-sum workspace ws");
   if (!ctx.check(a.x, bytes, "x") || !ctx.check(a.g, bytes, "g") || !ctx.check(a.mean, a.rows * 4, "mean") ||
       !ctx.check(a.rstd, a.rows * 4, "rstd") || (a.w && !ctx.check(a.w, a.D * sizeof(S), "w")) ||
-      (a.dx && !ctx.check(a.dx, bytes, "dx")) || (a.ws && !ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws")))
+      (a.dx && !ctx.check(a.dx, bytes, "dx")) || (a.ws && !ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws")) ||
+      (a.dw && !ctx.check(a.dw, a.D * sizeof(S), "dw")) || (a.db && !ctx.check(a.db, a.D * sizeof(S), "db")))
     return false;
   const S *x = (const S*)a.x, *g = (const S*)a.g, *w = (const S*)a.w;
   S* dx = (S*)a.dx;
@@ -636,14 +736,34 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const size_t lds = ws ? (size_t)(4 * a.D) * 4 : 0;
   if (lds > 64 * 1024 || a.D % 4) nv = 0;
   const dim3 grid((uint32_t)chunks);
+  auto go = [&](auto nvc, auto fullc, auto hwc) {
+    hipLaunchKernelGGL((ln_bwd_reg<T, decltype(nvc)::value, decltype(fullc)::value, decltype(hwc)::value>), grid, dim3(256),
+                       lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
+  };
+  auto by_w = [&](auto nvc, auto fullc) {
+    if (w) go(nvc, fullc, std::true_type());
+    else go(nvc, fullc, std::false_type());
+  };
+  auto by_full = [&](auto nvc) {
+    if (full_row(decltype(nvc)::value)) by_w(nvc, std::true_type());
+    else by_w(nvc, std::false_type());
+  };
   switch (nv) {
-    case 1: if (full_row(1)) hipLaunchKernelGGL((ln_bwd_reg<T, 1, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 1, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
-    case 2: if (full_row(2)) hipLaunchKernelGGL((ln_bwd_reg<T, 2, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 2, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
-    case 4: if (full_row(4)) hipLaunchKernelGGL((ln_bwd_reg<T, 4, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 4, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
-    case 8: if (full_row(8)) hipLaunchKernelGGL((ln_bwd_reg<T, 8, true>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); else hipLaunchKernelGGL((ln_bwd_reg<T, 8, false>), grid, dim3(256), lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D); break;
+    case 1: by_full(std::integral_constant<int, 1>()); break;
+    case 2: by_full(std::integral_constant<int, 2>()); break;
+    case 4: by_full(std::integral_constant<int, 4>()); break;
+    case 8: by_full(std::integral_constant<int, 8>()); break;
     default: hipLaunchKernelGGL(ln_bwd_row<T>, grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
   }
-  return hrt::launch_ok(hipGetLastError(), ctx, "ln_bwd");
+  if (!hrt::launch_ok(hipGetLastError(), ctx, "ln_bwd")) return false;
+  // dw / db by the column reduction of the partial sums, queued right behind (ln_wgrad's kernel).  A single
+  // launch whose last workgroups wait for the others' partial sums was tried: the waiting workgroups saw
+  // the last chunk's count ~12 us after it was made (device- or system-scope counters alike), 23 us in all.
+  if (wgrad) {
+    static const uint32_t no_grid[3] = {0, 0, 0};
+    return launch_ln_wgrad<T>(&a, no_grid, ctx);
+  }
+  return true;
 }
 
 template <typename T>
@@ -703,8 +823,7 @@ bool ln_bwd_into_scratch(hrt_ln_args a, hrt::LaunchCtx& ctx) {
     ctx.own_hi = base + cap;
     a.ws = base;
   }
-  if (!launch_ln_bwd<T>(&a, no_grid, ctx)) return false;
-  return !wgrad || launch_ln_wgrad<T>(&a, no_grid, ctx);
+  return launch_ln_bwd<T>(&a, no_grid, ctx);  // dx, and dw / db from the partial sums, as one entry point
 }
 
 HRT_REGISTER("softmax_fwd_f32", hrt_softmax_args, launch_softmax_fwd<F32>);

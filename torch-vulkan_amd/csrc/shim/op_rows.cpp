@@ -150,18 +150,15 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> k_layer_norm_backward(
     dx = at::empty_like(x, at::MemoryFormat::Contiguous);
     A.dx = dptr(dx);
   }
-  if (want_dw || want_db) {  // per-chunk column sums of g * xhat and g, reduced by "ln_wgrad_*"
+  if (want_dw || want_db) {  // per-chunk column sums of g * xhat and g, reduced into dw / db by the same call
     partial = at::empty({hrt_ln_chunks(sh->rows), 2, sh->D}, x.options().dtype(at::kFloat));
     A.ws = dptr(partial);
-  }
-  if (A.dx != 0 || A.ws != 0) queue(typed("ln_bwd", x.scalar_type()), A);
-  if (A.ws != 0) {
     if (want_dw) dw = at::empty_like(*weight, at::MemoryFormat::Contiguous);
     if (want_db) db = at::empty_like(*bias, at::MemoryFormat::Contiguous);
     A.dw = want_dw ? dptr(dw) : 0;
     A.db = want_db ? dptr(db) : 0;
-    queue(typed("ln_wgrad", x.scalar_type()), A);
   }
+  if (A.dx != 0 || A.ws != 0) queue(typed("ln_bwd", x.scalar_type()), A);
   note_gpu("aten::native_layer_norm_backward");
   return {dx, dw, db};
 }
