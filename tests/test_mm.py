@@ -294,3 +294,41 @@ def test_wide_split_k_on_large_tiles(m, k, n, ta, tb, dt):
     again = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.5)
     assert torch.equal(out.cpu(), again.cpu())
     no_fallback("aten::addmm")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k", [2, 4, 8, 16, 32])
+@pytest.mark.parametrize("m,n", [(1024, 2048), (37, 520), (5, 8), (300, 6144)])
+@pytest.mark.parametrize("wlayout", ["nk", "kn"])
+def test_short_k_products(dt, k, m, n, wlayout):
+    """K <= 32 (a low-rank adapter's up-projection: y = h B^T with B [N, r], dx = dh A with A [r, K]) runs
+    on the output-bound kernel: both layouts of the small factor, plain, with a row-broadcast bias, and
+    accumulating into the output (y += h B^T), against float64."""
+    h = randn((m, k), dt, m + k)
+    if wlayout == "nk":  # B [N, K] read as its transposed view: k-contiguous
+        w_store = randn((n, k), dt, n + 1, 0.1)
+        w = w_store.t()
+    else:                # A [K, N]: n-contiguous rows
+        w_store = randn((k, n), dt, n + 2, 0.1)
+        w = w_store
+    bias = randn((n,), dt, n + 3)
+    acc0 = randn((m, n), dt, n + 4)
+    hd, wd = h.to(dev), w_store.to(dev)
+    wd = wd.t() if wlayout == "nk" else wd
+    ref = f64(h) @ f64(w)
+    check(hd @ wd, ref, dt, k)
+    check(torch.addmm(bias.to(dev), hd, wd, beta=0.5, alpha=2.0), 0.5 * f64(bias)[None, :] + 2.0 * ref, dt, k)
+    check(torch.addmm(acc0.to(dev), hd, wd), f64(acc0) + ref, dt, k)  # a full [M, N] bias
+    no_fallback("aten::mm", "aten::addmm")
+    # accumulating in place (the bias is the output itself), through the C ABI
+    from torch_vulkan import abi
+    y = acc0.to(dev)
+    a = abi.MmArgs()
+    a.a, a.b, a.c, a.bias = hd.data_ptr(), wd.data_ptr(), y.data_ptr(), y.data_ptr()
+    a.M, a.N, a.K, a.batch = m, n, k, 1
+    a.a_sm, a.a_sk, a.b_sk, a.b_sn, a.c_sm, a.c_sn = hd.stride(0), hd.stride(1), wd.stride(0), wd.stride(1), n, 1
+    a.bias_sm, a.bias_sn, a.has_bias, a.alpha, a.beta = n, 1, 1, 1.0, 1.0
+    abi.Runtime().dispatch("mm_mfma_" + ("bf16" if dt == torch.bfloat16 else "f16"), a)
+    check(y, f64(acc0) + ref, dt, k)
+    if m == 1024 and k == 16:
+        assert torch.equal((hd @ wd).cpu(), (hd @ wd).cpu())  # deterministic

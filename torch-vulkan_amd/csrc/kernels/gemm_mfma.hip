@@ -18,6 +18,7 @@
 #include <type_traits>
 
 #include "../hrt/registry.h"
+#include "gemm_skinny.h"
 #include "lds_stage.h"
 
 namespace hk {
@@ -796,6 +797,8 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int64_t med = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
   const int64_t small = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
   if (small > 0x7fffffffLL) return ctx.fail("GEMM grid too large");
+  // a short reduction (K <= 32, a low-rank adapter's up-projection): bound by the output, not the matrix cores
+  if (!f32out && a.K <= 32 && skinny::queue_expand<T>(a, ctx.stream)) return hrt::launch_ok(hipGetLastError(), ctx, "mm_expand");
   // fast path: the largest tile that still gives enough workgroups.  256 x 256 tiles (two-buffer ring) copy a
   // third fewer bytes per flop than 128 x 256 (the copies, not the MFMAs, bound these kernels once the grid
   // fills the chip) but wait a whole step for each copy: measured 3% faster at K = 2048 (M = 2048, 4096 and
