@@ -411,6 +411,96 @@ class Bench:
                 "flop": flops, "base_gemms_ms": round(tb, 4), "lora_ms": round(t - tb, 4), "timing": how,
                 "launches": len(ops)}
 
+    def dit_block(self):
+        """One DiT block with LoRA through the PyTorch operator API on the vk device, forward + backward, at
+        the production shape of the benchmark stack: 1024 tokens, C = 2048, 16 heads of 128, a 4C tanh-GELU
+        MLP, AdaLN shift / scale / gate from a conditioning vector, LayerNorm without affine parameters, fused
+        attention on [B, T, H, D] projections viewed as [B, H, T, D], rank-16 LoRA on the four linears
+        (frozen base weights, trainable factors and input).  The reference drives such blocks from
+        sd-scripts (tests/anima_on_vk.py:25-102); sd-scripts is absent here, so the block is written out.
+        `ms` is the wall time per step (W warm-up steps, then K steps between synchronisations);
+        `gpu_busy_ms` replays one recorded step (every kernel the step queued, as a HIP graph) and
+        `gpu_busy_frac` = gpu_busy_ms / ms: the share of the step the GPU spends computing rather than
+        waiting for the host.  The replay adds a graph node's launch cost (~1.5 us) to each of the step's
+        `kernels_per_step` kernels, so a value near or above 1 means the step is GPU-bound.  `cpu_fallbacks`
+        lists operators that ran on the CPU during the timed steps."""
+        import torch.nn.functional as F
+
+        torch, rt, args = self.torch, self.rt, self.args
+        bf = torch.bfloat16
+        B, T, C, H, R = 1, 1024, 2048, 16, 16
+        D = C // H
+        P = {"ada_w": self.randn((6 * C, C), bf, 1, 0.02), "ada_b": self.randn((6 * C,), bf, 2, 0.02)}
+        lin = (("qkv", C, 3 * C), ("proj", C, C), ("fc1", C, 4 * C), ("fc2", 4 * C, C))
+        for i, (name, fin, fout) in enumerate(lin):
+            P[name + "_w"], P[name + "_b"] = self.randn((fout, fin), bf, 10 + i, 0.02), self.randn((fout,), bf, 20 + i, 0.02)
+            P[name + "_A"] = self.randn((R, fin), bf, 30 + i, 0.02).requires_grad_(True)
+            P[name + "_B"] = self.randn((fout, R), bf, 40 + i, 0.01).requires_grad_(True)
+        x0, c, g = self.randn((B, T, C), bf, 50), self.randn((B, C), bf, 51), self.randn((B, T, C), bf, 52)
+        trainable = [P[n + s] for n, _, _ in lin for s in ("_A", "_B")]
+
+        def lora(x, n):
+            return F.linear(x, P[n + "_w"], P[n + "_b"]) + F.linear(F.linear(x, P[n + "_A"]), P[n + "_B"])
+
+        def step():
+            for t in trainable:
+                t.grad = None
+            x = x0.detach().requires_grad_(True)
+            s1, sc1, g1, s2, sc2, g2 = F.linear(F.silu(c), P["ada_w"], P["ada_b"]).unsqueeze(1).chunk(6, dim=-1)
+            h = F.layer_norm(x, (C,), eps=1e-6) * (1 + sc1) + s1
+            q, k, v = lora(h, "qkv").view(B, T, 3, H, D).unbind(2)
+            a = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+            y = x + g1 * lora(a.transpose(1, 2).reshape(B, T, C), "proj")
+            h = F.layer_norm(y, (C,), eps=1e-6) * (1 + sc2) + s2
+            out = y + g2 * lora(F.gelu(lora(h, "fc1"), approximate="tanh"), "fc2")
+            out.backward(g)
+
+        for _ in range(max(args.warmup, 3)):
+            step()
+        rt.synchronize()
+        n0 = self.tv.stats()["dispatch_n"]
+        step()
+        rt.synchronize()
+        kernels = int(self.tv.stats()["dispatch_n"] - n0)
+        self.tv.reset_fallback_counts()
+        K = max(args.steps, 10)
+        rt.event_record(4)
+        t0 = time.perf_counter()
+        for _ in range(K):
+            step()
+        rt.event_record(5)
+        rt.synchronize()
+        wall = (time.perf_counter() - t0) / K * 1e3
+        events = rt.elapsed_ms(4, 5) / K
+        fallbacks = self.tv.fallback_counts()
+        # base products (forward and dX; the base weights are frozen) + LoRA products + attention (fwd + bwd)
+        base = sum(2.0 * T * fin * fout for _, fin, fout in lin)
+        flops = 2 * base + sum(2.0 * T * R * (fin + fout) * 3 for _, fin, fout in lin)
+        flops += sum(attn_flops(B, H, T, T, D)) + 2 * (2.0 * B * C * 6 * C)
+        out = {"ms": round(wall, 4), "ms_gpu_events": round(events, 4), "tflops": round(flops / (wall * 1e-3) / 1e12, 2),
+               "flop": flops, "cpu_fallbacks": fallbacks, "steps": K, "kernels_per_step": kernels,
+               "shape": {"tokens": T, "C": C, "heads": H, "head_dim": D, "mlp": 4 * C, "lora_rank": R}}
+        try:
+            gid = rt.graph(step)
+        except RuntimeError as e:  # a step that waits for the GPU (a CPU fallback) cannot be recorded
+            out["gpu_busy_ms"] = out["gpu_busy_frac"] = None
+            out["gpu_busy_note"] = f"the step could not be recorded: {e}"
+            return out
+        try:
+            rt.graph_launch(gid)  # replays only the recorded step, right after recording it
+            rt.synchronize()
+            rt.event_record(6)
+            for _ in range(5):
+                rt.graph_launch(gid)
+            rt.event_record(7)
+            rt.synchronize()
+            busy = rt.elapsed_ms(6, 7) / 5
+        finally:
+            rt.graph_destroy(gid)
+        out["gpu_busy_ms"] = round(busy, 4)
+        out["gpu_busy_frac"] = round(busy / wall, 4)
+        return out
+
     def dq8_linear(self, M):
         torch, abi = self.torch, self.abi
         N, K = 8192, 2048
@@ -935,6 +1025,8 @@ def main():
         line["dq8_linear"] = [bench.dq8_linear(1024), bench.dq8_linear(4096)]
         line["dit_lora_stack"] = bench.dit_lora_stack()
         print(f"[bench] DiT LoRA stack {line['dit_lora_stack']}", file=sys.stderr, flush=True)
+        line["dit_block"] = bench.dit_block()
+        print(f"[bench] DiT block {line['dit_block']}", file=sys.stderr, flush=True)
         line["softmax_f32_16384x1024"] = bench.softmax()
         line["layer_norm_bf16_1024x2048"] = bench.layer_norm()
         line["dequant_int8_8192x2048_bf16"] = bench.dequant()
