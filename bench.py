@@ -326,7 +326,7 @@ class Bench:
 
     def mm_ops(self, A, B, C, bias=None, alpha=1.0, beta=0.0, ws=None):
         """Argument blocks for C = alpha * A @ B + beta * bias on 2-D views (any strides), the way the shim
-        queues them (csrc/shim/ops_mm.cpp: try_gemm): one "mm_mfma_bf16" launch, or, for products too narrow
+        queues them (csrc/shim/op_gemm.cpp: try_product): one "mm_mfma_bf16" launch, or, for products too narrow
         to fill the GPU with 64 x 64 tiles, the split-K pair "mm_mfma_bf16" (fp32 partials into ws) +
         "mm_reduce_bf16" with the shim's split rule."""
         abi = self.abi
@@ -343,7 +343,11 @@ class Bench:
             bsm, bsn = (0, bias.stride(0)) if bias.dim() == 1 else (bias.stride(0), bias.stride(1))
             m.bias, m.bias_sm, m.bias_sn, m.has_bias = bias.data_ptr(), bsm, bsn, 1
         S = 1  # the shim's K-split rule (op_gemm.cpp: k_splits)
-        if K % 64 == 0 and min(M, N) <= 64:
+        if K % 64 == 0 and min(M, N) <= 16:
+            tiles = -(-(M if N <= 16 else N) // 16)
+            while tiles * S < 256 and K % (64 * 2 * S) == 0 and K // (2 * S) >= 256:
+                S *= 2
+        elif K % 64 == 0 and min(M, N) <= 64:
             tiles = -(-M // 64) * -(-N // 64)
             while tiles * S * 2 <= 256 and (K // 64) % (S * 2) == 0 and K // (S * 2) >= 128:
                 S *= 2

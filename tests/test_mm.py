@@ -332,3 +332,53 @@ def test_short_k_products(dt, k, m, n, wlayout):
     check(y, f64(acc0) + ref, dt, k)
     if m == 1024 and k == 16:
         assert torch.equal((hd @ wd).cpu(), (hd @ wd).cpu())  # deterministic
+
+
+NARROW = [(1024, 16, 2048), (37, 3, 40), (2048, 16, 1024), (520, 1, 4096), (64, 12, 104), (136, 16, 4104)]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("p,r,q", NARROW)
+@pytest.mark.parametrize("form", ["x_At", "g_B", "gt_h", "dht_x", "A_xt"])
+def test_narrow_output_products(dt, p, r, q, form):
+    """An output side of at most 16 (a rank-r adapter: h = x A^T, dh = g B, dB = g^T h, dA = dh^T x, and
+    A x^T) runs as one launch that splits the reduction over the wavefronts of a workgroup: every operand
+    layout of those products, ragged P, R and Q (Q not a multiple of the 32-wide step, P not of the
+    16-row tile), addmm's bias x alpha/beta, accumulation in place through the C ABI, and run-to-run
+    identity, against float64."""
+    if form == "x_At":     # X [P, Q] q-contiguous, Y = A^T read along q
+        x, w = randn((p, q), dt, 51), randn((r, q), dt, 52, 0.1)
+        mk = lambda X, W: (X, W.mT)
+    elif form == "g_B":    # Y [Q, R] r-contiguous
+        x, w = randn((p, q), dt, 53), randn((q, r), dt, 54, 0.1)
+        mk = lambda X, W: (X, W)
+    elif form == "gt_h":   # X = g^T p-contiguous
+        x, w = randn((q, p), dt, 55), randn((q, r), dt, 56, 0.1)
+        mk = lambda X, W: (X.mT, W)
+    elif form == "dht_x":  # output [R, P]: M = R
+        w, x = randn((q, r), dt, 57, 0.1), randn((q, p), dt, 58)
+        mk = lambda X, W: (W.mT, X)
+    else:                  # A x^T: output [R, P], both operands k-contiguous
+        w, x = randn((r, q), dt, 59, 0.1), randn((p, q), dt, 60)
+        mk = lambda X, W: (W, X.mT)
+    A64, B64 = mk(f64(x), f64(w))
+    ref = A64 @ B64
+    A, B = mk(x.to(dev), w.to(dev))
+    m, n = ref.shape
+    torch_vulkan.reset_fallback_counts()
+    out = A @ B
+    check(out, ref, dt, q)
+    bias = randn((n,), dt, 61)
+    check(torch.addmm(bias.to(dev), A, B, alpha=0.75, beta=1.25), 1.25 * f64(bias)[None, :] + 0.75 * ref, dt, q)
+    no_fallback("aten::mm", "aten::addmm")
+    assert torch.equal(out.cpu(), (A @ B).cpu())
+    from torch_vulkan import abi
+    acc0 = randn((m, n), dt, 62)
+    y = acc0.to(dev)
+    a = abi.MmArgs()
+    a.a, a.b, a.c, a.bias = A.data_ptr(), B.data_ptr(), y.data_ptr(), y.data_ptr()
+    a.M, a.N, a.K, a.batch = m, n, q, 1
+    a.a_sm, a.a_sk, a.b_sk, a.b_sn, a.c_sm, a.c_sn = A.stride(0), A.stride(1), B.stride(0), B.stride(1), n, 1
+    a.bias_sm, a.bias_sn, a.has_bias, a.alpha, a.beta = n, 1, 1, 1.0, 1.0
+    abi.Runtime().dispatch("mm_mfma_" + ("bf16" if dt == torch.bfloat16 else "f16"), a)
+    check(y, f64(acc0) + ref, dt, q)

@@ -799,6 +799,10 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (small > 0x7fffffffLL) return ctx.fail("GEMM grid too large");
   // a short reduction (K <= 32, a low-rank adapter's up-projection): bound by the output, not the matrix cores
   if (!f32out && a.K <= 32 && skinny::queue_expand<T>(a, ctx.stream)) return hrt::launch_ok(hipGetLastError(), ctx, "mm_expand");
+  // a narrow output (M or N <= 16, a low-rank adapter's down-projection and factor gradients, also the
+  // fp32 slices of such a product split along K)
+  if ((a.M <= 16 || a.N <= 16) && skinny::queue_narrow<T>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_narrow");
   // fast path: the largest tile that still gives enough workgroups.  256 x 256 tiles (two-buffer ring) copy a
   // third fewer bytes per flop than 128 x 256 (the copies, not the MFMAs, bound these kernels once the grid
   // fills the chip) but wait a whole step for each copy: measured 3% faster at K = 2048 (M = 2048, 4096 and

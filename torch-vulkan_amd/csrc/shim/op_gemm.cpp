@@ -116,7 +116,11 @@ std::optional<Plan> plan(const at::Tensor& a, const at::Tensor& b, const at::Ten
 
 // K-split factor of a matrix-core product (1 = no split; unbatched products only, the slices use the batch
 // dimension; K in whole 64-element steps):
-//  * narrow products, one 64-wide output tile across (min(M, N) <= 64: rank-16 LoRA factors): S doubles
+//  * products with an output side of at most 16 (a rank-16 LoRA's x A^T, g B, g^T h, dh^T x) run on the
+//    narrow-output kernel, one workgroup per 16 rows of the long side P, K split across its wavefronts: S
+//    doubles while the P / 16 workgroups times S stay under 256 and every slice keeps >= 256 of K (1024
+//    rows and K = 2048: S = 4, 256 workgroups; 6144 rows: no split);
+//  * other narrow products, one 64-wide output tile across (min(M, N) <= 64: rank-16 LoRA factors): S doubles
 //    while the grid of 64 x 64 tiles stays within one workgroup per CU (256) and every slice keeps >= 128
 //    of K;
 //  * wide products whose 128 x 256 (or 256 x 128) tiles alone give fewer than 192 workgroups (1024 x 2048
@@ -129,6 +133,11 @@ std::optional<Plan> plan(const at::Tensor& a, const at::Tensor& b, const at::Ten
 int64_t k_splits(const Plan& p) {
   if (p.batched || p.K % 64 != 0) return 1;
   int64_t s = 1;
+  if (std::min(p.M, p.N) <= 16) {
+    const int64_t tiles = ((p.N <= 16 ? p.M : p.N) + 15) / 16;
+    while (tiles * s < 256 && p.K % (64 * 2 * s) == 0 && p.K / (2 * s) >= 256) s *= 2;
+    return s;
+  }
   if (std::min(p.M, p.N) <= 64) {
     const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64), steps = p.K / 64;
     while (tiles * (2 * s) <= 256 && steps % (2 * s) == 0 && p.K / (2 * s) >= 128) s *= 2;
