@@ -345,7 +345,7 @@ class Bench:
         S = 1  # the shim's K-split rule (op_gemm.cpp: k_splits)
         if K % 64 == 0 and min(M, N) <= 16:
             tiles = -(-(M if N <= 16 else N) // 16)
-            while tiles * S < 256 and K % (64 * 2 * S) == 0 and K // (2 * S) >= 256:
+            while tiles * S < 256 and K % (64 * 2 * S) == 0 and K // (2 * S) >= 1536:
                 S *= 2
         elif K % 64 == 0 and min(M, N) <= 64:
             tiles = -(-M // 64) * -(-N // 64)

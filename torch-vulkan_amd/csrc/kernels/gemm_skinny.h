@@ -11,6 +11,7 @@
 
 #include <type_traits>
 
+#include "lds_stage.h"
 #include "mfma_common.h"
 
 namespace hk {
@@ -57,22 +58,41 @@ __device__ __forceinline__ void unpack8(u32x4 w, float* v) {
 
 // C[m, n] = alpha * sum_k A[m, k] B[k, n] + beta * X[m, n], X = the bias view (which may be C itself: an
 // accumulating product) or nothing.  KP = K / 2 pairs.  BT: B is k-contiguous (B[k, n] at b + n*b_sn + k,
-// the transposed view of an [N, K] weight); else n-contiguous rows.  Workgroup = one wavefront: 512 columns
-// (8 per lane) of RB rows.  Every load of the workgroup is issued before the first use (one round trip to
-// memory): the lane's 8 columns of B, its 8 columns of the RB rows of X, and the RB x K block of A spread
-// over the lanes (lane l holds pair l of the block), from which each row's pairs go to scalar registers.
-constexpr int kExpandRows = 8;
+// the transposed view of an [N, K] weight); else n-contiguous rows.  Workgroup = four wavefronts over the
+// same 512 columns (8 per lane), RB rows each.  Every load of a wavefront is issued before the first use
+// (one round trip to memory): its lane's 8 columns of B, its 8 columns of the RB rows of X, and the RB x K
+// block of A spread over the lanes (lane l holds pair l of the block), from which each row's pairs go to
+// scalar registers.  B laid out along k (K a multiple of 8) is read once per workgroup in coalesced 16-byte
+// chunks and handed to the lanes through LDS (a lane's 8 columns are 16 K contiguous bytes: read per lane,
+// each 16-byte load would touch 64 cache lines); the chunks of a lane's row are XOR-swizzled so that the
+// lanes' 128-bit reads of one chunk index fall on distinct banks.
+constexpr int kExpandRows = 8, kExpandWaves = 4;
 template <typename T, int KP, bool BT, bool HASX>
-__global__ __launch_bounds__(64) void mm_expand(hrt_mm_args a) {
+__global__ __launch_bounds__(kExpandWaves * 64) void mm_expand(hrt_mm_args a) {
   using S = uint16_t;
-  constexpr int RB = kExpandRows, HV = (RB * KP + 63) / 64;
-  const int lane = threadIdx.x;
-  const int64_t n0 = (int64_t)blockIdx.x * 512 + lane * 8;
+  constexpr int RB = kExpandRows, HV = (RB * KP + 63) / 64, K = 2 * KP;
+  constexpr bool SHARED = BT && K % 8 == 0;   // B through LDS
+  constexpr int CPC = K / 8, CPR = K;         // 16-byte chunks per column / per lane's 8 columns
+  constexpr int CPT = SHARED ? 64 * CPR / (kExpandWaves * 64) : 1;  // chunks loaded per thread
+  __shared__ __attribute__((aligned(16))) u32x4 fl[SHARED ? 64 * CPR : 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t nb0 = (int64_t)blockIdx.x * 512, n0 = nb0 + lane * 8;
   const bool live_n = n0 < a.N;
   const int64_t nl = live_n ? n0 : a.N - 8;  // lanes past the end work on the last 8 columns, store nothing
-  const int64_t m0 = (int64_t)blockIdx.y * RB;
+  const int64_t m0 = ((int64_t)blockIdx.y * kExpandWaves + wave) * RB;
   const HK_G S* A = gcptr<S>(a.a);
   const HK_G S* B = gcptr<S>(a.b);
+  uint32_t bw[8][KP];  // bw[c][j] = (B[2j, n+c], B[2j+1, n+c])
+  u32x4 fc[CPT];
+  if constexpr (SHARED) {  // chunk t of the block: column t / CPC, k = 8 (t % CPC) .. +7
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int t = tid + kExpandWaves * 64 * i;
+      const int64_t n = nb0 + t / CPC < a.N ? nb0 + t / CPC : a.N - 1;
+      fc[i] = *reinterpret_cast<const HK_G u32x4*>(B + n * a.b_sn + 8 * (t % CPC));
+    }
+    issue_order_fence();
+  }
   // the A block: pair p = lane + 64 i is (row p / KP, pair p % KP); rows past the end repeat the last row
   uint32_t hblk[HV];
 #pragma unroll
@@ -90,8 +110,21 @@ __global__ __launch_bounds__(64) void mm_expand(hrt_mm_args a) {
       xv[r] = *reinterpret_cast<const HK_G u32x4*>(X + m * a.bias_sm + nl);
     }
   }
-  uint32_t bw[8][KP];  // bw[c][j] = (B[2j, n+c], B[2j+1, n+c])
-  if constexpr (BT) {
+  if constexpr (SHARED) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int t = tid + kExpandWaves * 64 * i;
+      const int c = t / CPC, L = c / 8, sl = (c % 8) * CPC + t % CPC;
+      fl[L * CPR + (sl ^ (L & (CPR - 1)))] = fc[i];
+    }
+    barrier_keep_vm_lds<HV + (HASX ? RB : 0)>();  // the chunks are in LDS; the row loads stay in flight
+#pragma unroll
+    for (int sl = 0; sl < CPR; ++sl) {
+      const u32x4 v = fl[lane * CPR + (sl ^ (lane & (CPR - 1)))];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bw[sl / CPC][4 * (sl % CPC) + e] = v[e];
+    }
+  } else if constexpr (BT) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const HK_G uint32_t* col = reinterpret_cast<const HK_G uint32_t*>(B + (nl + c) * a.b_sn);
@@ -144,17 +177,18 @@ bool queue_expand(const hrt_mm_args& a, hipStream_t s) {
   if (K < 2 || K > 32 || K % 2 || a.batch != 1 || a.M <= 0 || a.N < 8 || a.N % 8) return false;
   if (a.c % 16 || a.c_sn != 1 || a.c_sm % 8) return false;
   if (a.a % 4 || a.a_sk != 1 || a.a_sm % 2) return false;
-  const bool bt = a.b_sk == 1 && a.b_sn % 2 == 0 && a.b % 4 == 0;
+  // k-contiguous B: 4-byte pairs per column; with K a multiple of 8 the 16-byte chunks read through LDS
+  const bool bt = a.b_sk == 1 && a.b_sn % 2 == 0 && a.b % 4 == 0 && (K % 8 != 0 || (a.b_sn % 8 == 0 && a.b % 16 == 0));
   const bool bn = a.b_sn == 1 && a.b_sk % 8 == 0 && a.b % 16 == 0;
   if (!bt && !bn) return false;
   const bool hasx = a.has_bias && a.beta != 0.f;
   if (hasx && (a.bias % 16 || a.bias_sn != 1 || (a.bias_sm != 0 && a.bias_sm % 8))) return false;
   if (a.M > 0x7fffffffLL || a.N > 0x7fffffffLL) return false;
-  const int64_t nb = (a.N + 511) / 512, mb = (a.M + kExpandRows - 1) / kExpandRows;
+  const int64_t nb = (a.N + 511) / 512, mb = (a.M + kExpandRows * kExpandWaves - 1) / (kExpandRows * kExpandWaves);
   if (mb > 65535) return false;
   const dim3 grid((uint32_t)nb, (uint32_t)mb);
   auto go = [&](auto kp, auto btc, auto hxc) {
-    hipLaunchKernelGGL((mm_expand<T, decltype(kp)::value, decltype(btc)::value, decltype(hxc)::value>), grid, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((mm_expand<T, decltype(kp)::value, decltype(btc)::value, decltype(hxc)::value>), grid, dim3(kExpandWaves * 64), 0, s, a);
   };
   auto by_x = [&](auto kp, auto btc) {
     if (hasx) go(kp, btc, std::true_type());

@@ -118,8 +118,9 @@ std::optional<Plan> plan(const at::Tensor& a, const at::Tensor& b, const at::Ten
 // dimension; K in whole 64-element steps):
 //  * products with an output side of at most 16 (a rank-16 LoRA's x A^T, g B, g^T h, dh^T x) run on the
 //    narrow-output kernel, one workgroup per 16 rows of the long side P, K split across its wavefronts: S
-//    doubles while the P / 16 workgroups times S stay under 256 and every slice keeps >= 256 of K (1024
-//    rows and K = 2048: S = 4, 256 workgroups; 6144 rows: no split);
+//    doubles while the P / 16 workgroups times S stay under 256 and every slice keeps >= 1536 of K.  Only
+//    long reductions over few rows repay the second launch: measured at 1024 rows, K = 8192 takes 9.1 us
+//    at S = 4 against 16.3 unsplit, K = 6144 8.2 against 9.0, but K = 2048 5.8 unsplit against 6.7-7.5.
 //  * other narrow products, one 64-wide output tile across (min(M, N) <= 64: rank-16 LoRA factors): S doubles
 //    while the grid of 64 x 64 tiles stays within one workgroup per CU (256) and every slice keeps >= 128
 //    of K;
@@ -135,7 +136,7 @@ int64_t k_splits(const Plan& p) {
   int64_t s = 1;
   if (std::min(p.M, p.N) <= 16) {
     const int64_t tiles = ((p.N <= 16 ? p.M : p.N) + 15) / 16;
-    while (tiles * s < 256 && p.K % (64 * 2 * s) == 0 && p.K / (2 * s) >= 256) s *= 2;
+    while (tiles * s < 256 && p.K % (64 * 2 * s) == 0 && p.K / (2 * s) >= 1536) s *= 2;
     return s;
   }
   if (std::min(p.M, p.N) <= 64) {
