@@ -99,7 +99,6 @@ def test_baseline_m4096(M):
     q, s = weights(8192, 2048, 21)
     x = randn((M, 2048), torch.bfloat16, 7)
     y = torch_vulkan.dequant_int8_linear(x.to(dev), q.to(dev), s.to(dev))
-    rows = slice(0, 512)  # output rows are independent: a slice against the oracle
-    ref = oracle.gemm(f64(x[rows]), deq64(q, s).T)
-    check(y[rows], ref, 2048)
-    assert torch.isfinite(y.float().cpu()).all()
+    ref = oracle.gemm(f64(x), deq64(q, s).T)  # all 4096 rows (a float64 GEMM of ~2 s)
+    check(y, ref, 2048)
+    assert oracle.rel_l2(f64(y), ref) <= 1e-2
