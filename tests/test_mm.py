@@ -382,3 +382,32 @@ def test_narrow_output_products(dt, p, r, q, form):
     a.bias_sm, a.bias_sn, a.has_bias, a.alpha, a.beta = n, 1, 1, 1.0, 1.0
     abi.Runtime().dispatch("mm_mfma_" + ("bf16" if dt == torch.bfloat16 else "f16"), a)
     check(y, f64(acc0) + ref, dt, q)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4, 7])
+@pytest.mark.parametrize("bias_kind", [None, "row", "full"])
+def test_split_k_reduction_paths_agree(splits, bias_kind):
+    """mm_reduce's vector path (8 outputs of a row per thread, C rows contiguous) and its general path (any
+    output strides) add the slices in the same order: bit-identical bf16 results, checked against float64."""
+    from torch_vulkan import abi
+    M, N = 96, 136
+    g = torch.Generator().manual_seed(splits)
+    ws = torch.randn((splits, M, N), generator=g).to(dev)
+    bias = None if bias_kind is None else randn((N,) if bias_kind == "row" else (M, N), torch.bfloat16, 70 + splits).to(dev)
+    c_vec = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    c_gen_store = torch.empty((M, 2 * N), dtype=torch.bfloat16, device=dev)
+    c_gen = c_gen_store[:, ::2]  # column stride 2: the general path
+    for c in (c_vec, c_gen):
+        r = abi.MmReduceArgs()
+        r.ws, r.c = ws.data_ptr(), c.data_ptr()
+        r.M, r.N, r.splits, r.c_sm, r.c_sn = M, N, splits, c.stride(0), c.stride(1)
+        r.alpha, r.beta = 0.5, 1.5
+        if bias is not None:
+            r.bias, r.has_bias = bias.data_ptr(), 1
+            r.bias_sm, r.bias_sn = (0, 1) if bias.dim() == 1 else (bias.stride(0), 1)
+        abi.Runtime().dispatch("mm_reduce_bf16", r)
+    assert torch.equal(c_vec.cpu(), c_gen.cpu())
+    ref = 0.5 * ws.double().cpu().sum(0).numpy()
+    if bias is not None:
+        ref = ref + 1.5 * f64(bias)
+    check(c_vec, ref, torch.bfloat16, splits)

@@ -969,6 +969,45 @@ __global__ __launch_bounds__(256) void mm_reduce(hrt_mm_reduce_args p) {
   }
 }
 
+// Vector form of mm_reduce for the common layout (N % 8 == 0, C rows contiguous and 16-byte aligned, the bias
+// absent or with contiguous rows): a thread takes 8 consecutive outputs of one row (one division for the
+// row), loads exactly the S slices' two 16-byte pieces (four slices' loads in flight at a time), adds them in
+// slice order 0, 1, ... exactly as mm_reduce does (bit-identical results) and writes one 16-byte store.
+template <typename T>
+__global__ __launch_bounds__(256) void mm_reduce_vec(hrt_mm_reduce_args p, int64_t nvec) {
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= nvec) return;
+  const int64_t i0 = v * 8, total = p.M * p.N;
+  const int64_t m = i0 / p.N, n = i0 - m * p.N;
+  const HK_G f32x4* w = gcptr<f32x4>(p.ws) + i0 / 4;
+  const int64_t st = total / 4;  // 16-byte pieces per slice
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  int64_t k = 0;
+  for (; k + 4 <= p.splits; k += 4) {
+    f32x4 a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = w[(k + u) * st], b[u] = w[(k + u) * st + 1];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s0 += a[u], s1 += b[u];
+  }
+  for (; k < p.splits; ++k) s0 += w[k * st], s1 += w[k * st + 1];
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = p.alpha * s0[e], o[4 + e] = p.alpha * s1[e];
+  if (p.has_bias) {
+    const u32x4 bb = *reinterpret_cast<const HK_G u32x4*>(gcptr<uint16_t>(p.bias) + m * p.bias_sm + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[2 * e] += p.beta * T::to_f32((uint16_t)(bb[e] & 0xffffu));
+      o[2 * e + 1] += p.beta * T::to_f32((uint16_t)(bb[e] >> 16));
+    }
+  }
+  u32x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = (uint32_t)T::from_f32(o[2 * e]) | ((uint32_t)T::from_f32(o[2 * e + 1]) << 16);
+  *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(p.c) + m * p.c_sm + n) = r;
+}
+
 template <typename T>
 bool launch_mm_reduce(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_mm_reduce_args*>(pp);
@@ -981,7 +1020,14 @@ bool launch_mm_reduce(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!ctx.check(a.ws, hrt::span_bytes(3, sw, tw, 4), "ws") || !ctx.check(a.c, hrt::span_bytes(2, sc, tc, 2), "c") ||
       (a.has_bias && !ctx.check(a.bias, hrt::span_bytes(2, sc, tb, 2), "bias")))
     return false;
-  hipLaunchKernelGGL(mm_reduce<T>, dim3((uint32_t)cdiv(total, 1024)), dim3(256), 0, ctx.stream, a);
+  const bool vec = a.N % 8 == 0 && a.c_sn == 1 && a.c % 16 == 0 && a.c_sm % 8 == 0 && a.ws % 16 == 0 &&
+                   (!a.has_bias || (a.bias_sn == 1 && a.bias % 16 == 0 && a.bias_sm % 8 == 0));
+  if (vec) {
+    const int64_t nvec = total / 8;
+    hipLaunchKernelGGL(mm_reduce_vec<T>, dim3((uint32_t)cdiv(nvec, 256)), dim3(256), 0, ctx.stream, a, nvec);
+  } else {
+    hipLaunchKernelGGL(mm_reduce<T>, dim3((uint32_t)cdiv(total, 1024)), dim3(256), 0, ctx.stream, a);
+  }
   return hrt::launch_ok(hipGetLastError(), ctx, "mm_reduce");
 }
 
