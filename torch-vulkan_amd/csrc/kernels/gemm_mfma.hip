@@ -725,11 +725,14 @@ bool mm_dma_ok(const hrt_mm_args& a, int BM, int BN, bool& atr, bool& btr) {
 // xbm x bn (xbm | tm, bn | tn, eight blocks) with the fewest panel bytes per XCD, xbm * a_panel +
 // bn * b_panel (a_panel / b_panel: bytes of one BM-row A panel / BN-row B panel over K); 0 (n-fastest
 // order) when the grid does not split into eight such blocks, there is more than one product, or K < 2048.
-// Measured: 1024 x 2048 x 2048 on 64 x 64 tiles 15.4-16.1 us against 16.6-18.1 n-fastest (41.9 -> 33.6 MB
-// of panels read), 4096 x 2048 x 8192 1.5% faster; but 1024^3 6.65 against 6.45 us although it reads
-// 12.6 instead of 18.9 MB, so short reductions keep the n-fastest order.
+// The block order is used only where it reads at least 10% fewer panel bytes than the n-fastest order (which,
+// with tn a multiple of 8, gives each XCD tn / 8 B panels and every A panel): where the two read the same,
+// as at 1024 x 2048 x 8192 on 128 x 256 tiles, the block order measured ~1.5% slower.  Measured:
+// 1024 x 2048 x 2048 on 64 x 64 tiles 15.4-16.1 us against 16.6-18.1 n-fastest (41.9 -> 33.6 MB of panels
+// read), 4096 x 2048 x 8192 1.5% faster; but 1024^3 6.65 against 6.45 us although it reads 12.6 instead of
+// 18.9 MB, so short reductions keep the n-fastest order.
 int xcd_block_rows(int64_t tm, int64_t tn, int64_t batch, int64_t K, double a_panel, double b_panel) {
-  if (batch != 1 || K < 2048 || (tm * tn) % 8 != 0) return 0;
+  if (batch != 1 || K < 2048 || tn % 8 != 0) return 0;
   const int64_t per = tm * tn / 8;
   int best = 0;
   double cost = 0.0;
@@ -740,7 +743,8 @@ int xcd_block_rows(int64_t tm, int64_t tn, int64_t batch, int64_t K, double a_pa
     const double c = bm * a_panel + bn * b_panel;
     if (best == 0 || c < cost) best = (int)bm, cost = c;
   }
-  return best;
+  const double n_fastest = tm * a_panel + (tn / 8) * b_panel;
+  return best > 0 && cost <= 0.9 * n_fastest ? best : 0;
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int RING = 3, bool F32OUT = false>
