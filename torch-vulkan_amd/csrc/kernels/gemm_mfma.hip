@@ -843,8 +843,15 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   // fast path: the largest tile that still gives enough workgroups.  256 x 256 tiles (two-buffer ring) copy a
   // third fewer bytes per flop than 128 x 256 (the copies, not the MFMAs, bound these kernels once the grid
   // fills the chip) but wait a whole step for each copy: measured 3% faster at K = 2048 (M = 2048, 4096 and
-  // N = 8192), 5% slower at 8192^3
-  if (!f32out && a.K <= 4096 && a.batch * (a.M / 256) * (a.N / 256) >= 256 &&
+  // N = 8192), 5% slower at 8192^3.  Both run one workgroup per CU, so a grid runs in rounds of 256 tiles;
+  // 256 x 256 is taken only when its rounds are as full as those of the 128 x 256 / 256 x 128 tiling (the
+  // convolution's input-gradient product 4608 x 4096 x 512: 288 tiles fill 56% of two rounds, 576 half-size
+  // tiles 75% of three, measured 41.9 against 36.2-37.2 us).
+  auto round_fill = [](int64_t t) { return t > 0 ? (double)t / (double)(((t + 255) / 256) * 256) : 0.0; };
+  const int64_t t256 = a.M % 256 == 0 && a.N % 256 == 0 ? a.batch * (a.M / 256) * (a.N / 256) : 0;
+  const int64_t t_wide = a.M % 128 == 0 && a.N % 256 == 0 ? a.batch * (a.M / 128) * (a.N / 256) : 0;
+  const int64_t t_tall = a.M % 256 == 0 && a.N % 128 == 0 ? a.batch * (a.M / 256) * (a.N / 128) : 0;
+  if (!f32out && a.K <= 4096 && t256 >= 256 && round_fill(t256) >= round_fill(std::max(t_wide, t_tall)) &&
       queue_dma<T, 256, 256, 64, 128, 2>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (!f32out && a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256, 64, 64>(a, ctx.stream))
