@@ -411,3 +411,22 @@ def test_split_k_reduction_paths_agree(splits, bias_kind):
     if bias is not None:
         ref = ref + 1.5 * f64(bias)
     check(c_vec, ref, torch.bfloat16, splits)
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [True, False])
+@pytest.mark.parametrize("m,k,n", [(1024, 256, 6144), (2048, 128, 3072)])
+def test_tiles_128x192(m, k, n, ta, tb):
+    """Products whose N is a multiple of 192 and whose 128 x 192 tiles fill the GPU's rounds better than
+    128 x 256 ones (a DiT block's QKV projection x W^T, N = 6144) take the 128 x 192 tile kernel when B is laid
+    out along K (tb: B given as the transposed view of an [N, K] weight), either A layout; B laid out along N
+    keeps the 128 x 256 tiles.  Against the oracle, with addmm's bias."""
+    a = randn((k, m) if ta else (m, k), torch.bfloat16, 81)
+    b = randn((n, k) if tb else (k, n), torch.bfloat16, 82, 0.1)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), torch.bfloat16, 83)
+    out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.0)
+    check(out, ref, torch.bfloat16, k)
+    assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
