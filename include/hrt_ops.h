@@ -321,6 +321,31 @@ typedef struct hrt_im2col_args {
   int64_t N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW;
 } hrt_im2col_args;
 
+/* "conv3x3_wprep_{bf16,f16}" and "conv3x3_{bf16,f16}" — a direct 3x3 convolution (stride 1, zero padding 1,
+ * no dilation, one group) without the column matrix: an implicit GEMM that stages each 16-channel block of
+ * three input rows once and applies the nine taps from it.  No counterpart in the reference, whose
+ * convolution is im2col + GEMM (csrc/ops_conv.cpp:89-140); the result is the same convolution in fp32
+ * accumulation with one rounding (the reduction order differs from im2col + GEMM).
+ *  "conv3x3_wprep_{dt}": wr[o, cb, t, i] = w[o, 16 cb + i, t] for the forward (flip = 0, w: [O, I, 3, 3],
+ *                        O = Co, I = C), or, for the input gradient (flip = 1), wr[c, cb, t, i] =
+ *                        w[16 cb + i, c, 8 - t] with w: [I, O, 3, 3] read as the flipped transpose (O = C,
+ *                        I = Co).  wr: [O, I / 16, 9, 16] contiguous, I a multiple of 16.
+ *  "conv3x3_{dt}":       y[n, o, h, w] = sum_{i, kh, kw} wr[o, i / 16, 3 kh + kw, i % 16] *
+ *                        x[n, i, h + kh - 1, w + kw - 1] (0 outside x) + bias[o] when has_bias; x: [N, I, H,
+ *                        W], y: [N, O, H, W], both contiguous; I a multiple of 16, O of 128, W of 64.  The
+ *                        forward is (x, wprep(w, 0)); the input gradient of y = conv(x, w) is
+ *                        (dy, wprep(w, 1)) with I = Co, O = C. */
+typedef struct hrt_conv3_wprep_args {
+  uint64_t w, wr;
+  int64_t O, I;
+  uint32_t flip, pad;
+} hrt_conv3_wprep_args;
+typedef struct hrt_conv3_args {
+  uint64_t x, wr, bias, y;
+  int64_t N, I, O, H, W;
+  uint32_t has_bias, pad;
+} hrt_conv3_args;
+
 /* "upsample_nearest_fwd_{dt}" / "upsample_nearest_bwd_{dt}" — nearest-neighbour upsampling of [NC, H, W]
  * by the integer factors OH / H and OW / W (src index = dst index / factor) and its backward, dst [NC, H, W]
  * = the sum of each factor block of src [NC, OH, OW] (fp32, fixed order).  Contiguous.  Replaces "up_fwd" /

@@ -67,6 +67,7 @@ KERNELS = (
     + [f"attn_delta_{k}" for k in ("f32", "bf16", "f16")]
     + [f"mm_dq8_{k}" for k in ("bf16", "f16")]
     + [f"mm_reduce_{k}" for k in ("bf16", "f16")]
+    + [f"conv3x3_{k}" for k in ("bf16", "f16")] + [f"conv3x3_wprep_{k}" for k in ("bf16", "f16")]
 )
 
 
@@ -123,7 +124,7 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
     structs = {
         "hrt_add_f32_args": abi.AddF32Args, "hrt_copy_args": abi.CopyArgs, "hrt_fill_args": abi.FillArgs, "hrt_ew_args": abi.EwArgs, "hrt_reduce_args": abi.ReduceArgs,
         "hrt_cat_args": abi.CatArgs,
-        "hrt_im2col_args": abi.Im2colArgs, "hrt_upsample_args": abi.UpsampleArgs, "hrt_gn_args": abi.GnArgs,
+        "hrt_im2col_args": abi.Im2colArgs, "hrt_conv3_wprep_args": abi.Conv3WprepArgs, "hrt_conv3_args": abi.Conv3Args, "hrt_upsample_args": abi.UpsampleArgs, "hrt_gn_args": abi.GnArgs,
         "hrt_mm_args": abi.MmArgs, "hrt_mm_dq8_args": abi.MmDq8Args, "hrt_mm_reduce_args": abi.MmReduceArgs,
         "hrt_attn_args": abi.AttnArgs,
         "hrt_softmax_args": abi.SoftmaxArgs, "hrt_ln_args": abi.LnArgs, "hrt_dq8_args": abi.Dq8Args,

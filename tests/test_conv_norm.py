@@ -95,6 +95,76 @@ def test_conv_forward_and_input_grad(dt, case, bias):
     assert torch_vulkan.kernel_counts().get("aten::convolution_overrideable", 0) >= 1
 
 
+DIRECT = [  # (N, C, H, W, Co): shapes of the direct 3x3 kernel (stride 1, pad 1, C % 16, Co % 128, W % 64)
+    (1, 16, 1, 64, 128),
+    (2, 32, 3, 128, 256),
+    (1, 48, 5, 64, 128),
+    (1, 128, 16, 64, 128),
+    (1, 512, 64, 64, 512),
+]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", DIRECT)
+@pytest.mark.parametrize("bias", [True, False])
+def test_conv3x3_direct_forward_and_input_grad(dt, case, bias, monkeypatch):
+    """3x3 / stride 1 / padding 1 convolutions that the direct kernel (conv3x3: an implicit GEMM over staged
+    input rows, no column matrix) takes: forward with and without bias, and the input gradient (the same
+    kernel on the output gradient with the flipped, transposed kernel when C % 128 == 0), against the oracle;
+    1- and 3-row images exercise the zero rows above and below, 128-pixel rows two segments per row."""
+    monkeypatch.setenv("VKT_CONV_DIRECT", "1")  # the direct kernel is opt-in
+    N, C, H, W, Co = case
+    x = rnd((N, C, H, W), dt, 11)
+    w = rnd((Co, C, 3, 3), dt, 12, scale=0.3)
+    b = rnd((Co,), dt, 13) if bias else None
+    r = rnd((N, Co, H, W), torch.float32, 14)
+    ref = oracle.conv2d(f64(x), f64(w), f64(b) if bias else None, (1, 1), (1, 1))
+    xd = x.to(dev).requires_grad_(True)
+    out = F.conv2d(xd, w.to(dev), b.to(dev) if bias else None, padding=1)
+    rel_close(out, ref, dt, "forward")
+    if C * H * W <= 128 * 16 * 64:  # the oracle's backward is slow at the full size
+        gref, _, _ = oracle.conv2d_backward(f64(x), f64(w), f64(r.to(dt)), (1, 1), (1, 1))
+        (out * r.to(dt).to(dev)).sum().backward()
+        rel_close(xd.grad, gref, dt, "grad_input")
+    no_fallback("aten::convolution_overrideable", "aten::convolution_backward_overrideable")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("flip", [0, 1])
+def test_conv3x3_c_abi(dt, flip):
+    """The two entry points called directly: conv3x3_wprep reorders [O, I, 3, 3] (flip 0) or reads
+    [I, O, 3, 3] as its flipped transpose (flip 1), and conv3x3 then gives the convolution (flip 0) or the
+    input gradient of the convolution with w (flip 1), against the oracle; the argument checks reject
+    channel counts the kernel does not take."""
+    N, H, W, c_small, c_big = 2, 3, 128, 32, 128
+    name = "bf16" if dt == torch.bfloat16 else "f16"
+    rt = abi.Runtime()
+    if flip == 0:  # x [N, 32, H, W], w [128, 32, 3, 3] -> y [N, 128, H, W]
+        xin = rnd((N, c_small, H, W), dt, 21)
+        w = rnd((c_big, c_small, 3, 3), dt, 22, scale=0.3)
+        ref = oracle.conv2d(f64(xin), f64(w), None, (1, 1), (1, 1))
+        I, O = c_small, c_big
+    else:  # the input gradient of conv(x [N, 128, H, W], w [32, 128, 3, 3]): dy [N, 32, H, W] -> dx [N, 128, H, W]
+        xin = rnd((N, c_small, H, W), dt, 23)
+        w = rnd((c_small, c_big, 3, 3), dt, 24, scale=0.3)
+        ref, _, _ = oracle.conv2d_backward(np.zeros((N, c_big, H, W)), f64(w), f64(xin), (1, 1), (1, 1))
+        I, O = c_small, c_big
+    xd, wd = xin.to(dev), w.to(dev)
+    wr = torch.empty((O, I // 16, 9, 16), dtype=dt, device=dev)
+    y = torch.empty((N, O, H, W), dtype=dt, device=dev)
+    P = abi.Conv3WprepArgs()
+    P.w, P.wr, P.O, P.I, P.flip = wd.data_ptr(), wr.data_ptr(), O, I, flip
+    rt.dispatch("conv3x3_wprep_" + name, P)
+    A = abi.Conv3Args()
+    A.x, A.wr, A.y, A.N, A.I, A.O, A.H, A.W = xd.data_ptr(), wr.data_ptr(), y.data_ptr(), N, I, O, H, W
+    rt.dispatch("conv3x3_" + name, A)
+    rel_close(y, ref, dt, f"conv3x3 flip {flip}")
+    bad = abi.Conv3Args.from_buffer_copy(A)
+    bad.O = 64  # not a multiple of 128
+    with pytest.raises(RuntimeError):
+        rt.dispatch("conv3x3_" + name, bad)
+
+
 @pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("case", [CASES[2], CASES[6], CASES[0], CASES[3], CASES[1]])
 def test_conv_weight_and_bias_grad(dt, case):

@@ -38,6 +38,7 @@ HRT_SOURCES = [
     "kernels/ew_map.hip",
     "kernels/reduce.hip",
     "kernels/conv_norm.hip",
+    "kernels/conv3x3.hip",
     "kernels/dq8.hip",
     "kernels/gemm.hip",
     "kernels/gemm_mfma.hip",

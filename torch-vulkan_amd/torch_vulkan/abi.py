@@ -66,6 +66,15 @@ class Im2colArgs(ctypes.Structure):
     _fields_ = [("x", u64), ("cols", u64)] + [(n, i64) for n in ("N", "C", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW", "PH", "PW")]
 
 
+class Conv3WprepArgs(ctypes.Structure):
+    _fields_ = [("w", u64), ("wr", u64), ("O", i64), ("I", i64), ("flip", u32), ("pad", u32)]
+
+
+class Conv3Args(ctypes.Structure):
+    _fields_ = [("x", u64), ("wr", u64), ("bias", u64), ("y", u64), ("N", i64), ("I", i64), ("O", i64), ("H", i64),
+                ("W", i64), ("has_bias", u32), ("pad", u32)]
+
+
 class UpsampleArgs(ctypes.Structure):
     _fields_ = [("src", u64), ("dst", u64), ("NC", i64), ("H", i64), ("W", i64), ("OH", i64), ("OW", i64)]
 
