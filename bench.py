@@ -594,7 +594,7 @@ class Bench:
 
     def dequant(self):
         torch, abi = self.torch, self.abi
-        R, C, sets = 8192, 2048, 12
+        R, C, sets = 8192, 2048, 24
         qs, ss, outs = [], [], []
         for i in range(sets):
             g = torch.Generator().manual_seed(i)

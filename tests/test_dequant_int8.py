@@ -67,6 +67,28 @@ def test_dequant_extreme_values_and_zero_scale():
         assert np.array_equal(bits(torch_vulkan.dequant_int8(q.to(dev), scale.to(dev), dt)), expect(q, scale, kind))
 
 
+@pytest.mark.parametrize("cols", [2048, 64, 1040])
+def test_dequant_nonfinite_subnormal_and_overflowing_scales(cols):
+    """Scales of +-inf, NaN, bf16 subnormals and values whose product with an int8 overflows to inf, each
+    on its own 64-column block: the bf16 output rounds every non-NaN product to nearest even (subnormals
+    included, never flushed), gives 0x7FC0 for every NaN (0 * inf, NaN * q) and keeps +-inf; f16 / f32 as
+    the oracle.  2048 columns take the row-per-wavefront path of the 16-bit kernel, 64 and 1040 the
+    per-lane one."""
+    rows, nb = 6, (cols + 63) // 64
+    g = torch.Generator().manual_seed(cols)
+    q = torch.randint(-128, 128, (rows, cols), generator=g, dtype=torch.int8)
+    q[:, ::7] = 0  # zero times inf is NaN
+    special = np.array([0x7F80, 0xFF80, 0x7FC1, 0xFFC0, 0x0001, 0x8003, 0x007F, 0x7F7F, 0xFF7F, 0x0080, 0x3F80],
+                       dtype=np.uint16)
+    sb = special[np.arange(rows * nb) % len(special)].reshape(rows, nb)
+    scale = torch.from_numpy(sb.view(np.int16).copy()).view(torch.bfloat16)
+    for kind, dt in OUT.items():
+        out = torch_vulkan.dequant_int8(q.to(dev), scale.to(dev), dt)
+        with np.errstate(invalid="ignore", over="ignore"):  # 0 * inf and the overflowing products
+            ref = oracle.dequant_int8(q.numpy(), sb, kind)
+        assert np.array_equal(bits(out), ref), f"{kind} {cols}"
+
+
 def test_dequant_noncontiguous_inputs_are_made_contiguous():
     q, scale = make(8, 200, 3)
     sub = q.to(dev)[:, :128]

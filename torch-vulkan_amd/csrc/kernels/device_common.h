@@ -74,13 +74,17 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)c.f;
 }
 
+// float -> IEEE half bits: the hardware conversion (round to nearest even, subnormals kept, overflow to
+// inf) for every non-NaN value; a NaN keeps its sign and top ten payload bits, quieted (0x200), as the
+// reference's f2h does (vkrt/shaders/types.glsl:18-41), where the hardware conversion would not.
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
   union {
     uint16_t u;
     _Float16 f;
   } c;
   c.f = (_Float16)x;
-  return c.u;
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) & 0x8000u) | 0x7e00u | ((u >> 13) & 0x3ffu) : (uint32_t)c.u;
 }
 
 // Element type tags used as template parameters.
