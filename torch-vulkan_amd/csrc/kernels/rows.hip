@@ -457,12 +457,15 @@ __global__ __launch_bounds__(256) void ln_fwd_row(const typename T::storage* __r
 
 // Backward, register path: one chunk of 4 rows per workgroup, one wavefront per row.  dx per row; with ws,
 // the chunk's column sums of g*xhat and g (its 4 rows added through LDS: every wavefront stores its row,
-// then each thread sums the 4 rows of its columns) as ws row pair `chunk`.  HW: weight present.
+// then each thread sums the 4 rows of its columns) as ws row pair `chunk`.  With `both` (8 D floats of
+// LDS) the two quantities are staged together behind one barrier, else one after the other (three
+// barriers).  HW: weight present.
 template <typename T, int NV, bool FULL, bool HW>
 __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restrict__ x, const typename T::storage* __restrict__ g,
                                              const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
                                              const typename T::storage* __restrict__ w, typename T::storage* __restrict__ dx,
-                                             float* __restrict__ ws, int64_t rows, int64_t D, int64_t chunk, float* part) {
+                                             float* __restrict__ ws, int64_t rows, int64_t D, int64_t chunk, float* part,
+                                             bool both) {
   constexpr int V = Vec<T>::N;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row0 = chunk * 4 + wave;
@@ -532,6 +535,29 @@ __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restri
   if (!ws) return;  // uniform across the workgroup: no barrier below is skipped by only some waves
   // rows past the end and lanes past the row hold zeros (xh = gv = 0 above)
   float* out = ws + chunk * 2 * D;
+  if (both) {  // part holds [2][4 rows][D]: both quantities staged, one barrier
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+      const int64_t col = (int64_t)(c * 64 + lane) * V;
+      if ((FULL || col < D)) {
+        float o[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = gv[c][e] * xh[c][e];
+        Vec<F32>::store(part + wave * D + col, o);
+        if constexpr (V == 8) Vec<F32>::store(part + wave * D + col + 4, o + 4);
+        Vec<F32>::store(part + (4 + wave) * D + col, gv[c]);
+        if constexpr (V == 8) Vec<F32>::store(part + (4 + wave) * D + col + 4, gv[c] + 4);
+      }
+    }
+    __syncthreads();
+    for (int64_t i = (int64_t)threadIdx.x * 4; i < 2 * D; i += 256 * 4) {  // i: position in the 2D-wide ws row
+      const float* b = part + (i < D ? i : 3 * D + i);  // quantity 1 starts at 4 D in part, at D in the ws row
+      const f32x4 r0 = *reinterpret_cast<const f32x4*>(b), r1 = *reinterpret_cast<const f32x4*>(b + D);
+      const f32x4 r2 = *reinterpret_cast<const f32x4*>(b + 2 * D), r3 = *reinterpret_cast<const f32x4*>(b + 3 * D);
+      *reinterpret_cast<f32x4*>(out + i) = (r0 + r1) + (r2 + r3);
+    }
+    return;
+  }
 #pragma unroll
   for (int qn = 0; qn < 2; ++qn) {  // qn = 0: g * xhat, 1: g
     if (qn) __syncthreads();         // the previous quantity's sums have been read
@@ -561,9 +587,9 @@ __global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __r
                                                   const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
                                                   const typename T::storage* __restrict__ w,
                                                   typename T::storage* __restrict__ dx, float* __restrict__ ws, int64_t rows,
-                                                  int64_t D) {
-  extern __shared__ float part[];  // [4 rows][D] when ws != nullptr
-  ln_bwd_chunk<T, NV, FULL, HW>(x, g, mean_in, rstd_in, w, dx, ws, rows, D, blockIdx.x, part);
+                                                  int64_t D, bool both) {
+  extern __shared__ float part[];  // [4 rows][D] or [2][4 rows][D] (both) when ws != nullptr
+  ln_bwd_chunk<T, NV, FULL, HW>(x, g, mean_in, rstd_in, w, dx, ws, rows, D, blockIdx.x, part, both);
 }
 
 // Sum over chunks of one column of the per-chunk partial sums (src = the column's value in chunk 0, stride
@@ -663,6 +689,55 @@ __global__ __launch_bounds__(1024) void ln_wgrad_reduce(const float* __restrict_
   if (grp == 0 && col < D) dst[col] = T::from_f32(combine_groups16<64>(sp + cl));
 }
 
+// The same sums when D % 16 == 0 and ws is 16-byte aligned, on 2D / 32 workgroups of 512 threads:
+// workgroup w owns 32 consecutive positions u of the 2D-wide ws rows (128 bytes, one cache line per chunk
+// row, so no line is shared with a workgroup on another XCD; u < D: dw[u], else db[u - D], D % 16 == 0
+// keeps a half block on one side); thread t sums the 4 positions of quad t % 8 over chunks t / 8,
+// t / 8 + 64, ... in chunk order (16-byte loads, four in flight: one round at 256 chunks), then each
+// position's 64 group sums are added in a fixed tree through LDS, so the result does not depend on timing.
+template <typename T>
+__global__ __launch_bounds__(512) void ln_wgrad_cols32(const float* __restrict__ ws, typename T::storage* __restrict__ dw,
+                                                       typename T::storage* __restrict__ db, int64_t chunks, int64_t D) {
+  __shared__ float sp[64 * 32];  // [group][position]
+  __shared__ float sq[16 * 32];  // [block of 4 groups][position]
+  const int t = threadIdx.x, quad = t & 7, grp = t >> 3;
+  const int64_t u0 = (int64_t)blockIdx.x * 32;
+  const int64_t stride = 2 * D;
+  const float* src = ws + u0 + quad * 4;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (u0 + quad * 4 < 2 * D) {  // the last block may cover only 16 positions
+    int64_t c = grp;
+    for (; c + 192 < chunks; c += 256) {
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + c * stride);
+      const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (c + 64) * stride);
+      const f32x4 v2 = *reinterpret_cast<const f32x4*>(src + (c + 128) * stride);
+      const f32x4 v3 = *reinterpret_cast<const f32x4*>(src + (c + 192) * stride);
+      acc += v0;
+      acc += v1;
+      acc += v2;
+      acc += v3;
+    }
+    for (; c < chunks; c += 64) acc += *reinterpret_cast<const f32x4*>(src + c * stride);
+  }
+  *reinterpret_cast<f32x4*>(sp + grp * 32 + quad * 4) = acc;
+  __syncthreads();
+  {
+    const int v = t & 31, b = t >> 5;  // groups 4b .. 4b + 3 of position v
+    sq[b * 32 + v] = (sp[(4 * b) * 32 + v] + sp[(4 * b + 1) * 32 + v]) + (sp[(4 * b + 2) * 32 + v] + sp[(4 * b + 3) * 32 + v]);
+  }
+  __syncthreads();
+  if (t < 32) {
+    const int64_t u = u0 + t;
+    typename T::storage* dst = u < D ? dw : db;
+    if (u < 2 * D && dst) {
+      float r[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) r[k] = sq[(2 * k) * 32 + t] + sq[(2 * k + 1) * 32 + t];
+      dst[u < D ? u : u - D] = T::from_f32(((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7])));
+    }
+  }
+}
+
 template <typename T>
 bool launch_ln_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_ln_args*>(p);
@@ -733,12 +808,13 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const float *mu = (const float*)a.mean, *rs = (const float*)a.rstd;
   int nv = reg_nv<T>(a.D, {a.x, a.g, a.w, a.dx});
   const auto full_row = [&](int v) { return a.D == (int64_t)v * 64 * Vec<T>::N; };  // rows fill every chunk: no column guards
-  const size_t lds = ws ? (size_t)(4 * a.D) * 4 : 0;
+  const bool both = ws && (size_t)(8 * a.D) * 4 <= 64 * 1024;
+  const size_t lds = ws ? (size_t)((both ? 8 : 4) * a.D) * 4 : 0;
   if (lds > 64 * 1024 || a.D % 4) nv = 0;
   const dim3 grid((uint32_t)chunks);
   auto go = [&](auto nvc, auto fullc, auto hwc) {
     hipLaunchKernelGGL((ln_bwd_reg<T, decltype(nvc)::value, decltype(fullc)::value, decltype(hwc)::value>), grid, dim3(256),
-                       lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
+                       lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D, both);
   };
   auto by_w = [&](auto nvc, auto fullc) {
     if (w) go(nvc, fullc, std::true_type());
@@ -776,8 +852,12 @@ bool launch_ln_wgrad(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws") || (a.dw && !ctx.check(a.dw, a.D * sizeof(S), "dw")) ||
       (a.db && !ctx.check(a.db, a.D * sizeof(S), "db")))
     return false;
-  hipLaunchKernelGGL(ln_wgrad_reduce<T>, dim3((uint32_t)cdiv(a.D, 64), 2), dim3(1024), 0, ctx.stream, (const float*)a.ws,
-                     (S*)a.dw, (S*)a.db, chunks, a.D);
+  if (a.D % 16 == 0 && a.ws % 16 == 0 && 2 * a.D / 16 <= 0x7fffffffLL)
+    hipLaunchKernelGGL(ln_wgrad_cols32<T>, dim3((uint32_t)cdiv(2 * a.D, 32)), dim3(512), 0, ctx.stream, (const float*)a.ws,
+                       (S*)a.dw, (S*)a.db, chunks, a.D);
+  else
+    hipLaunchKernelGGL(ln_wgrad_reduce<T>, dim3((uint32_t)cdiv(a.D, 64), 2), dim3(1024), 0, ctx.stream, (const float*)a.ws,
+                       (S*)a.dw, (S*)a.db, chunks, a.D);
   return hrt::launch_ok(hipGetLastError(), ctx, "ln_wgrad");
 }
 
