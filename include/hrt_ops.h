@@ -323,27 +323,44 @@ typedef struct hrt_im2col_args {
 
 /* "conv3x3_wprep_{bf16,f16}" and "conv3x3_{bf16,f16}" — a direct 3x3 convolution (stride 1, zero padding 1,
  * no dilation, one group) without the column matrix: an implicit GEMM that stages each 16-channel block of
- * three input rows once and applies the nine taps from it.  No counterpart in the reference, whose
+ * the input rows once and applies the nine taps from it.  No counterpart in the reference, whose
  * convolution is im2col + GEMM (csrc/ops_conv.cpp:89-140); the result is the same convolution in fp32
  * accumulation with one rounding (the reduction order differs from im2col + GEMM).
- *  "conv3x3_wprep_{dt}": wr[o, cb, t, i] = w[o, 16 cb + i, t] for the forward (flip = 0, w: [O, I, 3, 3],
- *                        O = Co, I = C), or, for the input gradient (flip = 1), wr[c, cb, t, i] =
- *                        w[16 cb + i, c, 8 - t] with w: [I, O, 3, 3] read as the flipped transpose (O = C,
- *                        I = Co).  wr: [O, I / 16, 9, 16] contiguous, I a multiple of 16.
- *  "conv3x3_{dt}":       y[n, o, h, w] = sum_{i, kh, kw} wr[o, i / 16, 3 kh + kw, i % 16] *
- *                        x[n, i, h + kh - 1, w + kw - 1] (0 outside x) + bias[o] when has_bias; x: [N, I, H,
- *                        W], y: [N, O, H, W], both contiguous; I a multiple of 16, O of 128, W of 64.  The
- *                        forward is (x, wprep(w, 0)); the input gradient of y = conv(x, w) is
- *                        (dy, wprep(w, 1)) with I = Co, O = C. */
+ *  "conv3x3_wprep_{dt}": reorders the weights into wr, hrt_conv3_wr_bytes(O, I) bytes (16-byte aligned):
+ *                        for output block b = o / 128 and channel block cb, a tile of 128 rows of 152
+ *                        values at byte ((b * I / 16 + cb) * 128 + o % 128) * 304, value 16 t + i of row
+ *                        o % 128 = w[o, 16 cb + i, t] for the forward (flip = 0, w: [O, I, 3, 3], O = Co,
+ *                        I = C) or w[16 cb + i, o, 8 - t] for the input gradient (flip = 1, w: [I, O, 3, 3]
+ *                        read as the flipped transpose, O = C, I = Co); values 144..151 of a row are 0.
+ *                        O a multiple of 128, I of 16, w 16-byte aligned.
+ *  "conv3x3_{dt}":       y[n, o, h, w] = sum_{i, kh, kw} wr(o, i, 3 kh + kw) * x[n, i, h + kh - 1, w + kw - 1]
+ *                        (0 outside x) + bias[o] when has_bias; x: [N, I, H, W], y: [N, O, H, W], both
+ *                        contiguous and 16-byte aligned; I a multiple of 16, O of 128, W of 64.  The input
+ *                        channels are split over `splits` (>= 1, dividing I / 16) workgroups per output
+ *                        tile; splits > 1 needs ws, splits * N * O * H * W fp32 values (16-byte aligned),
+ *                        for the partial sums, which a second kernel queued by the same call adds in split
+ *                        order.  hrt_conv3_splits gives the split the shim uses.  The forward is
+ *                        (x, wprep(w, 0)); the input gradient of y = conv(x, w) is (dy, wprep(w, 1)) with
+ *                        I = Co, O = C. */
+#define HRT_CONV3_SLAB_BYTES 38912
+static inline int64_t hrt_conv3_wr_bytes(int64_t O, int64_t I) { return (O / 128) * (I / 16) * HRT_CONV3_SLAB_BYTES; }
+/* Input-channel split of "conv3x3_{dt}": doubles while the grid (N * ceil(H / 2) * W / 64 * O / 128 tiles,
+ * times the split) stays under 256 workgroups and every split keeps at least 4 channel blocks. */
+static inline int64_t hrt_conv3_splits(int64_t N, int64_t I, int64_t O, int64_t H, int64_t W) {
+  const int64_t tiles = N * ((H + 1) / 2) * (W / 64) * (O / 128), nb = I / 16;
+  int64_t s = 1;
+  while (tiles * s * 2 <= 256 && nb % (2 * s) == 0 && nb / (2 * s) >= 4) s *= 2;
+  return s;
+}
 typedef struct hrt_conv3_wprep_args {
   uint64_t w, wr;
   int64_t O, I;
   uint32_t flip, pad;
 } hrt_conv3_wprep_args;
 typedef struct hrt_conv3_args {
-  uint64_t x, wr, bias, y;
+  uint64_t x, wr, bias, y, ws;
   int64_t N, I, O, H, W;
-  uint32_t has_bias, pad;
+  uint32_t has_bias, splits;
 } hrt_conv3_args;
 
 /* "upsample_nearest_fwd_{dt}" / "upsample_nearest_bwd_{dt}" — nearest-neighbour upsampling of [NC, H, W]

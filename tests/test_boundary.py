@@ -148,6 +148,28 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
     assert abi.ln_chunks(1024) == 256 and abi.ln_chunks(5) == 2
 
 
+def test_conv3_sizes_and_splits_match_the_c_header(tmp_path):
+    """abi.conv3_wr_bytes / abi.conv3_splits compute what hrt_conv3_wr_bytes / hrt_conv3_splits do, over
+    image sizes and channel counts around the split rule's thresholds (256 workgroups, 4 channel blocks)."""
+    from torch_vulkan import abi
+
+    cases = [(n, i, o, h, w) for n in (1, 2, 3) for i in (16, 64, 128, 512) for o in (128, 512) for h in (1, 5, 16, 64)
+             for w in (64, 128)]
+    lines = ['#include <stdio.h>', '#include "hrt_ops.h"', "int main(void) {"]
+    for n, i, o, h, w in cases:
+        lines.append(f'  printf("%lld %lld\\n", (long long)hrt_conv3_wr_bytes({o}, {i}), '
+                     f'(long long)hrt_conv3_splits({n}, {i}, {o}, {h}, {w}));')
+    lines.append("  return 0; }")
+    src = tmp_path / "conv3.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "conv3"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True, check=True).stdout.split("\n")
+    got = [tuple(map(int, l.split())) for l in out if l.strip()]
+    assert got == [(abi.conv3_wr_bytes(o, i), abi.conv3_splits(n, i, o, h, w)) for n, i, o, h, w in cases]
+    assert abi.conv3_splits(1, 512, 512, 64, 64) == 2 and abi.conv3_splits(1, 128, 128, 16, 64) == 2
+
+
 def test_python_ew_op_codes_match_the_c_header(tmp_path):
     """abi.EW_OPS names the hrt_ew_op codes of include/hrt_ops.h in order."""
     from torch_vulkan import abi

@@ -107,13 +107,13 @@ DIRECT = [  # (N, C, H, W, Co): shapes of the direct 3x3 kernel (stride 1, pad 1
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", DIRECT)
 @pytest.mark.parametrize("bias", [True, False])
-def test_conv3x3_direct_forward_and_input_grad(dt, case, bias, monkeypatch):
+def test_conv3x3_direct_forward_and_input_grad(dt, case, bias):
     """3x3 / stride 1 / padding 1 convolutions that the direct kernel (conv3x3: an implicit GEMM over staged
     input rows, no column matrix) takes: forward with and without bias, and the input gradient (the same
     kernel on the output gradient with the flipped, transposed kernel when C % 128 == 0), against the oracle;
     1- and 3-row images exercise the zero rows above and below, 128-pixel rows two segments per row."""
-    monkeypatch.setenv("VKT_CONV_DIRECT", "1")  # the direct kernel is opt-in
     N, C, H, W, Co = case
+    before = torch_vulkan.kernel_counts().get("torch_vulkan::conv3x3", 0)
     x = rnd((N, C, H, W), dt, 11)
     w = rnd((Co, C, 3, 3), dt, 12, scale=0.3)
     b = rnd((Co,), dt, 13) if bias else None
@@ -122,20 +122,38 @@ def test_conv3x3_direct_forward_and_input_grad(dt, case, bias, monkeypatch):
     xd = x.to(dev).requires_grad_(True)
     out = F.conv2d(xd, w.to(dev), b.to(dev) if bias else None, padding=1)
     rel_close(out, ref, dt, "forward")
+    runs = 1
     if C * H * W <= 128 * 16 * 64:  # the oracle's backward is slow at the full size
         gref, _, _ = oracle.conv2d_backward(f64(x), f64(w), f64(r.to(dt)), (1, 1), (1, 1))
         (out * r.to(dt).to(dev)).sum().backward()
         rel_close(xd.grad, gref, dt, "grad_input")
+        runs += C % 128 == 0  # the input gradient takes the direct kernel when C is a multiple of 128
     no_fallback("aten::convolution_overrideable", "aten::convolution_backward_overrideable")
+    assert torch_vulkan.kernel_counts().get("torch_vulkan::conv3x3", 0) - before == runs
+
+
+def test_conv3x3_im2col_switch(monkeypatch):
+    """VKT_CONV_IM2COL=1 keeps the unfolding + GEMM for a shape the direct kernel takes: same convolution
+    (to bf16 tolerance against the oracle), and the direct kernel's counter does not move."""
+    x = rnd((1, 32, 4, 64), torch.bfloat16, 31)
+    w = rnd((128, 32, 3, 3), torch.bfloat16, 32, scale=0.3)
+    ref = oracle.conv2d(f64(x), f64(w), None, (1, 1), (1, 1))
+    monkeypatch.setenv("VKT_CONV_IM2COL", "1")
+    before = torch_vulkan.kernel_counts().get("torch_vulkan::conv3x3", 0)
+    rel_close(F.conv2d(x.to(dev), w.to(dev), None, padding=1), ref, torch.bfloat16, "unfolded")
+    assert torch_vulkan.kernel_counts().get("torch_vulkan::conv3x3", 0) == before
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("flip", [0, 1])
-def test_conv3x3_c_abi(dt, flip):
+@pytest.mark.parametrize("splits", [1, 2])
+def test_conv3x3_c_abi(dt, flip, splits):
     """The two entry points called directly: conv3x3_wprep reorders [O, I, 3, 3] (flip 0) or reads
     [I, O, 3, 3] as its flipped transpose (flip 1), and conv3x3 then gives the convolution (flip 0) or the
-    input gradient of the convolution with w (flip 1), against the oracle; the argument checks reject
-    channel counts the kernel does not take."""
+    input gradient of the convolution with w (flip 1), against the oracle, with the input channels in one
+    piece or split in two (fp32 partial sums added by the same call); an odd row count leaves the last
+    workgroup's second output row outside the image.  The argument checks reject channel counts the kernel
+    does not take and splits that do not divide the channel blocks."""
     N, H, W, c_small, c_big = 2, 3, 128, 32, 128
     name = "bf16" if dt == torch.bfloat16 else "f16"
     rt = abi.Runtime()
@@ -150,17 +168,23 @@ def test_conv3x3_c_abi(dt, flip):
         ref, _, _ = oracle.conv2d_backward(np.zeros((N, c_big, H, W)), f64(w), f64(xin), (1, 1), (1, 1))
         I, O = c_small, c_big
     xd, wd = xin.to(dev), w.to(dev)
-    wr = torch.empty((O, I // 16, 9, 16), dtype=dt, device=dev)
+    wr = torch.empty(abi.conv3_wr_bytes(O, I) // 2, dtype=dt, device=dev)
     y = torch.empty((N, O, H, W), dtype=dt, device=dev)
+    ws = torch.empty(splits * N * O * H * W, dtype=torch.float32, device=dev)
     P = abi.Conv3WprepArgs()
     P.w, P.wr, P.O, P.I, P.flip = wd.data_ptr(), wr.data_ptr(), O, I, flip
     rt.dispatch("conv3x3_wprep_" + name, P)
     A = abi.Conv3Args()
     A.x, A.wr, A.y, A.N, A.I, A.O, A.H, A.W = xd.data_ptr(), wr.data_ptr(), y.data_ptr(), N, I, O, H, W
+    A.ws, A.splits = (ws.data_ptr() if splits > 1 else 0), splits
     rt.dispatch("conv3x3_" + name, A)
-    rel_close(y, ref, dt, f"conv3x3 flip {flip}")
+    rel_close(y, ref, dt, f"conv3x3 flip {flip} splits {splits}")
     bad = abi.Conv3Args.from_buffer_copy(A)
     bad.O = 64  # not a multiple of 128
+    with pytest.raises(RuntimeError):
+        rt.dispatch("conv3x3_" + name, bad)
+    bad = abi.Conv3Args.from_buffer_copy(A)
+    bad.splits = 3  # does not divide I / 16 = 2
     with pytest.raises(RuntimeError):
         rt.dispatch("conv3x3_" + name, bad)
 

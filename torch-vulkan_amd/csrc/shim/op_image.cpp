@@ -83,13 +83,13 @@ at::Tensor cols_of(const at::Tensor& input, const ConvShape& g) {
 
 // The direct 3x3 kernel ("conv3x3_{dt}": an implicit GEMM over the input rows, no column matrix) takes
 // stride 1, padding 1, a matrix-core dtype, input channels in multiples of 16, output channels in multiples of
-// 128 and rows of a multiple of 64 pixels (VAE decoder and UNet levels at 64 px and up).  It is opt-in
-// (VKT_CONV_DIRECT=1, read on every call): at 512 channels on 64x64 it runs 57 us against the unfolding +
-// GEMM's 51 us, its 32 channel steps each waiting on a fetch.  in_ch / out_ch: the channels the kernel
-// reads / writes (swapped for the adjoint).
+// 128 and rows of a multiple of 64 pixels (VAE decoder and UNet levels at 64 px and up): at 512 channels
+// on 64x64 it runs 44 us against the unfolding + GEMM's 51 us (forward + input gradient 86 against 105).
+// VKT_CONV_IM2COL=1 (read on every call) keeps the unfolding.  in_ch / out_ch: the channels the kernel reads
+// / writes (swapped for the adjoint).
 bool conv3_ok(const ConvShape& g, at::ScalarType t, int64_t in_ch, int64_t out_ch) {
-  const char* on = std::getenv("VKT_CONV_DIRECT");
-  return on != nullptr && on[0] == '1' && coop_is_enabled() && (t == at::kBFloat16 || t == at::kHalf) && g.KH == 3 && g.KW == 3 && g.SH == 1 &&
+  const char* off = std::getenv("VKT_CONV_IM2COL");
+  return !(off != nullptr && off[0] == '1') && coop_is_enabled() && (t == at::kBFloat16 || t == at::kHalf) && g.KH == 3 && g.KW == 3 && g.SH == 1 &&
          g.SW == 1 && g.PH == 1 && g.PW == 1 && in_ch % 16 == 0 && out_ch % 128 == 0 && g.W % 64 == 0 &&
          g.N * g.H * (g.W / 64) * (out_ch / 128) <= 0x7fffffffLL;
 }
@@ -98,16 +98,20 @@ bool conv3_ok(const ConvShape& g, at::ScalarType t, int64_t in_ch, int64_t out_c
 // flip = 1: the input gradient, w [in_ch, out_ch, 3, 3] read as its flipped transpose), plus bias.
 at::Tensor conv3_run(const at::Tensor& x, const at::Tensor& w, const at::Tensor* bias, const ConvShape& g,
                      int64_t in_ch, int64_t out_ch, uint32_t flip) {
-  const at::Tensor wr = at::empty({out_ch, in_ch / 16, 9, 16}, x.options());
+  const at::Tensor wr = at::empty({hrt_conv3_wr_bytes(out_ch, in_ch) / 2}, x.options());
   hrt_conv3_wprep_args P{};
   P.w = dptr(w), P.wr = dptr(wr), P.O = out_ch, P.I = in_ch, P.flip = flip;
   queue(typed("conv3x3_wprep", x.scalar_type()), P);
   at::Tensor y = at::empty({g.N, out_ch, g.H, g.W}, x.options());
+  const int64_t splits = hrt_conv3_splits(g.N, in_ch, out_ch, g.H, g.W);
+  at::Tensor ws;  // the splits' fp32 partial sums
+  if (splits > 1) ws = at::empty({splits * g.N * out_ch * g.H * g.W}, x.options().dtype(at::kFloat));
   hrt_conv3_args A{};
-  A.x = dptr(x), A.wr = dptr(wr), A.y = dptr(y);
-  A.N = g.N, A.I = in_ch, A.O = out_ch, A.H = g.H, A.W = g.W;
+  A.x = dptr(x), A.wr = dptr(wr), A.y = dptr(y), A.ws = splits > 1 ? dptr(ws) : 0;
+  A.N = g.N, A.I = in_ch, A.O = out_ch, A.H = g.H, A.W = g.W, A.splits = (uint32_t)splits;
   if (bias) A.bias = dptr(*bias), A.has_bias = 1;
   queue(typed("conv3x3", x.scalar_type()), A);
+  note_gpu("torch_vulkan::conv3x3");  // lets callers and tests see which path ran
   return y;
 }
 

@@ -71,8 +71,24 @@ class Conv3WprepArgs(ctypes.Structure):
 
 
 class Conv3Args(ctypes.Structure):
-    _fields_ = [("x", u64), ("wr", u64), ("bias", u64), ("y", u64), ("N", i64), ("I", i64), ("O", i64), ("H", i64),
-                ("W", i64), ("has_bias", u32), ("pad", u32)]
+    _fields_ = [("x", u64), ("wr", u64), ("bias", u64), ("y", u64), ("ws", u64), ("N", i64), ("I", i64), ("O", i64),
+                ("H", i64), ("W", i64), ("has_bias", u32), ("splits", u32)]
+
+
+CONV3_SLAB_BYTES = 38912  # HRT_CONV3_SLAB_BYTES
+
+
+def conv3_wr_bytes(O, I):
+    """hrt_conv3_wr_bytes: bytes of the reordered 3x3 weights of "conv3x3_wprep_*"."""
+    return (O // 128) * (I // 16) * CONV3_SLAB_BYTES
+
+
+def conv3_splits(N, I, O, H, W):
+    """hrt_conv3_splits: the input-channel split of "conv3x3_*" the shim uses."""
+    tiles, nb, s = N * ((H + 1) // 2) * (W // 64) * (O // 128), I // 16, 1
+    while tiles * s * 2 <= 256 and nb % (2 * s) == 0 and nb // (2 * s) >= 4:
+        s *= 2
+    return s
 
 
 class UpsampleArgs(ctypes.Structure):
