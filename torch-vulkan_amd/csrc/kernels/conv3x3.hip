@@ -110,8 +110,11 @@ __global__ __launch_bounds__(512) void conv3_igemm_k(hrt_conv3_args p) {
   // last one is loaded and not stored); vector bv (8 pixels) of input row h0 - 1 + brow of channel bi; the
   // halo pixel hside of row hrow of channel hi (stored by tid < 128).  Every thread issues every load with a
   // clamped address (no branch between loads); out-of-image values are zeroed at the LDS store.
-  const int bv = tid & 7, brow = (tid >> 3) & 3, bi = tid >> 5;
-  const int hside = tid & 1, hrow = (tid >> 1) & 3, hi = (tid >> 3) & 15;
+  // Lanes of a wavefront take the 16 channels x 2 vectors x 2 rows of one (vector pair, row pair), so their
+  // 2-byte LDS stores (pixel slots 48 bytes apart, channel innermost) fall in four disjoint 8-bank ranges
+  // (with 8 vectors x 4 rows x 2 channels per wavefront they met on 8 banks: 4-way conflicts).
+  const int bi = lane & 15, bv = 2 * (wave & 3) + ((lane >> 4) & 1), brow = 2 * (wave >> 2) + ((lane >> 5) & 1);
+  const int hi = lane & 15, hside = (lane >> 4) & 1, hrow = 2 * (wave & 1) + ((lane >> 5) & 1);
   const int64_t bh = h0 - 1 + brow, hr2 = h0 - 1 + hrow, hw = hside ? w0 + C3_PX : w0 - 1;
   const bool b_ok = bh >= 0 && bh < H, h_ok = hr2 >= 0 && hr2 < H && hw >= 0 && hw < W;
   const int64_t boff = (bi * H + (b_ok ? bh : 0)) * W + w0 + bv * 8;
@@ -199,13 +202,22 @@ __global__ __launch_bounds__(512) void conv3_igemm_k(hrt_conv3_args p) {
   const int64_t HW = H * W, px = row * W + w0 + l32;
   if (S == 1) {
     HK_G uint16_t* Y = gptr<uint16_t>(p.y) + n * O * HW + px;
-    const HK_G uint16_t* bias = gcptr<uint16_t>(p.bias);
+    float bv2[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bv2[e] = 0.f;
+    if (p.has_bias) {  // all 16 loads issued before the first use
+      const HK_G uint16_t* bias = gcptr<uint16_t>(p.bias) + co0 + wm * 32 + 4 * hh;
+      uint16_t braw[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) braw[e] = bias[8 * (e >> 2) + (e & 3)];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) bv2[e] = T::to_f32(braw[e]);
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int64_t co = co0 + wm * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
-      const float bv2 = p.has_bias ? T::to_f32(bias[co]) : 0.f;
-      Y[co * HW] = T::from_f32(acc0[e] + bv2);
-      Y[co * HW + 32] = T::from_f32(acc1[e] + bv2);
+      Y[co * HW] = T::from_f32(acc0[e] + bv2[e]);
+      Y[co * HW + 32] = T::from_f32(acc1[e] + bv2[e]);
     }
   } else {
     HK_G float* Wp = gptr<float>(p.ws) + (sp * p.N + n) * O * HW + px;
