@@ -3,6 +3,8 @@ reference tolerance max|err| <= tol * max(|ref|max, 1) * (1 + 0.01 sqrt(K)), tol
 f16 2e-3: odd shapes, transposed and sliced operands read in place, bias broadcast x alpha/beta, batched,
 nn.Linear autograd, matrix-core vs FMA agreement, and the BASELINE shapes (1024^3 + bias, 1024x2048x8192)."""
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -430,3 +432,33 @@ def test_tiles_128x192(m, k, n, ta, tb):
     ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.0)
     check(out, ref, torch.bfloat16, k)
     assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
+
+
+VERIFY_PROBE = """
+import torch, torch_vulkan
+g = torch.Generator().manual_seed(7)
+for (m, k, n) in [(256, 512, 384), (1024, 1024, 1024), (64, 4096, 16)]:
+    a = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    b = torch.randn((k, n), generator=g).to(torch.bfloat16)
+    c = (a.to("vk") @ b.to("vk")).cpu().float()
+    ref = a.float() @ b.float()
+    err = ((c - ref).norm() / ref.norm()).item()
+    assert err < 1e-2, (m, k, n, err)
+print("PRODUCTS_OK")
+"""
+
+
+def test_verify_mm_cross_check_runs_silently_on_correct_products():
+    """VKT_VERIFY_MM=1 (the reference's debug aid, csrc/ops_mm.cpp:148-172) recomputes every matrix-core
+    product with the FMA kernel and reports calls whose results differ beyond a few ulp.  The variable is
+    read once per process, so the products run in a child process: square, wide and narrow (split-K on the
+    narrow-output kernel) bf16 products all pass the check without a report and match the CPU product."""
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, VKT_VERIFY_MM="1")
+    env["PYTHONPATH"] = os.pathsep.join([repo, os.path.join(repo, "torch-vulkan_amd"), env.get("PYTHONPATH", "")])
+    r = subprocess.run([sys.executable, "-c", VERIFY_PROBE], capture_output=True, text=True, env=env, timeout=300)
+    assert r.returncode == 0 and "PRODUCTS_OK" in r.stdout, r.stderr[-800:]
+    assert "VERIFY-MM" not in r.stderr, r.stderr[-800:]
