@@ -3,16 +3,19 @@
 
 Headline (`value`): bf16 flash-attention forward + backward at B1 H16 S1024 D128 (the reference's attention
 benchmark shape), in algorithmic TFLOP/s: 4*B*H*S^2*D forward + 2.5x that backward = 3.006e10 flop per
-step (the convention of the reference's tools/bench_attention.py:39).  A step is the hot path's three
-kernels (forward, dQ with the delta pass folded in, dK/dV) over one batch already resident in HBM, queued
-through the hrt C ABI exactly as the PyTorch shim queues them, directly on the runtime's stream, and timed
-with HIP events on that stream.  The roofline object belongs to the step's dominant kernel; its duration
-comes from the same direct step repeated with an event after every kernel, its HBM traffic from the
-rocprofv3 counter summary in profiles/.  The same JSON line carries the step through the PyTorch operator
-path (F.scaled_dot_product_attention + autograd, host work included), the other benchmark workloads (GEMMs,
-softmax, layer_norm, int8 dequant, the fused int8 linear, attention at S=4096, ...) as absolute TFLOP/s or
-GB/s and as a fraction of MI355X's published peaks, and the CPU baseline: the reference's CPU path (torch
-CPU aten) at the full configuration, with the other configurations and the oracle's float64 port beside it.
+step (the convention of the reference's tools/bench_attention.py:39).  A step is what the reference's
+benchmark times: F.scaled_dot_product_attention forward + backward through autograd on the vk device over
+one batch already resident in HBM, which queues the hot path's three kernels (forward, dQ with the delta
+pass folded in, dK/dV); W warm-up steps, then K steps between two synchronisations (wall clock, HIP events
+beside it).  The three kernels queued directly through the hrt C ABI (no PyTorch) are reported beside it.
+The roofline object belongs to the step's dominant kernel: its average duration over 200 back-to-back
+launches between two events on the runtime stream, its HBM traffic from the rocprofv3 counter summary in
+profiles/.  The same JSON line carries the other benchmark workloads (GEMMs, softmax, layer_norm, int8
+dequant, the fused int8 linear, attention at S=4096, the DiT stack and block, image operators, ...) as
+absolute TFLOP/s or GB/s and as a fraction of MI355X's published peaks, each timed after 25 ms of untimed
+runs (its inputs are drawn on the CPU just before, and the idle GPU's clock needs milliseconds of load to
+come back), and the CPU baseline: the reference's CPU path (torch CPU aten) at the full configuration,
+with the other configurations and the oracle's float64 port beside it.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--skip-cpu] [--only-attn]
        python bench.py --profile {fwd,dq,dkdv,copy,gemm,gemm1024,dq8,softmax,ln,dequant,dit} [--steps K]
@@ -118,9 +121,29 @@ class Bench:
         g = self.torch.Generator().manual_seed(seed)
         return (self.torch.randn(shape, generator=g) * scale).to(dtype).to(self.dev)
 
+    SETTLE_S = 0.025
+
+    def settle(self, launch):
+        """Untimed launch() calls for at least 25 ms, in bursts of ~2 ms of GPU work each followed by a
+        synchronisation (so the host never queues far ahead): every workload's inputs are drawn on the CPU
+        just before it is timed, the GPU idles meanwhile, and its clock then needs milliseconds of load to
+        come back up (the same kernel runs ~20% slower in the first milliseconds).  The warm-up time follows
+        the default of triton.testing.do_bench (25 ms)."""
+        rt = self.rt
+        rt.event_record(8)
+        launch()
+        rt.event_record(9)
+        burst = max(1, int(2.0 / max(rt.elapsed_ms(8, 9), 1e-3)))
+        t_end = time.perf_counter() + self.SETTLE_S
+        while time.perf_counter() < t_end:
+            for _ in range(burst):
+                launch()
+            rt.synchronize()
+        rt.synchronize()
+
     def time_graph(self, enqueue, reps, launches=3):
         """Average GPU time of one enqueue() call: a graph of `reps` calls, replayed `launches` times
-        between two events on the runtime stream (after one untimed replay)."""
+        between two events on the runtime stream (after 25 ms of untimed replays, settle())."""
         rt = self.rt
         if self.profile_n:
             for i in range(self.profile_n):
@@ -129,8 +152,7 @@ class Bench:
             return 1.0
         gid = rt.graph(lambda: [enqueue(i) for i in range(reps)])
         try:
-            rt.graph_launch(gid)
-            rt.synchronize()
+            self.settle(lambda: rt.graph_launch(gid))
             rt.event_record(0)
             for _ in range(launches):
                 rt.graph_launch(gid)
@@ -143,8 +165,8 @@ class Bench:
     def time_direct(self, enqueue, reps, launches=3):
         """Average GPU time of one enqueue() call queued directly on the runtime stream: the launches of reps
         calls are collected once and queued with one hrt_dispatch_batch call per round (so Python's per-call
-        cost does not stall the stream), launches rounds back to back between two events, after one untimed
-        round."""
+        cost does not stall the stream), launches rounds back to back between two events, after 25 ms of
+        untimed rounds (settle())."""
         rt = self.rt
         pairs = []
         rt.dispatch = lambda name, args: pairs.append((name, args))  # collect instead of queueing
@@ -154,8 +176,7 @@ class Bench:
         finally:
             del rt.dispatch
         b = rt.batch(pairs)
-        rt.run_batch(b)
-        rt.synchronize()
+        self.settle(lambda: rt.run_batch(b))
         rt.event_record(0)
         for _ in range(launches):
             rt.run_batch(b)
@@ -468,7 +489,7 @@ class Bench:
 
         for _ in range(max(args.warmup, 3)):
             step()
-        rt.synchronize()
+        self.settle(step)
         n0 = self.tv.stats()["dispatch_n"]
         step()
         rt.synchronize()
@@ -498,8 +519,9 @@ class Bench:
             out["gpu_busy_note"] = f"the step could not be recorded: {e}"
             return out
         try:
-            rt.graph_launch(gid)  # replays only the recorded step, right after recording it
-            rt.synchronize()
+            # replays of the recorded step alone (no host work), after 25 ms of untimed replays: recording it
+            # leaves the GPU idle long enough to drop its clock
+            self.settle(lambda: rt.graph_launch(gid))
             rt.event_record(6)
             for _ in range(5):
                 rt.graph_launch(gid)
@@ -754,16 +776,15 @@ class Bench:
 
     def image_ops(self):
         """VAE-decoder shaped operators through PyTorch on the vk device (the adapters' host work included):
-        conv3x3 512 -> 512 channels at 64x64 bf16 forward and backward (im2col + the MFMA GEMM), group_norm
-        (32 groups) forward / backward on [1, 512, 128, 128] bf16, nearest x2 upsampling of [1, 512, 64, 64]
-        bf16 forward / backward.  GPU time from events around 20 calls after 3 untimed."""
+        conv3x3 512 -> 512 channels at 64x64 bf16 forward and forward + input gradient (the direct implicit
+        GEMM), group_norm (32 groups) forward / backward on [1, 512, 128, 128] bf16, nearest x2 upsampling of
+        [1, 512, 64, 64] bf16 forward / backward.  GPU time from events around 20 calls after 25 ms of
+        untimed calls (settle())."""
         torch, rt = self.torch, self.rt
         import torch.nn.functional as F
 
         def gpu_ms(fn, n=20):
-            for _ in range(3):
-                fn()
-            rt.synchronize()
+            self.settle(fn)
             rt.event_record(2)
             for _ in range(n):
                 fn()
