@@ -434,6 +434,25 @@ def test_tiles_128x192(m, k, n, ta, tb):
     assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [True, False])
+@pytest.mark.parametrize("m,k,n", [(2048, 256, 2048), (1024, 192, 4096)])
+def test_tiles_64x128(m, k, n, ta, tb, dt):
+    """Products with too few 128 x 256 / 256 x 128 tiles to fill the GPU but several hundred 64 x 128 ones
+    (2048^2 outputs) take the 64 x 128 tile kernel (four wavefronts of 32 x 64), every A and B layout, both
+    16-bit types; against the oracle, with addmm's bias, and run to run bit-identical."""
+    a = randn((k, m) if ta else (m, k), dt, 91)
+    b = randn((n, k) if tb else (k, n), dt, 92, 0.1)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), dt, 93)
+    out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.0)
+    check(out, ref, dt, k)
+    assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
+
+
 VERIFY_PROBE = """
 import torch, torch_vulkan
 g = torch.Generator().manual_seed(7)

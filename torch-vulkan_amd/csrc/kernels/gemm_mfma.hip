@@ -889,6 +889,12 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (!f32out && a.batch * (a.M / 256) * (a.N / 128) >= 192 && queue_dma<T, 256, 128, 64, 64>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
+  // 64 x 128 tiles (four wavefronts of 32 x 64: a third fewer LDS bytes per MFMA than 32 x 32 ones) where they
+  // still give a few hundred workgroups: 2048^3 34.5 -> 24.8 us, 1024 x 512 x 4096 10.3 -> 9.1 us, 1024 x 2048
+  // x 2048 unchanged (the 64 x 64 grid's second round there costs what the larger tiles save)
+  if (!f32out && a.M % 64 == 0 && a.N % 128 == 0 && a.batch * (a.M / 64) * (a.N / 128) >= 192 &&
+      queue_dma<T, 64, 128, 32, 64>(a, ctx.stream))
+    return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   if (!f32out && a.batch * (a.M / 64) * (a.N / 64) >= 128 && queue_dma<T, 64, 64, 32, 32>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   // fp32 partials of a split-K product whose slices (the batch) fill the GPU with the large tiles
