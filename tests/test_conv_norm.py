@@ -331,6 +331,18 @@ def test_group_norm_chunked_statistics(HW, G):
     gn_close(out, y, torch.float32, "y", mult=4.0)
 
 
+@pytest.mark.parametrize("shape", [(2, 512, 80, 80), (2, 256, 128, 127)])
+def test_group_norm_large_apply_blocks_with_ragged_tail(shape):
+    """Groups of 102400 / 130048 elements in >= 256 apply blocks of 16384: the last block of each group
+    is partial (vector and scalar loads), with bf16 affine parameters."""
+    G, dt = 32, torch.bfloat16
+    x = rnd(shape, dt, 15)
+    w, b = rnd((shape[1],), dt, 16), rnd((shape[1],), dt, 17)
+    out = F.group_norm(x.to(dev), G, w.to(dev), b.to(dev), 1e-6)
+    y, _, _ = oracle.group_norm_fwd(f64(x), G, f64(w), f64(b), 1e-6)
+    gn_close(out, y, dt)
+
+
 def test_vae_decoder_block_chain():
     """conv3x3 -> group_norm -> silu -> upsample x2 -> conv3x3 in bf16 at 64x64, forward and backward."""
     dt = torch.bfloat16

@@ -743,7 +743,11 @@ bool launch_gn_fwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const int64_t chunks = hrt_gn_chunks(a.C, a.HW, a.G), M = (a.C / a.G) * a.HW;
   const int64_t cs = vec ? cdiv(cdiv(M, chunks), V) * V : cdiv(M, chunks);  // chunks start on a vector
   const dim3 g((uint32_t)chunks, (uint32_t)(a.N * a.G));
-  constexpr int64_t AS = 4096;  // apply block, a multiple of every V
+  // apply block (a multiple of every V): 16384 elements, each workgroup's merge of its group's statistics
+  // then paying for four times the data of 4096 (group_norm of [1, 512, 128, 128] / [1, 256, 256, 256] /
+  // [1, 128, 512, 512] bf16: 16.2 -> 15.5, 25.5 -> 22.8, 43.4 -> 38.3-39.2 us; 32768 and 65536 were slower),
+  // unless that leaves fewer than 256 workgroups
+  const int64_t AS = cdiv(M, 16384) * a.N * a.G >= 256 ? 16384 : 4096;
   const dim3 ga((uint32_t)cdiv(M, AS), (uint32_t)(a.N * a.G));
   if (vec) {
     hipLaunchKernelGGL((gn_stats_k<T, V>), g, dim3(256), 0, ctx.stream, a, chunks, cs);
