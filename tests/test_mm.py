@@ -453,6 +453,25 @@ def test_tiles_64x128(m, k, n, ta, tb, dt):
     assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [True, False])
+@pytest.mark.parametrize("m,k,n", [(1024, 4096, 1024), (512, 4160, 1024), (256, 4288, 2048)])
+def test_tiles_64x64_long_k_four_buffer_ring(m, k, n, ta, tb, dt):
+    """Long reductions on 64 x 64 tiles (K >= 4096, at most 512 workgroups) copy three steps ahead through
+    four LDS buffers; 64, 65 and 67 K steps, so the ring's last block is whole, or leaves 1 or 3 steps.
+    Every layout, both 16-bit types, against the oracle, run to run bit-identical."""
+    a = randn((k, m) if ta else (m, k), dt, 94)
+    b = randn((n, k) if tb else (k, n), dt, 95, 0.1)
+    A = a.to(dev).t() if ta else a.to(dev)
+    B = b.to(dev).t() if tb else b.to(dev)
+    bias = randn((n,), dt, 96)
+    out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0)
+    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.0)
+    check(out, ref, dt, k)
+    assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
+
+
 VERIFY_PROBE = """
 import torch, torch_vulkan
 g = torch.Generator().manual_seed(7)

@@ -16,6 +16,7 @@
 //     gives each XCD a band of N-panels that it reads once into its own L2.
 #include <cstring>
 #include <type_traits>
+#include <utility>
 
 #include "../hrt/registry.h"
 #include "gemm_skinny.h"
@@ -26,6 +27,17 @@ namespace hk {
 bool mm_check_operands(const hrt_mm_args& a, uint64_t elem, hrt::LaunchCtx& ctx);
 
 namespace {
+
+// f(std::integral_constant<int, I>()) for I = 0 .. N - 1, unrolled at compile time (ring buffers are separate
+// LDS objects picked by a compile-time index)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>()), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>());
+}
 
 enum LoadMode { KVEC = 0, MNVEC = 1, GATHER = 2 };
 
@@ -338,9 +350,10 @@ __global__ __launch_bounds__(256) void mm_dq8_mfma(hrt_mm_dq8_args p, int64_t ti
 // 32 x 32 sub-tiles (4 wavefronts, several workgroups per CU), so that a 1024 x 1024 product still spreads
 // over 256 workgroups (measured faster than 128 x 128 tiles of 64 x 64 at 1024 x {1024, 2048, 8192} x N).
 // K advances in steps of 64
-// through a ring of three LDS buffers filled by global_load_lds_dwordx4 copies of the operands' raw rows:
-// the copies of step kt + 2 are spread over the MFMAs of step kt, so a copy has two steps to land (one step
-// of compute is shorter than the L2 latency plus the transfer of a 48 KiB step), one barrier per step.  An operand whose K axis is contiguous (A [M][K],
+// through a ring of RING LDS buffers (three; two or up to six for the plain GEMM) filled by
+// global_load_lds_dwordx4 copies of the operands' raw rows: the copies of step kt + RING - 1 are spread over
+// the MFMAs of step kt, so a copy has RING - 1 steps to land (one step of compute is shorter than the L2
+// latency plus the transfer of a 48 KiB step), one barrier per step.  An operand whose K axis is contiguous (A [M][K],
 // or B given as [N][K]) is staged as [row][k] and read with 128-bit row reads; an operand contiguous along
 // M or N (A given as [K][M], B as [K][N]) is staged as [k][row] and read with ds_read_b64_tr_b16 column
 // reads, so all four layouts need no register transposes.  Epilogue: alpha * acc + beta * bias in fp32,
@@ -360,7 +373,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
                                                                    uint64_t dq_scale, int64_t dq_nblocks) {
   static_assert(!DQ8 || !BTR, "int8 B is staged as [n][k] rows");
   static_assert(!(DQ8 && F32OUT), "the fused int8 linear writes its own dtype");
-  static_assert(RING == 3 || (RING == 2 && !DQ8), "three-buffer ring, or two buffers for the plain GEMM");
+  static_assert(RING == 3 || (RING >= 2 && RING <= 6 && !DQ8), "three-buffer ring, or 2 to 6 buffers for the plain GEMM");
   constexpr int WNN = BN / WN;         // wavefronts along n
   constexpr int NW = (BM / WM) * WNN;  // wavefronts
   constexpr int FM = WM / 32, FN = WN / 32;  // 32 x 32 accumulators per wavefront along m, n
@@ -381,9 +394,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   constexpr int Q_TILE = DQ8 ? BN * GBK : 16, IPQ = DQ8 ? BN * 4 / 64 / NW : 1, CPT = DQ8 ? BN * 8 / (NW * 64) : 1;
   static_assert(!DQ8 || (IPQ >= 1 && IPA + IPQ <= 16 && CPT * NW * 64 == BN * 8), "int8 copy split");
   // separate LDS objects per buffer, so that reads of one are known not to alias copies into another
-  __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], a2_raw[RING == 3 ? A_TILE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t a0_raw[A_TILE], a1_raw[A_TILE], a2_raw[RING >= 3 ? A_TILE : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t b0_raw[B_TILE], b1_raw[B_TILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t b2_raw[DQ8 ? Q_TILE : RING == 3 ? B_TILE : 16];  // DQ8: int8 tile 0
+  __shared__ __attribute__((aligned(1024))) uint8_t b2_raw[DQ8 ? Q_TILE : RING >= 3 ? B_TILE : 16];  // DQ8: int8 tile 0
+  __shared__ __attribute__((aligned(1024))) uint8_t a3_raw[RING >= 4 ? A_TILE : 16], b3_raw[RING >= 4 ? B_TILE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t a4_raw[RING >= 5 ? A_TILE : 16], b4_raw[RING >= 5 ? B_TILE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t a5_raw[RING >= 6 ? A_TILE : 16], b5_raw[RING >= 6 ? B_TILE : 16];
   __shared__ __attribute__((aligned(DQ8 ? 1024 : 16))) uint8_t q1_raw[Q_TILE], q2_raw[Q_TILE];
   HK_L uint8_t* const A0 = (HK_L uint8_t*)a0_raw;
   HK_L uint8_t* const A1 = (HK_L uint8_t*)a1_raw;
@@ -391,8 +407,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   HK_L uint8_t* const B0 = (HK_L uint8_t*)b0_raw;
   HK_L uint8_t* const B1 = (HK_L uint8_t*)b1_raw;
   HK_L uint8_t* const B2 = (HK_L uint8_t*)b2_raw;
-  auto abuf = [&](auto ic) { constexpr int I = decltype(ic)::value; return I == 0 ? A0 : I == 1 ? A1 : A2; };
-  auto bbuf = [&](auto ic) { constexpr int I = decltype(ic)::value; return I == 0 ? B0 : I == 1 ? B1 : B2; };
+  auto abuf = [&](auto ic) {
+    constexpr int I = decltype(ic)::value;
+    return (HK_L uint8_t*)(I == 0 ? a0_raw : I == 1 ? a1_raw : I == 2 ? a2_raw : I == 3 ? a3_raw : I == 4 ? a4_raw : a5_raw);
+  };
+  auto bbuf = [&](auto ic) {
+    constexpr int I = decltype(ic)::value;
+    return (HK_L uint8_t*)(I == 0 ? b0_raw : I == 1 ? b1_raw : I == 2 ? b2_raw : I == 3 ? b3_raw : I == 4 ? b4_raw : b5_raw);
+  };
   HK_L uint8_t* const Q0 = (HK_L uint8_t*)b2_raw;
   HK_L uint8_t* const Q1 = (HK_L uint8_t*)q1_raw;
   HK_L uint8_t* const Q2 = (HK_L uint8_t*)q2_raw;
@@ -519,17 +541,18 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
     for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
     __syncthreads();
   } else if constexpr (!DQ8) {
-    // steps 0 and 1 (step min(1, nk - 1): a single-step K re-copies step 0 into a buffer nobody reads)
+    // steps 0 .. RING - 2 into buffers 0 .. RING - 2 (step min(s, nk - 1): a short K re-copies its last step
+    // into buffers nobody reads)
+    static_for<RING - 1>([&](auto ic) {
+      constexpr int S = decltype(ic)::value;
+      const int ks = S < nk ? S : nk - 1;
 #pragma unroll
-    for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab, ass, A0, wave, alo, c);
+      for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab + ks * astep, ass, abuf(ic), wave, alo, c);
 #pragma unroll
-    for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb, bss, B0, wave, blo, c);
-    issue_order_fence();
-#pragma unroll
-    for (int c = 0; c < IPA; ++c) dma_tile_part<A_NCH, A_ROWS, NW>(Ab + k1 * astep, ass, A1, wave, alo, c);
-#pragma unroll
-    for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb + k1 * bstep, bss, B1, wave, blo, c);
-    barrier_keep_vm<IPA + IPB>();  // step 0 landed everywhere, step 1 in flight
+      for (int c = 0; c < IPB; ++c) dma_tile_part<B_NCH, B_ROWS, NW>(Bb + ks * bstep, bss, bbuf(ic), wave, blo, c);
+      issue_order_fence();
+    });
+    barrier_keep_vm<(RING - 2) * (IPA + IPB)>();  // step 0 landed everywhere, steps 1 .. RING - 2 in flight
   } else {
     // int8 steps 0, 1, 2 and A steps 0, 1; step 0's int8 tile converted before the loop
     float sv[CPT];
@@ -561,7 +584,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   // tile (kt + 1) % 2 (last read in step kt - 1); steps past the end convert a repeat nobody reads.
   auto step = [&](auto bc, auto bq, int kt) {
     constexpr int BUF = decltype(bc)::value;
-    constexpr int NXT = RING == 3 ? (BUF + 2) % 3 : (BUF + 1) % 2;
+    constexpr int NXT = DQ8 ? (BUF + 2) % 3 : (BUF + RING - 1) % RING;
     constexpr int BB = decltype(bq)::value;  // DQ8: B tile kt % 2
     constexpr int AHEAD = RING - 1;          // steps between a copy and its use
     const int kn = kt + AHEAD < nk ? kt + AHEAD : nk - 1;
@@ -612,9 +635,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
       if (more_b) barrier_keep_vm_lds<IPA + IPQ>();
       else if (more_a) barrier_keep_vm_lds<IPA>();
       else barrier_keep_vm_lds<0>();
-    } else if constexpr (RING == 3) {
-      if (more_a) barrier_keep_vm<IPA + IPB>();
-      else barrier_keep_vm<0>();
+    } else if constexpr (RING >= 3) {
+      // step kt + 1's copies (issued RING - 1 steps before it) must have landed; those of steps kt + 2 ..
+      // min(kt + RING - 1, nk - 1), issued after them, may stay in flight (a count below the true one only
+      // waits longer)
+      const int last = kt + RING - 1 < nk - 1 ? kt + RING - 1 : nk - 1;
+      const int fly = last - (kt + 1) > 0 ? last - (kt + 1) : 0;
+      static_for<RING - 1>([&](auto ic) {
+        constexpr int F = decltype(ic)::value;
+        if (fly == F || (F == RING - 2 && fly > F)) barrier_keep_vm<F * (IPA + IPB)>();
+      });
     } else {
       __syncthreads();  // the next step's copies, issued in this one, have landed everywhere
     }
@@ -631,13 +661,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
     if (kt < nk) step(I0(), I0(), kt);
   } else if constexpr (!DQ8) {
     int kt = 0;
-    for (; kt + 3 <= nk; kt += 3) {
-      step(I0(), I0(), kt);
-      step(I1(), I0(), kt + 1);
-      step(I2(), I0(), kt + 2);
-    }
-    if (kt < nk) step(I0(), I0(), kt);
-    if (kt + 1 < nk) step(I1(), I0(), kt + 1);
+    for (; kt + RING <= nk; kt += RING) static_for<RING>([&](auto ic) { step(ic, I0(), kt + decltype(ic)::value); });
+    static_for<RING - 1>([&](auto ic) {
+      if (kt + decltype(ic)::value < nk) step(ic, I0(), kt + decltype(ic)::value);
+    });
   } else {
     // A and int8 buffers rotate by 3, B tiles by 2: blocks of 6 steps, leaving after any step
     for (int kt = 0;; kt += 6) {
@@ -895,7 +922,13 @@ bool launch_mm_mfma(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (!f32out && a.M % 64 == 0 && a.N % 128 == 0 && a.batch * (a.M / 64) * (a.N / 128) >= 192 &&
       queue_dma<T, 64, 128, 32, 64>(a, ctx.stream))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
-  if (!f32out && a.batch * (a.M / 64) * (a.N / 64) >= 128 && queue_dma<T, 64, 64, 32, 32>(a, ctx.stream))
+  // 64 x 64 tiles, whose steps (4 MFMAs per wavefront) are far shorter than a copy's latency: a ring of four
+  // buffers (copies three steps ahead) for long reductions, 64 KiB per workgroup, still two per CU
+  // (1024 x 4096 x 1024 NT / NN 28.5 / 25.5 -> 24.0 us, 512 x 4096 x 2048 28.4 -> 23.7 us; at K <= 2048 the
+  // fourth buffer measured -4% to +9%, so shorter reductions keep three)
+  const int64_t t64 = a.batch * (a.M / 64) * (a.N / 64);
+  if (!f32out && t64 >= 128 &&
+      (a.K >= 4096 && t64 <= 512 ? queue_dma<T, 64, 64, 32, 32, 4>(a, ctx.stream) : queue_dma<T, 64, 64, 32, 32>(a, ctx.stream)))
     return hrt::launch_ok(hipGetLastError(), ctx, "mm_dma");
   // fp32 partials of a split-K product whose slices (the batch) fill the GPU with the large tiles
   if (f32out && a.batch * (a.M / 128) * (a.N / 256) >= 192 && queue_dma<T, 128, 256, 64, 64, 3, true>(a, ctx.stream))
