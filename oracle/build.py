@@ -1,7 +1,8 @@
 """Build the C restatement of the oracle (test infrastructure): oracle/_build/liboracle.so.
 
 The reference's own implementation cannot be built here (Rust + Vulkan runtime, GLSL shaders, a C++ shim
-that links the Rust library), so there is no oracle/_ref build; see DESIGN.md."""
+that links the Rust library), so there is no oracle/_ref build: the restatement is pinned by the
+reference's golden vectors, float64 torch and closed forms in tests/ instead."""
 
 import os
 import subprocess
