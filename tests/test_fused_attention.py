@@ -149,6 +149,29 @@ def test_unsupported_shapes_use_the_math_path():
     assert oracle.rel_l2(f64(got2), ref2.numpy()) < 3e-5
 
 
+@pytest.mark.parametrize("scale", [0.05, 0.0, -0.1])
+def test_explicit_scale(scale):
+    """A positive scale runs on the fused kernels (forward and backward against the oracle at that scale);
+    zero or negative scales take the math path (the kernels' running maxima assume scale > 0) and still
+    match the oracle."""
+    B, H, S, D = 1, 2, 200, 128
+    q, k, v, g = (uniform((B, H, S, D), torch.bfloat16, s) for s in (61, 62, 63, 64))
+    qv, kv, vv = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    o = F.scaled_dot_product_attention(qv, kv, vv, scale=scale)
+    o.backward(g.to(dev))
+    ro, rlse, rq, rk, rv = oracle_all(q, k, v, g, scale=scale)
+    # fused: this build's bf16 bound; math path (bf16 scores and probabilities): the reference's bf16 bound
+    tol = REL[torch.bfloat16] if scale > 0 else 2e-2
+    for name, got, ref in (("out", o, ro), ("dq", qv.grad, rq), ("dk", kv.grad, rk), ("dv", vv.grad, rv)):
+        if not np.any(ref):  # scale 0: dq = dk = 0 exactly
+            assert not np.any(f64(got)), name
+            continue
+        e = oracle.rel_l2(f64(got), ref)
+        assert e < tol, f"{name} scale {scale}: rel-L2 {e}"
+    fused = torch_vulkan.kernel_counts().get(OVR, 0)
+    assert (fused >= 1) == (scale > 0), (scale, fused)
+
+
 def test_auto_policy():
     torch_vulkan.set_fused_attention("auto")
     q = uniform((1, 2, 64, 64), torch.float32, 41)

@@ -27,6 +27,7 @@ namespace hk {
 
 bool attn_check(const hrt_attn_args& a, bool fwd, bool dkdv, bool dq, uint64_t elem, hrt::LaunchCtx& ctx) {
   if (a.B < 1 || a.H < 1 || a.Sq < 1 || a.Sk < 1 || a.D < 1 || a.D > 128) return ctx.fail("unsupported attention shape");
+  if (!(a.scale > 0.f) || !std::isfinite(a.scale)) return ctx.fail("attention scale must be positive and finite");
   if (a.q_sb < 0 || a.q_sh < 0 || a.q_ss < 0 || a.k_sb < 0 || a.k_sh < 0 || a.k_ss < 0 || a.v_sb < 0 || a.v_sh < 0 ||
       a.v_ss < 0 || a.do_sb < 0 || a.do_sh < 0 || a.do_ss < 0)
     return ctx.fail("negative stride");
@@ -660,44 +661,53 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
   }
 }
 
+constexpr int QST = 128;  // queries per LDS stage of the dK / dV kernel
+
 // ---- dK / dV fast path: D = 64 or 128, 16-byte aligned rows -------------------------------------------------
 //
 // Per workgroup 64 keys; Q and dO stream through LDS in double-buffered 128-query stages copied global ->
-// LDS directly, each stage computed as two 64-query halves (one barrier per 128 queries).  8 wavefronts on
-// v_mfma_f32_16x16x32 (see mfma_common.h for its lane layout): wave (k = w & 3, h = w >> 2) owns keys
-// 16 k .. +15 of the block (their K and V rows held as B fragments) and query rows 32 h .. +31 of every
-// 64-query half, so its dK/dV partials are 16 keys x D each (64 registers for D = 128) and every LDS
-// fragment read is conflict-free.  Per half and 16-query tile t:
-//   S_t = Q_t K^T, dP_t = dO_t V^T            (lane = key, 4 queries 4 g + i per tile, g = lane / 16)
-//   P = exp2(S sl2 - lse log2e), dS = P (dP - delta)
-//   dV += P^T dO, dK += dS^T Q                (A = P^T / dS^T packed from the two tiles' accumulators as
-//                                              the 32 k-slots {4 g + i, 16 + 4 g + i}; B = dO / Q read
-//                                              column-wise with ds_read_b64_tr_b16 in the same slot order)
-// lse and delta of the next half are prefetched into registers.  At the end the two query halves swap
-// partials through LDS (wave (k, 1) hands over its dK, wave (k, 0) its dV), so wave (k, 0) writes dK
-// (scaled) and wave (k, 1) writes dV, both as coalesced rows.  P and dS are rounded to the input dtype
-// before their products, as attn_coop.comp.in:235-236, 283-284.
-constexpr int QST = 128;  // queries per LDS stage
-constexpr int QHALF = 64;  // queries per computed half
-
-template <typename T, int DCH, bool A4>
-__global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
+// LDS directly, with that stage's lse and delta rows beside them.  8 wavefronts on v_mfma_f32_32x32x16:
+// wave (k = w & 1, q = w >> 1) owns keys 32 k .. +31 of the block and queries 32 q .. +31 of every stage,
+// so each wave computes one 32 x 32 tile per stage (lane = key; accumulator element 4 j + r = query
+// 8 j + 4 h + r of the wave's 32):
+//   S = Q_q K_k^T + (-lse / scale),  dP' = dO_q (-V_k)^T + delta   (A: Q / dO rows from LDS; B: K in
+//                                              registers, the negated V rows from the block's LDS tile)
+//   P = exp2(S sl2) = exp(scale S_qk - lse),  -dS = P dP' = P (delta - dP)
+//   dV += P^T dO, dK += (-dS)^T Q              (A: P^T / -dS^T packed from the accumulators as the 16 k-slots
+//                                              of two 8-query groups; B: dO / Q read column-wise with
+//                                              ds_read_b64_tr_b16 in the same slot order); dK *= -scale
+// Starting the accumulators at -lse / scale and delta (read from LDS) keeps lse and delta out of separate
+// registers, and the operands of every product are read ahead into small rings fenced by sched_barrier:
+// with 256 registers and the compiler's own order each MFMA waited for the LDS read issued right before it
+// (phase timestamps: 37-50% matrix-core use inside the product phases of the 16x16x32 form this replaces).
+// The four query quarters of a key group add their dK / dV partials through LDS in query-quarter order
+// (deterministic), wave (k, q) finishing d block q (D = 128; D = 64: dK blocks by q = 0, 1, dV blocks by
+// q = 2, 3), and store coalesced [key][d] rows.  P and dS are rounded to the input dtype before their
+// products, as attn_coop.comp.in:235-236, 283-284.
+template <typename T, int DCH>
+__global__ __launch_bounds__(512) void attn_dkdv_w32(hrt_attn_args p, int nkb) {
   constexpr int NW = 8;
-  constexpr int NCH = DCH * 4;
-  constexpr int ROWB = NCH * 16;
-  constexpr int TILE = QST * ROWB;   // bytes per Q or dO stage
-  constexpr int NDT = DCH * 2;       // 16-wide d tiles
-  constexpr int SW = NCH == 16 ? 1 : 0;  // the 16x16x32 tile layout (conflict-free reads, lds_stage.h)
+  constexpr int NCH = DCH * 4;        // 16-byte chunks per row
+  constexpr int ROWB = NCH * 16;      // bytes per LDS tile row
+  constexpr int TILE = QST * ROWB;    // bytes per Q or dO stage
+  constexpr int KSN = 2 * DCH;        // 16-wide d steps of S / dP
+  constexpr int IPW = QST * NCH / 64 / NW;  // copy instructions per tile and wavefront
   __shared__ __attribute__((aligned(1024))) uint8_t q0_raw[TILE], q1_raw[TILE], o0_raw[TILE], o1_raw[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_raw[64 * ROWB];
+  __shared__ __attribute__((aligned(1024))) float ls_raw[2][2 * QST];  // per stage buffer: lse, then delta
+  // Destination of the copies issued during a last stage that has no ragged rows: they are issued (so that
+  // no branch splits the stage's instruction stream) but land here, outside the tiles the merge reuses.
+  __shared__ __attribute__((aligned(1024))) uint8_t sink_raw[1024];
   HK_L uint8_t* const Q0 = (HK_L uint8_t*)q0_raw;
   HK_L uint8_t* const Q1 = (HK_L uint8_t*)q1_raw;
   HK_L uint8_t* const O0 = (HK_L uint8_t*)o0_raw;
   HK_L uint8_t* const O1 = (HK_L uint8_t*)o1_raw;
+  HK_L uint8_t* const VL = (HK_L uint8_t*)v_raw;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kg = wave & 3, qh = wave >> 2;
-  const int l16 = lane & 15, g4 = lane >> 4;
+  const int kg = wave & 1, qq = wave >> 1;
+  const int rl = lane & 31, hl = lane >> 5;
   uint32_t bh32, kb32;
   xcd_map32(blockIdx.x, (uint32_t)nkb * p.B * p.H, nkb, bh32, kb32);
   const int64_t bh = bh32, kb = kb32, b = bh32 / (uint32_t)p.H, hh = bh32 % (uint32_t)p.H;
@@ -705,13 +715,31 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
   const uint32_t qss = (uint32_t)(p.q_ss * 2), oss = (uint32_t)(p.do_ss * 2);
   const HK_G uint8_t* Qb = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.q) + b * p.q_sb + hh * p.q_sh);
   const HK_G uint8_t* Ob = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.dout) + b * p.do_sb + hh * p.do_sh);
+  const HK_G float* lseb = gcptr<float>(p.lse) + bh * Sq;
+  const HK_G float* dltb = gcptr<float>(p.delta) + bh * Sq;
   const int nst = (Sq + QST - 1) / QST;
 
-  const int j0 = wave * (QST * NCH / 64 / NW);
-  const DmaLanes qlo = dma_lane_offsets<NCH, SW>(qss, lane, j0), olo = dma_lane_offsets<NCH, SW>(oss, lane, j0);
-  // The block's 64 K and V rows go to the stage-1 buffers (free until stage 0 copies into them), copied once
-  // for the two wavefronts that share them (rows past Sk hold copies of the last key; their dK / dV rows
-  // are never stored), then stage 0 of Q and dO
+  const int j0 = wave * IPW;
+  // Values that depend only on the lane are re-derived where they are used from an opaque copy of the lane
+  // index, so that they are not kept live across the S / dP products (the accumulators, S, dP and the K
+  // fragments fill the 256 registers of a two-wavefront-per-SIMD kernel).
+  auto opaque = [](int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+  };
+  // lse / delta rows of a stage: waves 0..3 each copy 64 floats with one 4-byte-per-lane copy (wave w: rows
+  // 64 (w & 1) .. +63 of lse (w < 2) or delta), the rows of a single short stage clamped to Sq - 1
+  const __amdgpu_buffer_rsrc_t ls_rs = dma_rsrc(reinterpret_cast<const HK_G uint8_t*>(wave < 2 ? lseb : dltb));
+  const int ls_r = nst == 1 && 64 * (wave & 1) + lane >= Sq ? Sq - 1 : 64 * (wave & 1) + lane;
+  // (waves 4..7 copy lse rows into the sink instead: every wave issues the same instruction stream)
+  auto copy_ls = [&](int st, HK_L void* dst) {
+    const int org = nst > 1 ? (int)stage_origin<QST>(st, nst, Sq) : 0;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ls_rs, wave < 4 ? dst : (HK_L void*)sink_raw, 4, ls_r * 4, org * 4, 0, 0);
+  };
+  auto ls_dst = [&](int buf) { return (HK_L void*)(&ls_raw[buf][(wave >> 1) * QST + 64 * (wave & 1)]); };
+  // The block's 64 K rows go to stage-1's Q buffer (free until stage 0 copies into it) and are read into
+  // registers; its 64 V rows stay in their own tile for the whole loop (rows past Sk hold copies of the last
+  // key; their dK / dV rows are never stored).  Then stage 0.
   {
     const uint32_t kss = (uint32_t)(p.k_ss * 2), vss = (uint32_t)(p.v_ss * 2);
     const int kvalid = (int)(Sk - kb * 64);
@@ -720,192 +748,249 @@ __global__ __launch_bounds__(512) void attn_dkdv_dma(hrt_attn_args p, int nkb) {
                                kb * 64 * (int64_t)kss;
     const HK_G uint8_t* Vblk = reinterpret_cast<const HK_G uint8_t*>(gcptr<uint16_t>(p.v) + b * p.v_sb + hh * p.v_sh) +
                                kb * 64 * (int64_t)vss;
-    dma_tile<NCH, 64, NW, SW>(Kblk, kss, kvalid, Q1, wave, lane, dma_lane_offsets<NCH, SW>(kss, lane, jk));
-    dma_tile<NCH, 64, NW, SW>(Vblk, vss, kvalid, O1, wave, lane, dma_lane_offsets<NCH, SW>(vss, lane, jk));
+    dma_tile<NCH, 64, NW>(Kblk, kss, kvalid, Q1, wave, lane, dma_lane_offsets<NCH>(kss, lane, jk));
+    dma_tile<NCH, 64, NW>(Vblk, vss, kvalid, VL, wave, lane, dma_lane_offsets<NCH>(vss, lane, jk));
   }
   issue_order_fence();  // the first barrier counts on stage 0's copies being the last ones issued
-  dma_tile<NCH, QST, NW, SW>(Qb, qss, Sq, Q0, wave, lane, qlo);
-  dma_tile<NCH, QST, NW, SW>(Ob, oss, Sq, O0, wave, lane, olo);
+  dma_tile<NCH, QST, NW>(Qb, qss, Sq, Q0, wave, lane, dma_lane_offsets<NCH>(qss, lane, j0));
+  dma_tile<NCH, QST, NW>(Ob, oss, Sq, O0, wave, lane, dma_lane_offsets<NCH>(oss, lane, j0));
+  copy_ls(0, ls_dst(0));
 
-  // lse and delta of this lane's 8 queries of a half: tile t, rows 64 half + 32 qh + 16 t + 4 g + i of the
-  // stage (i = 0..3, four consecutive floats: one 16-byte load each when A4, i.e. Sq % 4 == 0 and 16-byte
-  // aligned arrays)
-  const HK_G float* lseb = gcptr<float>(p.lse) + bh * Sq;
-  const HK_G float* dltb = gcptr<float>(p.delta) + bh * Sq;
-  f32x4 nl[2], dl[2];  // lse, delta
-  // Stage st's tile starts at query row origin(st) (stage_origin when there is more than one stage); its
-  // rows outside [st QST, Sq) get lse = +inf, so P = dS = 0 for them.
-  auto fetch = [&](int st, int half, f32x4* lo, f32x4* dlo) {
-    const int64_t org = nst > 1 ? stage_origin<QST>(st, nst, Sq) : 0;
-    const int r0 = (int)org + half * QHALF + qh * 32 + 4 * g4;
-    if (A4 && st * QST + QST <= Sq) {
+  // per-lane byte offsets inside a 32-row quarter of a tile of the A-operand rows (row rl, chunk 2 ks + h);
+  // the tile rows of a quarter start at 32 q, which keeps the swizzle (it uses row bits 0..3)
+  int roff[KSN];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        lo[t] = *reinterpret_cast<const HK_G f32x4*>(lseb + r0 + 16 * t);
-        dlo[t] = *reinterpret_cast<const HK_G f32x4*>(dltb + r0 + 16 * t);
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int qq = r0 + 16 * t + i;
-          const bool ok = qq >= st * QST && qq < Sq;
-          lo[t][i] = ok ? lseb[qq] : INFINITY;
-          dlo[t][i] = ok ? dltb[qq] : 0.f;
-        }
-    }
-  };
-  fetch(0, 0, nl, dl);
+  for (int ks = 0; ks < KSN; ++ks) roff[ks] = tile_off<NCH>(rl, 2 * ks + hl);
 
-  // per-lane byte offsets: A-operand rows (query 32 qh + 16 t + l16, chunk 4 ks + g; t adds 16 rows and the
-  // half 64 rows, which keeps the swizzle) and B-operand column reads (rows 32 qh + 4 g + (l16 >> 2) (+16
-  // for the second read), columns 16 dt + 4 (l16 & 3))
-  int roff[DCH], coff[NDT];
+  f32x16 dk[DCH], dv[DCH];
 #pragma unroll
-  for (int ks = 0; ks < DCH; ++ks) roff[ks] = tile_off<NCH, SW>(qh * 32 + l16, 4 * ks + g4);
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-    coff[dt] = tile_off<NCH, SW>(qh * 32 + 4 * g4 + (l16 >> 2), 2 * dt + ((l16 >> 1) & 1)) + (l16 & 1) * 8;
-
-  f32x4 dk[NDT], dv[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) dk[dt] = dv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n < DCH; ++n) dk[n] = dv[n] = zero16();
   const float sl2 = p.scale * kLog2e;
 
-  // K and V rows landed (stage 0 of Q / dO may still be in flight); this lane's key (column l16 of the
-  // 16x16 tiles): K and V as B fragments, d = 32 ks + 8 g + i
-  barrier_keep_vm<2 * (QST * NCH / 64 / NW)>();
-  u32x4 kf[DCH], vf[DCH];
+  // K and V rows landed (stage 0 may still be in flight; waves 0..3 wait for one of its copies too)
+  barrier_keep_vm<2 * IPW>();
+  u32x4 kf[KSN];  // this lane's key (column rl of S): K as B fragments, d = 16 ks + 8 h + i
 #pragma unroll
-  for (int ks = 0; ks < DCH; ++ks) {
-    kf[ks] = *reinterpret_cast<const HK_L u32x4*>(Q1 + tile_off<NCH, SW>(kg * 16 + l16, 4 * ks + g4));
-    vf[ks] = *reinterpret_cast<const HK_L u32x4*>(O1 + tile_off<NCH, SW>(kg * 16 + l16, 4 * ks + g4));
+  for (int ks = 0; ks < KSN; ++ks) kf[ks] = *reinterpret_cast<const HK_L u32x4*>(Q1 + kg * 32 * ROWB + roff[ks]);
+  // V is negated in place (the sign bits of its 16-bit elements), so that dP's accumulator, started at delta,
+  // ends at delta - dP = -(dP - delta); the sign of dS is carried into dK's final scale (-scale)
+  for (int i = threadIdx.x; i < 64 * ROWB / 16; i += NW * 64) {
+    HK_L u32x4* v = reinterpret_cast<HK_L u32x4*>(VL) + i;
+    *v = *v ^ u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
   }
-  __syncthreads();  // stage 0 landed; every wave holds its K / V fragments before stage 1 is copied over them
-  // COPY: stage st + 1 is copied while stage st computes (its Q rows during the first half, its dO rows
-  // during the second), the copies placed between the MFMAs of S / dP; with more than one stage they are
-  // branch-free (stage_origin, as in the other attention kernels).
-  constexpr int IPW = QST * NCH / 64 / NW;
-  static_assert(IPW <= 2 * DCH, "a half's copies fit between its S / dP products");
-  auto half_stage = [&](auto bc, auto hc, auto cc, int st) {
+  __syncthreads();  // stage 0 landed; K fragments read and V negated before stage 1 is copied over K
+
+  const HK_L uint8_t* const Vq = VL + kg * 32 * ROWB;
+  // Stage st from buffer BUF.  Its copies of stage st + 1 are placed between the MFMAs of S / dP (a last
+  // stage without ragged rows copies its own rows again, into the sink: no branch).  RAGGED (the last stage
+  // when Sq % 128 != 0, or a single short stage) issues no copies and gives rows outside [st QST, Sq) P = 0.
+  // S's accumulator starts at -lse / scale and dP's at delta (V is negated), so that
+  //   P = exp2(acc_S sl2) = exp(scale S - lse),   -dS = P acc_dP = P (delta - dP).
+  const float nis = -1.f / p.scale;
+  auto stage = [&](auto bc, auto rc, int st) {
     constexpr int BUF = decltype(bc)::value;
-    constexpr int HALF = decltype(hc)::value;
-    constexpr bool COPY = decltype(cc)::value;
-    const HK_G uint8_t* src = HALF ? Ob + stage_origin<QST>(st + 1, nst, Sq) * oss
-                                   : Qb + stage_origin<QST>(st + 1, nst, Sq) * qss;
-    const bool more = HALF == 0 || st + 1 < nst;
-    f32x4 nn[2], dn[2];
-    if (more) fetch(HALF ? st + 1 : st, HALF ^ 1, nn, dn);
-    const HK_L uint8_t* Qt = (BUF ? Q1 : Q0) + HALF * QHALF * ROWB;
-    const HK_L uint8_t* Ot = (BUF ? O1 : O0) + HALF * QHALF * ROWB;
-    f32x4 s[2], dp[2];
+    constexpr bool RAGGED = decltype(rc)::value;
+    const bool COPY = st + 1 < nst;
+    const HK_L uint8_t* Qt = (BUF ? Q1 : Q0) + qq * 32 * ROWB;
+    const HK_L uint8_t* Ot = (BUF ? O1 : O0) + qq * 32 * ROWB;
+    const float* ls = &ls_raw[BUF][qq * 32 + 4 * hl];
+    // element 4 j + r: query 32 q + 8 j + 4 h + r of the stage tile
+    f32x16 s, dp;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s[t] = dp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(ls + 8 * j);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(ls + QST + 8 * j);
 #pragma unroll
-      for (int ks = 0; ks < DCH; ++ks) {
-        s[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Qt + roff[ks] + t * 16 * ROWB), kf[ks], s[t]);
-        dp[t] = Mfma<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Ot + roff[ks] + t * 16 * ROWB), vf[ks], dp[t]);
-        if constexpr (COPY) {
-          const int c = t * DCH + ks;
-          if (c < IPW) dma_tile_part<NCH, QST, NW>(src, HALF ? oss : qss, HALF ? (BUF ? O0 : O1) : (BUF ? Q0 : Q1),
-                                                   wave, HALF ? olo : qlo, c);
+      for (int r = 0; r < 4; ++r) {
+        s[4 * j + r] = l4[r] * nis;
+        dp[4 * j + r] = d4[r];
+      }
+    }
+    if constexpr (RAGGED) {
+      const int org = nst > 1 ? (int)stage_origin<QST>(st, nst, Sq) : 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qa = org + qq * 32 + 8 * j + 4 * hl + r;
+          s[4 * j + r] = qa >= st * QST && qa < Sq ? s[4 * j + r] : -INFINITY;
         }
+    }
+    const __amdgpu_buffer_rsrc_t qrs = dma_rsrc(Qb + stage_origin<QST>(st + 1, nst, Sq) * qss);
+    const __amdgpu_buffer_rsrc_t ors = dma_rsrc(Ob + stage_origin<QST>(st + 1, nst, Sq) * oss);
+    HK_L uint8_t* const sink = (HK_L uint8_t*)sink_raw;
+    HK_L uint8_t* const qdst = COPY ? (BUF ? Q0 : Q1) + j0 * 1024 : sink;
+    HK_L uint8_t* const odst = COPY ? (BUF ? O0 : O1) + j0 * 1024 : sink;
+    const int dstep = COPY ? 1024 : 0;
+    constexpr int RPI = 64 / NCH;
+    DmaLanes qlo, olo;
+    {
+      const int ln = opaque(lane);
+      qlo = dma_lane_offsets<NCH>(qss, ln, j0);
+      olo = dma_lane_offsets<NCH>(oss, ln, j0);
+    }
+    // S and dP products of d step ks; their operands (Q, dO, V rows) are read RA1 steps ahead into a ring,
+    // each step fenced by sched_barrier
+    constexpr int RA1 = 1;
+    u32x4 qr[RA1 + 1], orr[RA1 + 1], vr[RA1 + 1];
+    auto rd1 = [&](int ks) {
+      qr[ks % (RA1 + 1)] = *reinterpret_cast<const HK_L u32x4*>(Qt + roff[ks]);
+      orr[ks % (RA1 + 1)] = *reinterpret_cast<const HK_L u32x4*>(Ot + roff[ks]);
+      vr[ks % (RA1 + 1)] = *reinterpret_cast<const HK_L u32x4*>(Vq + roff[ks]);
+    };
+#pragma unroll
+    for (int ks = 0; ks < RA1; ++ks) rd1(ks);
+#pragma unroll
+    for (int ks = 0; ks < KSN; ++ks) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + RA1 < KSN) rd1(ks + RA1);
+      s = Mfma32<T>::mac(qr[ks % (RA1 + 1)], kf[ks], s);
+      dp = Mfma32<T>::mac(orr[ks % (RA1 + 1)], vr[ks % (RA1 + 1)], dp);
+      if constexpr (!RAGGED) {
+        if (ks < IPW)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(qrs, qdst + ks * dstep, 16, (int)qlo.off[ks % 4],
+                                                   (int)((uint32_t)((j0 + ks) * RPI) * qss), 0, 0);
+        else if (ks < 2 * IPW)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(ors, odst + (ks - IPW) * dstep, 16, (int)olo.off[(ks - IPW) % 4],
+                                                   (int)((uint32_t)((j0 + ks - IPW) * RPI) * oss), 0, 0);
+        if (ks == KSN - 1) copy_ls(st + 1, COPY ? ls_dst(BUF ^ 1) : (HK_L void*)sink);
       }
     }
-    float pv[8], ds[8];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pe = __builtin_amdgcn_exp2f(fmaf(s[t][i], sl2, -nl[t][i] * kLog2e));
-        pv[t * 4 + i] = pe;
-        ds[t * 4 + i] = pe * (dp[t][i] - dl[t][i]);
-      }
-    const u32x4 pa = u32x4{cvt2<T>(pv[0], pv[1]), cvt2<T>(pv[2], pv[3]), cvt2<T>(pv[4], pv[5]), cvt2<T>(pv[6], pv[7])};
-    const u32x4 da = u32x4{cvt2<T>(ds[0], ds[1]), cvt2<T>(ds[2], ds[3]), cvt2<T>(ds[4], ds[5]), cvt2<T>(ds[6], ds[7])};
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const u32x2 a0 = lds_tr4(Ot + coff[dt]), a1 = lds_tr4(Ot + coff[dt] + 16 * ROWB);
-      dv[dt] = Mfma<T>::mac(pa, u32x4{a0.x, a0.y, a1.x, a1.y}, dv[dt]);
-      const u32x2 b0 = lds_tr4(Qt + coff[dt]), b1 = lds_tr4(Qt + coff[dt] + 16 * ROWB);
-      dk[dt] = Mfma<T>::mac(da, u32x4{b0.x, b0.y, b1.x, b1.y}, dk[dt]);
+    for (int e = 0; e < 16; ++e) {
+      s[e] = __builtin_amdgcn_exp2f(s[e] * sl2);  // exp2(-inf) = 0 for masked rows
+      dp[e] *= s[e];
     }
-    if (more) {
-      nl[0] = nn[0], nl[1] = nn[1], dl[0] = dn[0], dl[1] = dn[1];
+    // B-operand column reads: rows 4 h + (l16 >> 2) and +8, columns 32 n + 16 ((lane >> 4) & 1) + 4 (l16 & 3)
+    int toff[DCH][2];
+    {
+      const int ln = opaque(lane);
+#pragma unroll
+      for (int n = 0; n < DCH; ++n)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int row = 8 * t + 4 * (ln >> 5) + ((ln & 15) >> 2);
+          const int c = 4 * n + 2 * ((ln >> 4) & 1) + ((ln >> 1) & 1);
+          toff[n][t] = tile_off<NCH>(row, c) + (ln & 1) * 8;
+        }
     }
-    if constexpr (HALF == 1 && COPY) __syncthreads();
+    const u32x4 pa0 = pack_slots<T>(s, 0, 1), pa1 = pack_slots<T>(s, 2, 3);
+    const u32x4 da0 = pack_slots<T>(dp, 0, 1), da1 = pack_slots<T>(dp, 2, 3);
+    // dV += P^T dO, dK += (-dS)^T Q: product i = (n, c, dV or dK) in the order n, c, {dV, dK}; its B operand
+    // (two column reads) is read RA products ahead into a ring, each step fenced by sched_barrier so that the
+    // reads stay ahead of the MFMAs that wait for them
+    constexpr int NP = 4 * DCH, RA = 2;
+    u32x4 ring[RA + 1];
+    auto rd = [&](int i) {
+      const int n = i >> 2, c = (i >> 1) & 1;
+      const HK_L uint8_t* t = (i & 1) ? Qt : Ot;
+      const u32x2 lo = lds_tr4(t + toff[n][0] + c * 16 * ROWB), hi = lds_tr4(t + toff[n][1] + c * 16 * ROWB);
+      ring[i % (RA + 1)] = u32x4{lo.x, lo.y, hi.x, hi.y};
+    };
+#pragma unroll
+    for (int i = 0; i < RA; ++i) rd(i);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + RA < NP) rd(i + RA);
+      const int n = i >> 2, c = (i >> 1) & 1;
+      if (i & 1)
+        dk[n] = Mfma32<T>::mac(c ? da1 : da0, ring[i % (RA + 1)], dk[n]);
+      else
+        dv[n] = Mfma32<T>::mac(c ? pa1 : pa0, ring[i % (RA + 1)], dv[n]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  // The last stage runs without copies (no stage follows; the tiles are reused as scratch below, and a copy
-  // landing there late has been seen to corrupt LDS written after the closing barrier), then one barrier.
-  // Pairs of copying stages run in the loop, the last one or two are peeled into straight-line code (one
-  // variant per buffer in the loop body keeps the D = 128 kernel within its 256 registers).
-  auto full = [&](auto bc, int st) {
-    half_stage(bc, I0(), std::true_type(), st);
-    half_stage(bc, I1(), std::true_type(), st);
-  };
-  auto last = [&](auto bc, int st) {
-    half_stage(bc, I0(), std::false_type(), st);
-    if (nst > 1 || Sq > QHALF) half_stage(bc, I1(), std::false_type(), st);
-  };
+  const int nfull = Sq % QST == 0 ? nst : nst - 1;  // stages without ragged rows
   int st = 0;
-  for (; st + 2 < nst; st += 2) {
-    full(I0(), st);
-    full(I1(), st + 1);
+  for (; st + 1 < nfull; st += 2) {
+    stage(I0(), std::false_type(), st);
+    stage(I1(), std::false_type(), st + 1);
   }
-  if (st + 1 < nst) {
-    full(I0(), st);
-    last(I1(), st + 1);
-  } else {
-    last(I0(), st);
+  if (st < nfull) {
+    stage(I0(), std::false_type(), st);
+    ++st;
   }
-  __syncthreads();
+  if (st < nst) {  // the ragged last stage, in buffer st & 1
+    if (st & 1)
+      stage(I1(), std::true_type(), st);
+    else
+      stage(I0(), std::true_type(), st);
+  }
 
-  // ---- sum the two query halves through tile k's area: slot 0 takes wave (k, 1)'s dK partials, slot 1 wave
-  // (k, 0)'s dV partials (16 bytes per lane and d tile); each wave then reuses its own slot to transpose its
-  // result into [key][d] rows for coalesced stores.
-  float* const area = reinterpret_cast<float*>(kg == 0 ? q0_raw : kg == 1 ? q1_raw : kg == 2 ? o0_raw : o1_raw);
-  constexpr int SLOT = NDT * 64 * 4;  // floats per slot
-  static_assert(2 * SLOT * 4 <= TILE && 16 * DCH * 32 == SLOT, "both slots fit a tile; a slot holds 16 rows of D");
-  f32x4* const give = reinterpret_cast<f32x4*>(area + (qh == 1 ? 0 : SLOT));
-  const f32x4* const take = reinterpret_cast<const f32x4*>(area + (qh == 1 ? SLOT : 0));
+  // ---- sum the four query quarters of each key group, dK first, then dV.  Piece (k, n) = d block n of key
+  // group k, finished by its owner wave (k, own(n)); the three other waves' partials go to slots 0..2 of
+  // the piece's area in query-quarter order, [slot][16 values][64 lanes] (conflict-free 16-byte accesses),
+  // and the owner adds all four in query-quarter order.  It then transposes its 32 x 32 block through its
+  // own area (rows of 40 floats) and stores 8 d of one key row per lane.
+  constexpr int PIECE = 3 * 16 * 64;  // floats
+  static_assert(2 * DCH * PIECE * 4 <= 4 * TILE, "the merge areas fit the stage tiles");
+  auto area = [&](int k, int n) -> float* {
+    const int idx = k * DCH + n;  // PIECE floats each, laid across the four stage tiles
+    constexpr int PPT = TILE / (PIECE * 4) > 0 ? TILE / (PIECE * 4) : 1;
+    uint8_t* t = idx / PPT == 0 ? q0_raw : idx / PPT == 1 ? q1_raw : idx / PPT == 2 ? o0_raw : o1_raw;
+    return reinterpret_cast<float*>(t) + (idx % PPT) * PIECE;
+  };
+  auto round = [&](auto quant) {
+    constexpr int R = decltype(quant)::value;  // 0: dK, 1: dV
+    auto own = [](int n) { return DCH == 4 ? n : n + 2 * R; };
+    f32x16* acc = R == 0 ? dk : dv;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) give[dt * 64 + lane] = qh == 1 ? dk[dt] : dv[dt];
-  __syncthreads();
-  f32x4 acc[NDT];
+    for (int n = 0; n < DCH; ++n) {
+      const int o = own(n);
+      if (o == qq) continue;
+      f32x4* dst = reinterpret_cast<f32x4*>(area(kg, n) + (qq < o ? qq : qq - 1) * 16 * 64) + lane;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc[dt] = take[dt * 64 + lane];  // all reads issued before the first use
-  const float mul = qh == 0 ? p.scale : 1.f;                          // dK is scaled, dV not (x * 1 == x)
+      for (int c = 0; c < 4; ++c) dst[c * 64] = f32x4{acc[n][4 * c], acc[n][4 * c + 1], acc[n][4 * c + 2], acc[n][4 * c + 3]};
+    }
+    __syncthreads();
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+    for (int n = 0; n < DCH; ++n) {
+      if (own(n) != qq) continue;
+      float* const ar = area(kg, n);
+      f32x16 sum = zero16();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[dt][i] = ((qh == 0 ? dk[dt][i] : dv[dt][i]) + acc[dt][i]) * mul;
-  // accumulator element i of d tile dt: key 4 g + i, d = 16 dt + l16.  Transposed through this wave's slot
-  // (read above, same wavefront, so the reads complete before these writes) into 16 [key][d] rows whose
-  // 16-float groups are XOR-permuted by (row / 4) % 4 (conflict-free writes), then stored 8 d per lane.
-  constexpr int DP = DCH * 32;
-  constexpr int LPR = DCH * 4;  // lanes per row
-  float* const tr = reinterpret_cast<float*>(const_cast<f32x4*>(take));
-  auto phys = [](int r, int c) { return r * DP + (c ^ (16 * ((r >> 2) & 3))); };
+      for (int src = 0; src < 4; ++src) {
+        if (src == qq) {
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+          for (int e = 0; e < 16; ++e) sum[e] += acc[n][e];
+        } else {
+          const f32x4* from = reinterpret_cast<const f32x4*>(ar + (src < qq ? src : src - 1) * 16 * 64) + lane;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tr[phys(4 * g4 + i, 16 * dt + l16)] = acc[dt][i];
-  const uint64_t dst_base = qh == 0 ? p.dk : p.dv;
-  const int64_t g_sb = qh == 0 ? p.k_sb : p.v_sb, g_sh = qh == 0 ? p.k_sh : p.v_sh, g_ss = qh == 0 ? p.k_ss : p.v_ss;
+          for (int c = 0; c < 4; ++c) {
+            const f32x4 x = from[c * 64];
 #pragma unroll
-  for (int ps = 0; ps < 16 * LPR / 64; ++ps) {
-    const int r = ps * (64 / LPR) + lane / LPR, c8 = (lane % LPR) * 8;
-    const f32x4 x = *reinterpret_cast<const f32x4*>(tr + phys(r, c8));
-    const f32x4 y = *reinterpret_cast<const f32x4*>(tr + phys(r, c8) + 4);
-    const int64_t kk = kb * 64 + kg * 16 + r;
-    if (kk < Sk)
-      *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + grad_row(p, b, hh, kk, Sk, g_sb, g_sh, g_ss) + c8) =
-          u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
-  }
+            for (int w = 0; w < 4; ++w) sum[4 * c + w] += x[w];
+          }
+        }
+      }
+      const float mul = R == 0 ? -p.scale : 1.f;  // dK's products used -dS; dV is not scaled (x * 1 == x)
+      // element 4 j + r: key 8 j + 4 h + r of the group, d = 32 n + rl; same wavefront wrote and reads the area
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ar[(8 * j + 4 * hl + r) * 40 + rl] = sum[4 * j + r] * mul;
+      const uint64_t dst_base = R == 0 ? p.dk : p.dv;
+      const int64_t g_sb = R == 0 ? p.k_sb : p.v_sb, g_sh = R == 0 ? p.k_sh : p.v_sh, g_ss = R == 0 ? p.k_ss : p.v_ss;
+#pragma unroll
+      for (int ps = 0; ps < 2; ++ps) {
+        const int key = ps * 16 + (lane >> 2), c8 = (lane & 3) * 8;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(ar + key * 40 + c8);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(ar + key * 40 + c8 + 4);
+        const int64_t kk = kb * 64 + kg * 32 + key;
+        if (kk < Sk)
+          *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + grad_row(p, b, hh, kk, Sk, g_sb, g_sh, g_ss) + n * 32 + c8) =
+              u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+      }
+    }
+  };
+  round(I0());
+  __syncthreads();  // every owner is done with the areas before the dV partials overwrite them
+  round(I1());
 }
 
 // The direct-to-LDS paths need D = 64 or 128, 16-byte aligned rows (q, k, v, dout) and per-stage row
@@ -926,19 +1011,11 @@ bool launch_dkdv(const void* pp, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (total > 0x7fffffffLL) return ctx.fail("grid too large");
   const dim3 g((uint32_t)total);
   if (bwd_dma_ok(a)) {
-    const bool a4 = a.Sq % 4 == 0 && a.lse % 16 == 0 && a.delta % 16 == 0;
-#define HK_DKDV(DCH)                                                                        \
-  if (a4)                                                                                   \
-    hipLaunchKernelGGL((attn_dkdv_dma<T, DCH, true>), g, dim3(512), 0, ctx.stream, a, nkb);  \
-  else                                                                                      \
-    hipLaunchKernelGGL((attn_dkdv_dma<T, DCH, false>), g, dim3(512), 0, ctx.stream, a, nkb);
-    if (a.D == 128) {
-      HK_DKDV(4)
-    } else {
-      HK_DKDV(2)
-    }
-#undef HK_DKDV
-    return hrt::launch_ok(hipGetLastError(), ctx, "attn_dkdv_dma");
+    if (a.D == 128)
+      hipLaunchKernelGGL((attn_dkdv_w32<T, 4>), g, dim3(512), 0, ctx.stream, a, nkb);
+    else
+      hipLaunchKernelGGL((attn_dkdv_w32<T, 2>), g, dim3(512), 0, ctx.stream, a, nkb);
+    return hrt::launch_ok(hipGetLastError(), ctx, "attn_dkdv_w32");
   }
   const int lm = !attn_vec_ok(a, true) ? LD_GATHER : (a.D % 32 == 0 ? LD_FULL : LD_VEC);
 #define HK_LAUNCH(DCH)                                                                                   \

@@ -81,16 +81,19 @@ bool wanted(const Dims& d, at::ScalarType t) {
   }
 }
 
+// The kernels take a positive, finite scale (their running maxima and the backward's exp2 forms scale the
+// logits after the max); any other scale goes to the math path.
 bool fused_ok(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, bool has_mask, double dropout_p,
-              bool is_causal, bool gqa) {
+              bool is_causal, bool gqa, std::optional<double> scale) {
   if (has_mask || dropout_p != 0.0 || is_causal || gqa) return false;
+  if (scale && !(*scale > 0.0 && std::isfinite(*scale))) return false;
   const std::optional<Dims> d = kernel_dims(q, k, v);
   return d && wanted(*d, q.scalar_type());
 }
 
 int64_t sdp_choice(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const std::optional<at::Tensor>& mask,
-                   double dropout_p, bool is_causal, std::optional<double>, bool enable_gqa) {
-  const bool fused = fused_ok(q, k, v, present(mask), dropout_p, is_causal, enable_gqa);
+                   double dropout_p, bool is_causal, std::optional<double> scale, bool enable_gqa) {
+  const bool fused = fused_ok(q, k, v, present(mask), dropout_p, is_causal, enable_gqa, scale);
   return static_cast<int64_t>(fused ? at::SDPBackend::overrideable : at::SDPBackend::math);
 }
 
@@ -130,7 +133,7 @@ using FwdOut = std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, c10::S
 FwdOut k_sdpa_fwd(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
                   const std::optional<at::Tensor>& attn_bias, double dropout_p, bool is_causal, bool /*return_debug_mask*/,
                   std::optional<double> scale) {
-  TORCH_CHECK(fused_ok(query, key, value, present(attn_bias), dropout_p, is_causal, false),
+  TORCH_CHECK(fused_ok(query, key, value, present(attn_bias), dropout_p, is_causal, false, scale),
               "vk: the fused attention kernels do not take this call");
   runtime();
   const at::Tensor q = unit_d(query), k = unit_d(key), v = unit_d(value);
@@ -160,7 +163,7 @@ BwdOut k_sdpa_bwd(const at::Tensor& grad_out, const at::Tensor& query, const at:
                   const at::Tensor& attn_bias, std::array<bool, 4> need, const at::Tensor& out, const at::Tensor& logsumexp,
                   const at::Tensor&, const at::Tensor&, c10::SymInt, c10::SymInt, double dropout_p, bool is_causal,
                   const at::Tensor&, const at::Tensor& o32, std::optional<double> scale) {
-  TORCH_CHECK(fused_ok(query, key, value, attn_bias.defined(), dropout_p, is_causal, false) && on_vk(grad_out) &&
+  TORCH_CHECK(fused_ok(query, key, value, attn_bias.defined(), dropout_p, is_causal, false, scale) && on_vk(grad_out) &&
                   on_vk(out) && on_vk(logsumexp),
               "vk: the fused attention kernels do not take this backward call");
   runtime();
