@@ -111,6 +111,9 @@ class Bench:
         from torch_vulkan import abi
 
         self.torch, self.tv, self.abi = torch, torch_vulkan, abi
+        # autograd's backward inline on this thread (the training loop's thread), as a vk training script
+        # would opt in: PyTorch otherwise hands the vk backward to a worker thread and waits for it
+        torch_vulkan.set_inline_backward(True)
         self.rt = abi.Runtime()
         self.dev = torch.device("vk")
         self.args = args

@@ -106,6 +106,34 @@ def test_shim_registers_the_reference_operator_surface():
     assert hasattr(torch, "vk") and torch.vk.device_count() == 1
 
 
+# The reference's pybind surface (csrc/shim.cpp:418-493, its m.def names in order).
+REFERENCE_PYBIND = (
+    "init", "dequant_int8", "device_name", "max_alloc", "live_bytes", "memory_info", "peak_live_bytes",
+    "reset_peak_live_bytes", "set_memory_limit", "synchronize", "empty_cache", "reserved_bytes", "live_blocks",
+    "slab_count", "validation_errors", "fallback_counts", "kernel_counts", "stats", "fallback_time_by_op",
+    "profile", "coop_caps", "set_coop_enabled", "set_fused_attention", "set_coop_range", "reset_coop_calls",
+    "coop_calls", "reset_counts",
+)
+
+
+def test_shim_module_has_the_reference_pybind_names():
+    """Every function the reference's extension module defines exists in this one (code that calls
+    torch_vulkan._C.<name> directly keeps working), and _C.stats() has the reference's keys (no device needed:
+    the runtime's counters read zero)."""
+    import torch_vulkan
+
+    missing = [n for n in REFERENCE_PYBIND if not hasattr(torch_vulkan._C, n)]
+    assert not missing, missing
+    keys = {"dispatch_s", "dispatch_n", "transfer_s", "transfer_n", "pipeline_create_s", "upload_MB", "download_MB",
+            "gpu_wait_s", "fallback_s"}
+    try:
+        st = torch_vulkan._C.stats()
+    except RuntimeError as e:  # no device in this container: the runtime cannot initialise
+        assert "vk" in str(e) or "device" in str(e).lower() or "hip" in str(e).lower(), e
+    else:
+        assert set(st) == keys, sorted(st)
+
+
 def test_slab_allocator_host(tmp_path):
     """Compiles tests/cpu/allocator_test.cpp against the runtime's allocator with ASan/UBSan (host code)."""
     exe = tmp_path / "alloc_test"

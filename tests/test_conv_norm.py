@@ -144,6 +144,28 @@ def test_conv3x3_im2col_switch(monkeypatch):
     assert torch_vulkan.kernel_counts().get("torch_vulkan::conv3x3", 0) == before
 
 
+def test_conv3x3_weight_view_at_odd_offset():
+    """A contiguous weight view at an odd element offset (a weight inside a flat parameter buffer) is not
+    16-byte aligned: the convolution takes the unfolding + GEMM path instead of the direct kernel, with no
+    error and the oracle's result, forward and input gradient."""
+    x = rnd((1, 128, 4, 64), torch.bfloat16, 41)
+    w = rnd((128, 128, 3, 3), torch.bfloat16, 42, scale=0.3)
+    r = rnd((1, 128, 4, 64), torch.bfloat16, 43)
+    flat = torch.zeros(1 + w.numel(), dtype=torch.bfloat16, device=dev)
+    flat[1:] = w.reshape(-1).to(dev)
+    wv = flat[1:].view(128, 128, 3, 3)  # contiguous, 2 bytes past a 16-byte boundary
+    assert wv.is_contiguous() and wv.data_ptr() % 16 != 0
+    before = torch_vulkan.kernel_counts().get("torch_vulkan::conv3x3", 0)
+    xd = x.to(dev).requires_grad_(True)
+    out = F.conv2d(xd, wv, None, padding=1)
+    rel_close(out, oracle.conv2d(f64(x), f64(w), None, (1, 1), (1, 1)), torch.bfloat16, "forward")
+    (out * r.to(dev)).sum().backward()
+    gref, _, _ = oracle.conv2d_backward(f64(x), f64(w), f64(r), (1, 1), (1, 1))
+    rel_close(xd.grad, gref, torch.bfloat16, "grad_input")
+    assert torch_vulkan.kernel_counts().get("torch_vulkan::conv3x3", 0) == before
+    no_fallback("aten::convolution_overrideable", "aten::convolution_backward_overrideable")
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("flip", [0, 1])
 @pytest.mark.parametrize("splits", [1, 2])

@@ -108,3 +108,14 @@ def test_memory_api():
     assert torch_vulkan.peak_live_bytes() >= base + (4 << 20)
     del t
     assert torch_vulkan.reserved_bytes() >= torch_vulkan.live_bytes()
+
+
+def test_stats_dictionary_matches_the_reference_keys():
+    """torch_vulkan._C.stats() (the reference's pybind name, csrc/shim.cpp:455-468) and torch_vulkan.stats()
+    return the same keys, and after a device product the dispatch count is positive."""
+    a = torch.randn(64, 64, device=dev)
+    (a @ a).cpu()
+    c, p = torch_vulkan._C.stats(), torch_vulkan.stats()
+    assert set(c) == set(p) == {"dispatch_s", "dispatch_n", "transfer_s", "transfer_n", "pipeline_create_s",
+                                "upload_MB", "download_MB", "gpu_wait_s", "fallback_s"}
+    assert c["dispatch_n"] >= 1 and c["download_MB"] > 0

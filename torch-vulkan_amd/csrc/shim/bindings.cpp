@@ -1,7 +1,8 @@
 // Python module torch_vulkan_C: what torch_vulkan/__init__.py builds the public API from (the
 // reference's pybind surface, csrc/shim.cpp:418-493, plus the pinned-memory, event and fused-linear
 // additions).  Runtime queries are bound through `ready<...>`, which initialises the runtime before the
-// call; the statistics dictionary is assembled in Python from `runtime_counters()`.
+// call.  `stats()` returns the reference's statistics dictionary (same keys and units); Python's
+// torch_vulkan.stats() assembles the same dictionary from `runtime_counters()`.
 #include <torch/extension.h>
 
 #include <map>
@@ -104,6 +105,20 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     std::vector<uint64_t> c;
     for (uint32_t i = 0; i < 8; ++i) c.push_back(hrt_stat(i));  // the order documented at hrt_stat
     return c;
+  });
+  m.def("stats", [] {
+    runtime();
+    // (key, hrt_stat index, unit scale): nanoseconds to seconds, bytes to MiB, counts as they are
+    static const std::tuple<const char*, uint32_t, double> keys[] = {
+        {"dispatch_s", 0, 1e-9},        {"dispatch_n", 1, 1.0},          {"transfer_s", 2, 1e-9},
+        {"transfer_n", 3, 1.0},         {"pipeline_create_s", 4, 1e-9},  {"upload_MB", 5, 1.0 / 1048576.0},
+        {"download_MB", 6, 1.0 / 1048576.0}, {"gpu_wait_s", 7, 1e-9}};
+    std::map<std::string, double> r;
+    for (const auto& [key, i, unit] : keys) r[key] = static_cast<double>(hrt_stat(i)) * unit;
+    double fb = 0.0;
+    for (const auto& kv : cpu_seconds_by_op()) fb += kv.second;
+    r["fallback_s"] = fb;
+    return r;
   });
   m.def("profile", [] {
     runtime();

@@ -86,9 +86,12 @@ at::Tensor cols_of(const at::Tensor& input, const ConvShape& g) {
 // 128 and rows of a multiple of 64 pixels (VAE decoder and UNet levels at 64 px and up): at 512 channels
 // on 64x64 it runs 44 us against the unfolding + GEMM's 51 us (forward + input gradient 86 against 105).
 // VKT_CONV_IM2COL=1 (read on every call) keeps the unfolding.  in_ch / out_ch: the channels the kernel reads
-// / writes (swapped for the adjoint).
-bool conv3_ok(const ConvShape& g, at::ScalarType t, int64_t in_ch, int64_t out_ch) {
+// / writes (swapped for the adjoint).  x, w: the operands the kernel would read, which it takes at 16-byte
+// aligned addresses only (a view at an odd offset, e.g. a weight inside a flat parameter buffer, goes to the
+// unfolding + GEMM path, which takes any alignment).
+bool conv3_ok(const ConvShape& g, at::ScalarType t, int64_t in_ch, int64_t out_ch, const at::Tensor& x, const at::Tensor& w) {
   const char* off = std::getenv("VKT_CONV_IM2COL");
+  if (dptr(x) % 16 != 0 || dptr(w) % 16 != 0) return false;
   return !(off != nullptr && off[0] == '1') && coop_is_enabled() && (t == at::kBFloat16 || t == at::kHalf) && g.KH == 3 && g.KW == 3 && g.SH == 1 &&
          g.SW == 1 && g.PH == 1 && g.PW == 1 && in_ch % 16 == 0 && out_ch % 128 == 0 && g.W % 64 == 0 &&
          g.N * g.H * (g.W / 64) * (out_ch / 128) <= 0x7fffffffLL;
@@ -115,11 +118,11 @@ at::Tensor conv3_run(const at::Tensor& x, const at::Tensor& w, const at::Tensor*
   return y;
 }
 
-// out[n] = A @ B[n] for A [M, K], B [N, K, L]: one product when N == 1, else bmm with A broadcast.
-at::Tensor left_matmul(const at::Tensor& A, const at::Tensor& B) {
-  const int64_t N = B.size(0);
-  if (N == 1) return at::mm(A, B.select(0, 0)).unsqueeze(0);
-  return at::bmm(A.unsqueeze(0).expand({N, A.size(0), A.size(1)}), B);
+// The weight matrix w2 [M, K] times each image's column matrix cols[n] [K, L] -> [N, M, L]: a plain GEMM for a
+// single image, else one batched GEMM whose left operand repeats w2 with a zero batch stride (no copy).
+at::Tensor weight_times(const at::Tensor& w2, const at::Tensor& cols) {
+  if (cols.size(0) == 1) return at::mm(w2, cols[0]).unsqueeze(0);
+  return at::bmm(w2.expand({cols.size(0), w2.size(0), w2.size(1)}), cols);
 }
 
 at::Tensor k_convolution_overrideable(const at::Tensor& input, const at::Tensor& weight, const std::optional<at::Tensor>& bias,
@@ -130,14 +133,15 @@ at::Tensor k_convolution_overrideable(const at::Tensor& input, const at::Tensor&
                                                 groups.guard_int(__FILE__, __LINE__));
   if (c && (!has_bias || (on_vk(*bias) && bias->scalar_type() == input.scalar_type() && bias->numel() == c->Co))) {
     const ConvShape& g = *c;
-    if (conv3_ok(g, input.scalar_type(), g.C, g.Co)) {
+    const at::Tensor xd = dense(input), wd = dense(weight);
+    if (conv3_ok(g, input.scalar_type(), g.C, g.Co, xd, wd)) {
       const at::Tensor b = has_bias ? dense(*bias) : at::Tensor();
-      at::Tensor out = conv3_run(dense(input), dense(weight), has_bias ? &b : nullptr, g, g.C, g.Co, 0);
+      at::Tensor out = conv3_run(xd, wd, has_bias ? &b : nullptr, g, g.C, g.Co, 0);
       note_gpu("aten::convolution_overrideable");
       return out;
     }
     at::Tensor cols = cols_of(input, g);
-    at::Tensor out = left_matmul(dense(weight).view({g.Co, g.K()}), cols).view({g.N, g.Co, g.OH, g.OW});
+    at::Tensor out = weight_times(wd.view({g.Co, g.K()}), cols).view({g.N, g.Co, g.OH, g.OW});
     if (has_bias) out.add_(bias->view({1, g.Co, 1, 1}));
     note_gpu("aten::convolution_overrideable");
     return out;
@@ -170,12 +174,13 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> k_convolution_backward_overrideab
   const ConvShape& g = *c;
   at::Tensor go = dense(grad_output);
   at::Tensor G = go.view({g.N, g.Co, g.L()});
-  at::Tensor w2 = dense(weight).view({g.Co, g.K()});
+  const at::Tensor wd = dense(weight);
+  at::Tensor w2 = wd.view({g.Co, g.K()});
   at::Tensor gi, gw, gb;
-  if (mask[0] && conv3_ok(g, go.scalar_type(), g.Co, g.C)) {
-    gi = conv3_run(go, dense(weight), nullptr, g, g.Co, g.C, 1);  // the adjoint: flipped, transposed kernel
+  if (mask[0] && conv3_ok(g, go.scalar_type(), g.Co, g.C, go, wd)) {
+    gi = conv3_run(go, wd, nullptr, g, g.Co, g.C, 1);  // the adjoint: flipped, transposed kernel
   } else if (mask[0]) {
-    at::Tensor gcols = dense(left_matmul(w2.t(), G));  // [N, K, L]
+    at::Tensor gcols = dense(weight_times(w2.t(), G));  // [N, K, L]
     if (g.direct()) {
       gi = gcols.view({g.N, g.C, g.H, g.W});
     } else {

@@ -288,8 +288,9 @@ def set_inline_backward(on: bool = True) -> None:
     hands the work of every non-CPU device to a per-device worker thread and waits for it; the vk device
     has one stream, so that thread adds only a cross-thread handoff: on MI355X a backward() call costs
     ~49 us of host time on vk that way against ~24 us inline, which left the GPU idle in short steps.
-    Gradients are the same either way.  Applied to the importing thread at import; VKT_THREADED_BACKWARD=1
-    keeps PyTorch's default."""
+    Gradients are the same either way.  Opt-in, because it changes the calling thread's autograd state
+    (and CUDA or other devices' backward on that thread would run inline too): call it on the thread that
+    runs the training loop, or set VKT_INLINE_BACKWARD=1 to apply it to the importing thread at import."""
     torch._C._set_multithreading_enabled(not on)
 
 
@@ -327,7 +328,7 @@ def _register():
 
 
 _register()
-if not os.environ.get("VKT_THREADED_BACKWARD"):
+if os.environ.get("VKT_INLINE_BACKWARD") == "1":
     set_inline_backward(True)
 
 
