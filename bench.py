@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-attn", action="store_true", help="headline step only (for profiling runs)")
     ap.add_argument("--profile", choices=["fwd", "dq", "dkdv", "copy", "gemm", "gemm1024", "dq8", "softmax", "ln", "dequant",
-                                          "dit", "ew", "reduce", "image"],
+                                          "dit", "ew", "reduce", "image", "dit_block"],
                     help="launch one kernel (or one benchmark workload) --steps times, untimed")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR", help="summarise rocprofv3 --pmc output directories")
     return ap.parse_args()
@@ -289,10 +289,13 @@ class Bench:
         self.kernel_step_ms = rt.elapsed_ms(0, 1) / args.steps
         del keep
 
-        # the operator path
+        # the operator path; device memory over the timed steps as tools/bench_attention.py:29-41 reports it
+        # (the allocator's peak of live bytes after a reset, and the live bytes before the steps)
         for _ in range(args.warmup):
             op_step()
         rt.synchronize()
+        self.tv.reset_peak_live_bytes()
+        live0 = self.tv.live_bytes()
         rt.event_record(2)
         t0 = time.perf_counter()
         for _ in range(args.steps):
@@ -301,6 +304,10 @@ class Bench:
         rt.synchronize()
         wall = (time.perf_counter() - t0) / args.steps * 1e3
         self.op_gpu_ms = rt.elapsed_ms(2, 3) / args.steps
+        self.op_mem = {"peak_live_bytes": int(self.tv.peak_live_bytes()), "live_bytes_before": int(live0),
+                       "note": "torch_vulkan.peak_live_bytes() over the K timed operator steps after "
+                               "reset_peak_live_bytes(), as tools/bench_attention.py:29-41; inputs q, k, v, dO "
+                               "(4 x 4 MiB) are live before the steps"}
         kc = self.tv.kernel_counts()
         assert kc.get("aten::_scaled_dot_product_fused_attention_overrideable", 0) > 0, "the fused kernels did not run"
 
@@ -454,11 +461,11 @@ class Bench:
         (frozen base weights, trainable factors and input).  The reference drives such blocks from
         sd-scripts (tests/anima_on_vk.py:25-102); sd-scripts is absent here, so the block is written out.
         `ms` is the wall time per step (W warm-up steps, then K steps between synchronisations);
-        `gpu_busy_ms` replays one recorded step (every kernel the step queued, as a HIP graph) and
-        `gpu_busy_frac` = gpu_busy_ms / ms: the share of the step the GPU spends computing rather than
-        waiting for the host.  The replay adds a graph node's launch cost (~1.5 us) to each of the step's
-        `kernels_per_step` kernels, so a value near or above 1 means the step is GPU-bound.  `cpu_fallbacks`
-        lists operators that ran on the CPU during the timed steps."""
+        `graph_replay_ms` replays one recorded step (every kernel the step queued, as a HIP graph), which adds
+        a graph node's launch cost (~1.5 us) to each of the step's `kernels_per_step` kernels.  The share of
+        the step the GPU spends in kernels is the sum of their durations over the wall time, from a rocprofv3
+        kernel trace of `--profile dit_block` (which runs 3 warm-up steps, then N steps, and prints the wall
+        time per step).  `cpu_fallbacks` lists operators that ran on the CPU during the timed steps."""
         import torch.nn.functional as F
 
         torch, rt, args = self.torch, self.rt, self.args
@@ -490,6 +497,18 @@ class Bench:
             out = y + g2 * lora(F.gelu(lora(h, "fc1"), approximate="tanh"), "fc2")
             out.backward(g)
 
+        if self.profile_n:  # --profile dit_block: the steps alone, for a kernel trace
+            for _ in range(3):
+                step()
+            rt.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(self.profile_n):
+                step()
+            rt.synchronize()
+            wall = (time.perf_counter() - t0) / self.profile_n * 1e3
+            print(json.dumps({"dit_block_profile": {"warmup_steps": 3, "steps": self.profile_n,
+                                                    "wall_ms_per_step": round(wall, 4)}}), file=sys.stderr, flush=True)
+            return {}
         for _ in range(max(args.warmup, 3)):
             step()
         self.settle(step)
@@ -515,11 +534,14 @@ class Bench:
         out = {"ms": round(wall, 4), "ms_gpu_events": round(events, 4), "tflops": round(flops / (wall * 1e-3) / 1e12, 2),
                "flop": flops, "cpu_fallbacks": fallbacks, "steps": K, "kernels_per_step": kernels,
                "shape": {"tokens": T, "C": C, "heads": H, "head_dim": D, "mlp": 4 * C, "lora_rank": R}}
+        # A recorded replay of the step (no host work) is reported beside the wall time as graph_replay_ms; a
+        # replay pays ~1.5 us per graph node, so it is not a measure of GPU idle time (the sum of the kernels'
+        # durations over the wall time, from a rocprofv3 kernel trace of --profile dit_block, is).
         try:
             gid = rt.graph(step)
         except RuntimeError as e:  # a step that waits for the GPU (a CPU fallback) cannot be recorded
-            out["gpu_busy_ms"] = out["gpu_busy_frac"] = None
-            out["gpu_busy_note"] = f"the step could not be recorded: {e}"
+            out["graph_replay_ms"] = None
+            out["graph_replay_note"] = f"the step could not be recorded: {e}"
             return out
         try:
             # replays of the recorded step alone (no host work), after 25 ms of untimed replays: recording it
@@ -533,8 +555,7 @@ class Bench:
             busy = rt.elapsed_ms(6, 7) / 5
         finally:
             rt.graph_destroy(gid)
-        out["gpu_busy_ms"] = round(busy, 4)
-        out["gpu_busy_frac"] = round(busy / wall, 4)
+        out["graph_replay_ms"] = round(busy, 4)
         return out
 
     def dq8_linear(self, M):
@@ -887,7 +908,7 @@ class Bench:
         workloads = {"gemm": lambda: self.gemm(1024, 2048, 8192, "nt"), "gemm1024": lambda: self.gemm(1024, 1024, 1024, "nn", True),
                      "dq8": lambda: self.dq8_linear(1024), "softmax": self.softmax, "ln": self.layer_norm,
                      "dequant": self.dequant, "dit": self.dit_lora_stack, "ew": self.elementwise,
-                     "reduce": self.reductions, "image": self.image_ops}
+                     "reduce": self.reductions, "image": self.image_ops, "dit_block": self.dit_block}
         if which in workloads:
             self.profile_n = n
             workloads[which]()
@@ -937,12 +958,29 @@ class Bench:
             return statistics.median(times), len(times)
 
         model = ""
-        try:
+        try:  # the model name, plus family / model / stepping (a VM may report only "AMD EPYC")
             with open("/proc/cpuinfo") as fh:
-                model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), "")
+                info = {}
+                for l in fh:
+                    if ":" in l:
+                        k_, v_ = (x.strip() for x in l.split(":", 1))
+                        info.setdefault(k_, v_)
+                    elif info:
+                        break
+            model = info.get("model name", "")
+            fam = [f"{k_} {info[k_]}" for k_ in ("cpu family", "model", "stepping") if k_ in info]
+            if fam:
+                model += " (" + ", ".join(fam) + ")"
         except OSError:
             pass
-        threads = torch.get_num_threads()
+        # every core this process may run on (the headline and the other configurations); torch's default
+        # pool (OMP_NUM_THREADS) is timed beside the headline
+        default_threads = torch.get_num_threads()
+        try:
+            threads = len(os.sched_getaffinity(0))
+        except (AttributeError, OSError):
+            threads = os.cpu_count() or default_threads
+        torch.set_num_threads(threads)
         gen = torch.Generator().manual_seed(0)
         bf = torch.bfloat16
 
@@ -955,7 +993,10 @@ class Bench:
             F.scaled_dot_product_attention(qq, kk, vv).backward(do)
 
         f, b = attn_flops(B, H, S, S, D)
-        t_aten, n_aten = median_time(aten, self.args.cpu_seconds * 0.6)
+        t_aten, n_aten = median_time(aten, self.args.cpu_seconds * 0.5)
+        torch.set_num_threads(default_threads)
+        t_def, n_def = median_time(aten, self.args.cpu_seconds * 0.1)
+        torch.set_num_threads(threads)
 
         # the oracle port on 2 heads (float64 numpy)
         Hs = 2
@@ -1006,11 +1047,15 @@ class Bench:
         rate("dequant_int8_8192x2048_bf16", lambda: (qi.float() * si.float().repeat_interleave(64, 1)[:, :2048]).to(bf),
              8192 * 2048 + 8192 * 32 * 2 + 8192 * 2048 * 2, "GB/s",
              "the reference's CPU closed form (torch_vulkan/__init__.py:203-205)")
+        torch.set_num_threads(default_threads)
         return {"value": round((f + b) / t_aten / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
-                "ms_per_sample": round(t_aten * 1e3, 2),
+                "ms_per_sample": round(t_aten * 1e3, 2), "cpu_model": model, "os_cpu_count": os.cpu_count(),
                 "sample": f"torch {torch.__version__} CPU aten F.scaled_dot_product_attention forward + backward, bf16, "
                           f"the full [1,16,1024,128] configuration (the reference's CPU path), median of {n_aten} runs "
-                          f"on {threads} threads, {model}",
+                          f"on {threads} threads (every core in this process's affinity set), {model}",
+                "default_pool": {"threads": default_threads, "value": round((f + b) / t_def / 1e12, 5),
+                                 "ms_per_sample": round(t_def * 1e3, 2),
+                                 "sample": f"the same on torch's default pool, median of {n_def} runs"},
                 "configs": cfg,
                 "oracle_port": {"value": round((fp + bp) / t_port / 1e12, 5), "unit": "TFLOP/s",
                                 "ms_per_sample": round(t_port * 1e3, 1),
@@ -1051,6 +1096,7 @@ def main():
         "kernel_step_ms": round(bench.kernel_step_ms, 5),
         "kernel_step_tflops": round(3.006477e10 / (bench.kernel_step_ms * 1e-3) / 1e12, 2),
         "ms_sum_of_kernel_averages": round(bench.kernel_sum_ms, 5),
+        "attn_step_memory": bench.op_mem,
     }
     if not args.only_attn:
         line["attn_s4096"] = bench.attn_s4096()

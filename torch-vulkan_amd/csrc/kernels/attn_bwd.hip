@@ -560,16 +560,29 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
     const HK_G uint8_t* vsrc = Vb + stage_origin<KST2>(st + 1, nst, Sk) * vss;
     const HK_L uint8_t* Kt = BUF ? K1 : K0;
     const HK_L uint8_t* Vt = BUF ? V1 : V0;
+    // S^T, dP^T of d step ks; their A operands (K, V rows) are read RA1 steps ahead into a ring, each step
+    // fenced by sched_barrier (the compiler's own order read each operand right before its MFMA)
     f32x16 s = zero16(), dp = zero16();
+    constexpr int RA1 = 2;
+    u32x4 kr[RA1 + 1], vr[RA1 + 1];
+    auto rd1 = [&](int ks) {
+      kr[ks % (RA1 + 1)] = *reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]);
+      vr[ks % (RA1 + 1)] = *reinterpret_cast<const HK_L u32x4*>(Vt + koff[ks]);
+    };
+#pragma unroll
+    for (int ks = 0; ks < RA1; ++ks) rd1(ks);
 #pragma unroll
     for (int ks = 0; ks < 2 * DCH; ++ks) {
-      s = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Kt + koff[ks]), qf[ks], s);
-      dp = Mfma32<T>::mac(*reinterpret_cast<const HK_L u32x4*>(Vt + koff[ks]), df[ks], dp);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + RA1 < 2 * DCH) rd1(ks + RA1);
+      s = Mfma32<T>::mac(kr[ks % (RA1 + 1)], qf[ks], s);
+      dp = Mfma32<T>::mac(vr[ks % (RA1 + 1)], df[ks], dp);
       if constexpr (COPY) {
         if (ks < IPW) dma_tile_part<NCH, KST2, NW>(ksrc, kss, BUF ? K0 : K1, wave, klo, ks);
         else if (ks < 2 * IPW) dma_tile_part<NCH, KST2, NW>(vsrc, vss, BUF ? V0 : V1, wave, vlo, ks - IPW);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
     // element 4j+r: tile row kq*32 + 8j + 4h + r of the stage, query = this lane's
     if (key0 + KST2 > Sk) {
       const int64_t kbase = (nst > 1 ? stage_origin<KST2>(st, nst, Sk) : 0) + kq * 32 + 4 * hl;
@@ -585,14 +598,25 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
       dp[e] = pv * (dp[e] - dlt);
     }
     const u32x4 d0 = pack_slots<T>(dp, 0, 1), d1 = pack_slots<T>(dp, 2, 3);
+    // dQ^T += K^T dS^T, product i = (n, kc) = (i >> 1, i & 1); its A operand (two column reads of K) is read
+    // RA products ahead into a ring
+    constexpr int NP = 2 * DCH, RA = 2;
+    u32x4 ring[RA + 1];
+    auto rd = [&](int i) {
+      const int n = i >> 1, kc = i & 1;
+      const u32x2 lo = lds_tr4(Kt + voff[n][0] + kc * 16 * ROWB), hi = lds_tr4(Kt + voff[n][1] + kc * 16 * ROWB);
+      ring[i % (RA + 1)] = u32x4{lo.x, lo.y, hi.x, hi.y};
+    };
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int n = 0; n < DCH; ++n)
+    for (int i = 0; i < RA; ++i) rd(i);
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const u32x2 lo = lds_tr4(Kt + voff[n][0] + kc * 16 * ROWB);
-        const u32x2 hi = lds_tr4(Kt + voff[n][1] + kc * 16 * ROWB);
-        acc[n] = Mfma32<T>::mac(u32x4{lo.x, lo.y, hi.x, hi.y}, kc ? d1 : d0, acc[n]);
-      }
+    for (int i = 0; i < NP; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + RA < NP) rd(i + RA);
+      acc[i >> 1] = Mfma32<T>::mac(ring[i % (RA + 1)], (i & 1) ? d1 : d0, acc[i >> 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
   };
   // Pairs of copying stages, the last one or two peeled into straight-line code (the loop body holds one
