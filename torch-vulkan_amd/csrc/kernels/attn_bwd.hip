@@ -971,7 +971,8 @@ __global__ __launch_bounds__(512) void attn_dkdv_w32(hrt_attn_args p, int nkb) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) dst[c * 64] = f32x4{acc[n][4 * c], acc[n][4 * c + 1], acc[n][4 * c + 2], acc[n][4 * c + 3]};
     }
-    __syncthreads();
+    // the partials are visible to every wave; the previous round's global stores may stay in flight
+    barrier_keep_vm_lds<63>();
 #pragma unroll
     for (int n = 0; n < DCH; ++n) {
       if (own(n) != qq) continue;
@@ -1013,7 +1014,7 @@ __global__ __launch_bounds__(512) void attn_dkdv_w32(hrt_attn_args p, int nkb) {
     }
   };
   round(I0());
-  __syncthreads();  // every owner is done with the areas before the dV partials overwrite them
+  barrier_keep_vm_lds<63>();  // every owner is done with the areas before the dV partials overwrite them
   round(I1());
 }
 

@@ -381,7 +381,8 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
       for (int e = 0; e < V; ++e) s += v[c][e];
     }
   }
-  const float mean = wave_sum_dpp(s) / (float)D;
+  const float inv_d = 1.f / (float)D;
+  const float mean = wave_sum_dpp(s) * inv_d;
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
@@ -389,12 +390,12 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
     if (FULL || col < D) {
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        const float d = v[c][e] - mean;
-        q += d * d;
+        v[c][e] -= mean;  // kept centred for the output below
+        q += v[c][e] * v[c][e];
       }
     }
   }
-  const float var = wave_sum_dpp(q) / (float)D;
+  const float var = wave_sum_dpp(q) * inv_d;
   const float rstd = 1.f / sqrtf(var + eps);
   // y = ((x - mean) * rstd) * w + b, the product and sum as one fma
 #pragma unroll
@@ -404,7 +405,7 @@ __global__ __launch_bounds__(256) void ln_fwd_reg(const typename T::storage* __r
     if constexpr (HB) Vec<T>::unpack(rb[c], bv);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-      const float t = (v[c][e] - mean) * rstd;
+      const float t = v[c][e] * rstd;
       if constexpr (HW && HB) v[c][e] = fmaf(t, wv[e], bv[e]);
       else if constexpr (HW) v[c][e] = t * wv[e];
       else if constexpr (HB) v[c][e] = t + bv[e];
@@ -490,38 +491,45 @@ __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restri
     if constexpr (HW) asm volatile("" : "+v"(rx[c]), "+v"(rg[c]) : "v"(rw[c]));
     else asm volatile("" : "+v"(rx[c]), "+v"(rg[c]));
   }
-  float s1 = 0.f, s2 = 0.f;
+  // A row past the end or a vector past D contributes nothing: its g is zeroed as loaded (so gw, g * xhat
+  // and g vanish; its xhat is that of data the live lanes process anyway, so a non-finite value there makes
+  // their sums non-finite as well).  xhat = x rstd - mean rstd (one fma per element).
+  const float mr = -mean * rstd;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int64_t col = (int64_t)(c * 64 + lane) * V;
     const bool ok = live && (FULL || col < D);
-    float wv[V];
+    rg[c] = ok ? rg[c] : u32x4{0u, 0u, 0u, 0u};
+  }
+  float wv[NV][V];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
     Vec<T>::unpack(rx[c], xh[c]);
     Vec<T>::unpack(rg[c], gv[c]);
-    if constexpr (HW) Vec<T>::unpack(rw[c], wv);
+    if constexpr (HW) Vec<T>::unpack(rw[c], wv[c]);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-      xh[c][e] = ok ? (xh[c][e] - mean) * rstd : 0.f;
-      gv[c][e] = ok ? gv[c][e] : 0.f;
-      const float gw = HW ? gv[c][e] * wv[e] : gv[c][e];
+      xh[c][e] = fmaf(xh[c][e], rstd, mr);
+      const float gw = HW ? gv[c][e] * wv[c][e] : gv[c][e];
       s1 += gw;
-      s2 += gw * xh[c][e];
+      s2 = fmaf(gw, xh[c][e], s2);
     }
   }
-  s1 = wave_sum_dpp(s1) / (float)D;
-  s2 = wave_sum_dpp(s2) / (float)D;
+  const float inv_d = 1.f / (float)D;
+  s1 = wave_sum_dpp(s1) * inv_d;
+  s2 = wave_sum_dpp(s2) * inv_d;
   if (dx) {
+    // dx = rstd (gw - s1 - xhat s2) = rstd gw + (xhat (-rstd s2) + (-rstd s1))
+    const float b2 = -rstd * s2, b1 = -rstd * s1;
     float o[NV][V];
 #pragma unroll
-    for (int c = 0; c < NV; ++c) {
-      float wv[V];
-      if constexpr (HW) Vec<T>::unpack(rw[c], wv);
+    for (int c = 0; c < NV; ++c)
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        const float gw = HW ? gv[c][e] * wv[e] : gv[c][e];
-        o[c][e] = rstd * (gw - s1 - xh[c][e] * s2);
+        const float gw = HW ? gv[c][e] * wv[c][e] : gv[c][e];
+        o[c][e] = fmaf(rstd, gw, fmaf(xh[c][e], b2, b1));
       }
-    }
     u32x4 out[NV];
     pack_chunks<T>(o, out);
     if (live) {
