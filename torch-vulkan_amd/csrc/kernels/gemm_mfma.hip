@@ -516,14 +516,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
   // 8 int8 -> 8 values of T per piece: the 8 lanes of a group write the 8 chunks of one 128-byte B row
   // (LDS writes are conflict-free when each group of 8 consecutive lanes stays inside one 128-byte row,
   // measured), and the int8 reads are contiguous 8-byte pieces.
-  // Round to the input dtype: the hardware pack (RNE) when the products are finite, which they are unless a
-  // scale is inf or NaN; then the software rounding, which maps NaN to 0x7FC0 like dq8_*.  The choice is
-  // made per wavefront (every scale of its rows finite), so the fast path carries no per-element selects.
   auto dq_convert = [&](const HK_L uint8_t* Qt, HK_L uint8_t* Bt, const float* sv) {
-    bool fin = true;
-#pragma unroll
-    for (int u = 0; u < CPT; ++u) fin = fin && __builtin_isfinite(sv[u]);
-    const bool hw = __all(fin);
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
       const int c = u * NW * 64 + (int)threadIdx.x, row = c >> 3, ch = c & 7;
@@ -531,11 +524,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
       float v[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)(((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xffu) * sv[u];
-      u32x4 h;
-      if (hw)
-        h = u32x4{cvt2<T>(v[0], v[1]), cvt2<T>(v[2], v[3]), cvt2<T>(v[4], v[5]), cvt2<T>(v[6], v[7])};
-      else
-        h = u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
+      // round to the input dtype: the hardware pack (RNE) when the products are finite, which they are
+      // unless the scale is inf or NaN; then the software rounding, which maps NaN to 0x7FC0 like dq8_*
+      const u32x4 h = __builtin_isfinite(sv[u]) ? u32x4{cvt2<T>(v[0], v[1]), cvt2<T>(v[2], v[3]), cvt2<T>(v[4], v[5]), cvt2<T>(v[6], v[7])}
+                                                 : u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
       *reinterpret_cast<HK_L u32x4*>(Bt + tile_off<B_NCH>(row, ch)) = h;
     }
   };
