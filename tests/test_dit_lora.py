@@ -52,17 +52,16 @@ def test_linear_with_lora_forward_backward(name, fin, fout):
 
     x64, W64, b64, A64, B64, g64 = (f64(t) for t in (x, W, b, A, B, g))
     h64 = rb(x64 @ A64.T)
-    rows = slice(0, 256)  # output rows are independent: the oracle checks a slice of the big products
-    y_ref = rb(oracle.gemm(x64[rows], W64.T, b64, 1.0, 1.0)) + rb(h64[rows] @ B64.T)
-    assert rel(y[rows], y_ref) <= 1e-2
+    y_ref = rb(oracle.gemm(x64, W64.T, b64, 1.0, 1.0)) + rb(h64 @ B64.T)  # every row of y and dx is checked
+    assert rel(y, y_ref) <= 1e-2
 
     dh = rb(g64 @ B64)                 # dL/dh
     dB_ref = g64.T @ h64               # [fout, 16]
     dA_ref = dh.T @ x64                # [16, fin]
-    dx_ref = g64[rows] @ W64 + dh[rows] @ A64
+    dx_ref = g64 @ W64 + dh @ A64
     assert rel(Bd.grad, dB_ref) <= 1e-2
     assert rel(Ad.grad, dA_ref) <= 1e-2
-    assert rel(xd.grad[rows], dx_ref) <= 1e-2
+    assert rel(xd.grad, dx_ref) <= 1e-2
     assert "aten::mm" not in torch_vulkan.fallback_counts()
 
 

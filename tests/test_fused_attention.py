@@ -235,6 +235,28 @@ def baseline_check(S, heads_checked):
         assert torch.isfinite(got.float().cpu()).all()
 
 
+@pytest.mark.parametrize("Sq,Sk,D", [(2048, 2048, 64), (2100, 1900, 128), (2048, 300, 128)])
+def test_long_sequences_128_query_blocks(Sq, Sk, D):
+    """Long sequences at 16 heads (several workgroups per CU, many key stages per workgroup): out and lse
+    against the float64 oracle on heads 0 and 15, ragged Sq and Sk (the last query block and key stage
+    partly empty, Sk shorter than Sq), the fused forward identical to the one autograd runs, and the
+    gradients of the whole step at the rel-L2 bar."""
+    B, H, dt = 1, 16, torch.bfloat16
+    q = randn((B, H, Sq, D), dt, 71)
+    k, v = randn((B, H, Sk, D), dt, 72), randn((B, H, Sk, D), dt, 73)
+    g = randn((B, H, Sq, D), dt, 74)
+    out, lse, *_ = torch.ops.aten._scaled_dot_product_fused_attention_overrideable(q.to(dev), k.to(dev), v.to(dev), None)
+    o, dq, dk, dv = run_vk(q, k, v, g)
+    assert torch.equal(o.cpu(), out.cpu())
+    for h in (0, H - 1):
+        hs = slice(h, h + 1)
+        ro, rl, rq, rk, rv = oracle_all(q[:, hs], k[:, hs], v[:, hs], g[:, hs])
+        assert oracle.rel_l2(f64(out[:, hs]), ro) <= REL[dt], h
+        assert np.allclose(f64(lse[:, hs]), rl, rtol=1e-4, atol=1e-4), h
+        for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+            assert oracle.rel_l2(f64(got[:, hs]), ref) <= REL[dt], (h, name)
+
+
 def test_baseline_s1024_h16_d128_bf16():
     baseline_check(1024, 16)
 

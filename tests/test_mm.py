@@ -336,7 +336,8 @@ def test_short_k_products(dt, k, m, n, wlayout):
         assert torch.equal((hd @ wd).cpu(), (hd @ wd).cpu())  # deterministic
 
 
-NARROW = [(1024, 16, 2048), (37, 3, 40), (2048, 16, 1024), (520, 1, 4096), (64, 12, 104), (136, 16, 4104)]
+NARROW = [(1024, 16, 2048), (37, 3, 40), (2048, 16, 1024), (520, 1, 4096), (64, 12, 104), (136, 16, 4104),
+          (1024, 16, 8192), (6144, 16, 1024), (72, 8, 3000)]
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
@@ -344,10 +345,10 @@ NARROW = [(1024, 16, 2048), (37, 3, 40), (2048, 16, 1024), (520, 1, 4096), (64, 
 @pytest.mark.parametrize("form", ["x_At", "g_B", "gt_h", "dht_x", "A_xt"])
 def test_narrow_output_products(dt, p, r, q, form):
     """An output side of at most 16 (a rank-r adapter: h = x A^T, dh = g B, dB = g^T h, dA = dh^T x, and
-    A x^T) runs as one launch that splits the reduction over the wavefronts of a workgroup: every operand
-    layout of those products, ragged P, R and Q (Q not a multiple of the 32-wide step, P not of the
-    16-row tile), addmm's bias x alpha/beta, accumulation in place through the C ABI, and run-to-run
-    identity, against float64."""
+    A x^T) runs as one launch that splits the reduction over the wavefronts of a workgroup (and, for long
+    reductions over few rows, over K slices added by a second kernel): every operand layout of those
+    products, ragged P, R and Q (Q not a multiple of the 32-wide step, P not of the 16-row tile), addmm's
+    bias x alpha/beta, accumulation in place through the C ABI, and run-to-run identity, against float64."""
     if form == "x_At":     # X [P, Q] q-contiguous, Y = A^T read along q
         x, w = randn((p, q), dt, 51), randn((r, q), dt, 52, 0.1)
         mk = lambda X, W: (X, W.mT)
