@@ -847,11 +847,22 @@ __global__ __launch_bounds__(512) void attn_dkdv_w32(hrt_attn_args p, int nkb) {
     HK_L uint8_t* const odst = COPY ? (BUF ? O0 : O1) + j0 * 1024 : sink;
     const int dstep = COPY ? 1024 : 0;
     constexpr int RPI = 64 / NCH;
+    // Lane offsets of this stage's copies (dma_lane_offsets, in fewer instructions): j0 is a multiple of the
+    // swizzle period (16 rows), and the swizzle is linear in the row bits, so instruction i's offset is
+    // rsub ss + ((slot ^ swz(rsub) ^ swz(i RPI)) << 4), the last term a constant
+    static_assert((IPW * RPI) % 16 == 0, "copy blocks start on a swizzle period");
     DmaLanes qlo, olo;
     {
       const int ln = opaque(lane);
-      qlo = dma_lane_offsets<NCH>(qss, ln, j0);
-      olo = dma_lane_offsets<NCH>(oss, ln, j0);
+      const int rsub = ln / NCH;
+      const uint32_t x0 = (uint32_t)(((ln % NCH) ^ tile_swz<NCH>(rsub)) << 4);
+      const uint32_t bq = (uint32_t)rsub * qss, bo = (uint32_t)rsub * oss;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t x = x0 ^ (uint32_t)(tile_swz<NCH>(i * RPI) << 4);
+        qlo.off[i] = bq + x;
+        olo.off[i] = bo + x;
+      }
     }
     // S and dP products of d step ks; their operands (Q, dO, V rows) are read RA1 steps ahead into a ring,
     // each step fenced by sched_barrier
@@ -887,17 +898,19 @@ __global__ __launch_bounds__(512) void attn_dkdv_w32(hrt_attn_args p, int nkb) {
       dp[e] *= s[e];
     }
     // B-operand column reads: rows 4 h + (l16 >> 2) and +8, columns 32 n + 16 ((lane >> 4) & 1) + 4 (l16 & 3)
+    // (column block n adds 4 n to a chunk index below 4, which enters the swizzle XOR on bits of its own:
+    // block n's offset is block 0's with bits 6-7 flipped by n)
     int toff[DCH][2];
     {
       const int ln = opaque(lane);
 #pragma unroll
-      for (int n = 0; n < DCH; ++n)
+      for (int t = 0; t < 2; ++t) {
+        const int row = 8 * t + 4 * (ln >> 5) + ((ln & 15) >> 2);
+        const int c0 = 2 * ((ln >> 4) & 1) + ((ln >> 1) & 1);
+        toff[0][t] = tile_off<NCH>(row, c0) + (ln & 1) * 8;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int row = 8 * t + 4 * (ln >> 5) + ((ln & 15) >> 2);
-          const int c = 4 * n + 2 * ((ln >> 4) & 1) + ((ln >> 1) & 1);
-          toff[n][t] = tile_off<NCH>(row, c) + (ln & 1) * 8;
-        }
+        for (int n = 1; n < DCH; ++n) toff[n][t] = toff[0][t] ^ (n << 6);
+      }
     }
     const u32x4 pa0 = pack_slots<T>(s, 0, 1), pa1 = pack_slots<T>(s, 2, 3);
     const u32x4 da0 = pack_slots<T>(dp, 0, 1), da1 = pack_slots<T>(dp, 2, 3);
