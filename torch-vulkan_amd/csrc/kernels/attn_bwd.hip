@@ -556,8 +556,9 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
     constexpr int BUF = decltype(bc)::value;
     constexpr bool COPY = decltype(cc)::value;
     const int64_t key0 = (int64_t)st * KST2;
-    const HK_G uint8_t* ksrc = Kb + stage_origin<KST2>(st + 1, nst, Sk) * kss;
-    const HK_G uint8_t* vsrc = Vb + stage_origin<KST2>(st + 1, nst, Sk) * vss;
+    // buffer resources over the next stage's first rows (scalar row offsets, no 64-bit address arithmetic)
+    const __amdgpu_buffer_rsrc_t krs = dma_rsrc(Kb + stage_origin<KST2>(st + 1, nst, Sk) * kss);
+    const __amdgpu_buffer_rsrc_t vrs = dma_rsrc(Vb + stage_origin<KST2>(st + 1, nst, Sk) * vss);
     const HK_L uint8_t* Kt = BUF ? K1 : K0;
     const HK_L uint8_t* Vt = BUF ? V1 : V0;
     // S^T, dP^T of d step ks; their A operands (K, V rows) are read RA1 steps ahead into a ring, each step
@@ -578,8 +579,8 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
       s = Mfma32<T>::mac(kr[ks % (RA1 + 1)], qf[ks], s);
       dp = Mfma32<T>::mac(vr[ks % (RA1 + 1)], df[ks], dp);
       if constexpr (COPY) {
-        if (ks < IPW) dma_tile_part<NCH, KST2, NW>(ksrc, kss, BUF ? K0 : K1, wave, klo, ks);
-        else if (ks < 2 * IPW) dma_tile_part<NCH, KST2, NW>(vsrc, vss, BUF ? V0 : V1, wave, vlo, ks - IPW);
+        if (ks < IPW) dma_tile_part_rs<NCH, KST2, NW>(krs, kss, BUF ? K0 : K1, wave, klo, ks);
+        else if (ks < 2 * IPW) dma_tile_part_rs<NCH, KST2, NW>(vrs, vss, BUF ? V0 : V1, wave, vlo, ks - IPW);
       }
     }
     __builtin_amdgcn_sched_barrier(0);

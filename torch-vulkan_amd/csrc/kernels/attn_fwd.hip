@@ -353,8 +353,10 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
     constexpr int NK = MODE == 2 ? IPW : 0;    // K copies of this stage
     const float nm = m == -INFINITY ? 0.f : -m;
     if constexpr (COPY) {
-      const HK_G uint8_t* ksrc = Kb + stage_origin<KST>(st + 2, nst, Sk) * kss;
-      const HK_G uint8_t* vsrc = Vb + stage_origin<KST>(st + 1, nst, Sk) * vss;
+      // buffer resources over the stages' first rows: a copy then takes its row offset in a scalar register
+      // and its lane offset as is, with no per-copy 64-bit address arithmetic
+      const __amdgpu_buffer_rsrc_t krs = dma_rsrc(Kb + stage_origin<KST>(st + 2, nst, Sk) * kss);
+      const __amdgpu_buffer_rsrc_t vrs = dma_rsrc(Vb + stage_origin<KST>(st + 1, nst, Sk) * vss);
       // S(st+1) with this iteration's copies placed after its MFMAs, one per MFMA, then P(st); the VALU
       // work of P(st) is interleaved with the MFMAs by sched_group_barrier
       const HK_L uint8_t* Kt = BUF ? K0 : K1;
@@ -365,8 +367,8 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
 #pragma unroll
       for (int ks = 0; ks < 2 * DCH; ++ks) {
         sn = Mfma32<T>::mac(kfr[ks], qf[ks], sn);
-        if (ks < NK) dma_tile_part<NCH, KST, NW>(ksrc, kss, BUF ? K1 : K0, wave, klo, ks);
-        else if (ks < NK + IPW) dma_tile_part<NCH, KST, NW>(vsrc, vss, BUF ? V0 : V1, wave, vlo, ks - NK);
+        if (ks < NK) dma_tile_part_rs<NCH, KST, NW>(krs, kss, BUF ? K1 : K0, wave, klo, ks);
+        else if (ks < NK + IPW) dma_tile_part_rs<NCH, KST, NW>(vrs, vss, BUF ? V0 : V1, wave, vlo, ks - NK);
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
