@@ -673,9 +673,10 @@ __global__ __launch_bounds__(512) void attn_dq_dma(hrt_attn_args p, int nqb) {
       const int qq = ps * 8 + (lane >> 3);
       const f32x4 v = *reinterpret_cast<const f32x4*>(area + qq * 36 + c4);
       const int64_t qrow = qb * 64 + g * 32 + qq;
+      const float v4[4] = {v[0], v[1], v[2], v[3]};
       if (qrow < Sq)
         *reinterpret_cast<HK_G u32x2*>(gptr<uint16_t>(p.dq) + grad_row(p, b, hh, qrow, Sq, p.q_sb, p.q_sh, p.q_ss) + N * 32 + c4) =
-            u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+            pack4<T>(v4);
     }
   };
   switch (kq) {
@@ -1021,9 +1022,10 @@ __global__ __launch_bounds__(512) void attn_dkdv_w32(hrt_attn_args p, int nkb) {
         const f32x4 x = *reinterpret_cast<const f32x4*>(ar + key * 40 + c8);
         const f32x4 y = *reinterpret_cast<const f32x4*>(ar + key * 40 + c8 + 4);
         const int64_t kk = kb * 64 + kg * 32 + key;
+        const float o8[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
         if (kk < Sk)
           *reinterpret_cast<HK_G u32x4*>(gptr<uint16_t>(dst_base) + grad_row(p, b, hh, kk, Sk, g_sb, g_sh, g_ss) + n * 32 + c8) =
-              u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+              pack8<T>(o8);
       }
     }
   };

@@ -505,7 +505,8 @@ __global__ __launch_bounds__(512) void attn_fwd_dma(hrt_attn_args p, int nqb) {
       const int64_t qrow = qb * 64 + g * 32 + qq;
       if (qrow < Sq) {
         const int64_t off = ((b * Sq + qrow) * p.H + hh) * p.D + N * 32 + c4;
-        *reinterpret_cast<HK_G u32x2*>(gptr<typename T::storage>(p.o) + off) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+        const float v4[4] = {v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<HK_G u32x2*>(gptr<typename T::storage>(p.o) + off) = pack4<T>(v4);
         if (p.o32) *reinterpret_cast<HK_G f32x4*>(gptr<float>(p.o32) + off) = v;
       }
     }

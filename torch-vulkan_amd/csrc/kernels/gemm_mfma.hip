@@ -289,7 +289,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x4 (&acc)[BM / WM / 16][B
       } else {
         HK_G uint16_t* c = C + gm * c_sm + gn * c_sn;
         if (full && c_sn == 1 && ((uint64_t)c & 15) == 0) {
-          *reinterpret_cast<HK_G u32x4*>(c) = u32x4{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3]), pack2<T>(o[4], o[5]), pack2<T>(o[6], o[7])};
+          *reinterpret_cast<HK_G u32x4*>(c) = pack8<T>(o);
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
@@ -741,8 +741,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void mm_dma(hrt_mm_args
         *reinterpret_cast<HK_G f32x4*>(C32 + off) = x;
         *reinterpret_cast<HK_G f32x4*>(C32 + off + 4) = y;
       } else {
-        *reinterpret_cast<HK_G u32x4*>(C + off) =
-            u32x4{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3])};
+        const float o8[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+        *reinterpret_cast<HK_G u32x4*>(C + off) = pack8<T>(o8);
       }
     }
   }

@@ -31,22 +31,6 @@ __device__ __forceinline__ float dot2<F16>(uint32_t x, uint32_t y, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x), __builtin_bit_cast(h2, y), acc, false);
 }
 
-// Eight outputs to a 16-byte vector of T: bf16 through the hardware conversion unless a value is NaN (then
-// the contract's rounding, every NaN -> 0x7FC0), f16 through the hardware conversion.
-template <typename T>
-__device__ __forceinline__ u32x4 pack8(const float* v) {
-  if constexpr (std::is_same<T, BF16>::value) {
-    float t = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t += v[e];
-    return t == t ? bf16_pack8_hw(v) : bf16_pack8_sw(v);
-  } else {
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = pack2<T>(v[2 * i], v[2 * i + 1]);
-    return r;
-  }
-}
 template <typename T>
 __device__ __forceinline__ void unpack8(u32x4 w, float* v) {
 #pragma unroll

@@ -9,6 +9,8 @@
 // and read with one 128-bit ds_read per fragment.
 #pragma once
 
+#include <type_traits>
+
 #include "device_common.h"
 
 namespace hk {
@@ -59,10 +61,30 @@ __device__ __forceinline__ uint32_t cvt2<F16>(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
 }
 
-// Convert 8 fp32 values to 8 packed 16-bit values of type T (round to nearest even).
+// Convert 8 (4) fp32 values to packed 16-bit values of type T with the contract's rounding (round to nearest
+// even; bf16: every NaN -> 0x7FC0).  bf16 goes through the hardware conversion (one v_cvt_pk_bf16_f32 per
+// pair, bit-identical to the software rounding for every non-NaN value) unless the values' sum is NaN,
+// i.e. unless one of them is a NaN (or an inf - inf pair, which the software path rounds the same anyway);
+// f16 converts in hardware with its own NaN fix-up.
 template <typename T>
 __device__ __forceinline__ u32x4 pack8(const float* v) {
-  return u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
+  if constexpr (std::is_same<T, BF16>::value) {
+    float t = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t += v[e];
+    return t == t ? bf16_pack8_hw(v) : bf16_pack8_sw(v);
+  } else {
+    return u32x4{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]), pack2<T>(v[6], v[7])};
+  }
 }
+template <typename T>
+__device__ __forceinline__ u32x2 pack4(const float* v) {
+  if constexpr (std::is_same<T, BF16>::value) {
+    const float t = (v[0] + v[1]) + (v[2] + v[3]);
+    if (t == t) return u32x2{cvt2<T>(v[0], v[1]), cvt2<T>(v[2], v[3])};
+  }
+  return u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+}
+
 
 }  // namespace hk
