@@ -621,7 +621,7 @@ class Bench:
         dxs = [torch.empty_like(x) for x in xs]
         mu = torch.empty(R, dtype=torch.float32, device=self.dev)
         rs = torch.empty(R, dtype=torch.float32, device=self.dev)
-        ws = torch.empty((self.abi.ln_chunks(R), 2, D), dtype=torch.float32, device=self.dev)
+        ws = torch.empty((self.abi.ln_chunks(R, D), 2, D), dtype=torch.float32, device=self.dev)
         dw, db = torch.empty(D, dtype=bf, device=self.dev), torch.empty(D, dtype=bf, device=self.dev)
 
         def fa(i):

@@ -244,7 +244,7 @@ typedef struct hrt_softmax_args {
  *                   y = (x-mean)*rstd*w + b   (w, b optional = 0); mean, rstd fp32 [rows].
  *  "ln_bwd_{dt}":   dx = rstd*(gw - mean(gw) - xhat*mean(gw*xhat)), gw = g*w, xhat = (x-mean)*rstd
  *                   (dx optional); when ws != 0 also writes per-chunk partial sums of g*xhat and g to
- *                   ws = fp32 [hrt_ln_chunks(rows)][2][D], and when dw or db is also given, queues the
+ *                   ws = fp32 [hrt_ln_chunks(rows, D)][2][D], and when dw or db is also given, queues the
  *                   "ln_wgrad_{dt}" reduction of them right behind (one call for dx, dw and db).  dw / db
  *                   without ws is an error.
  *  "ln_wgrad_{dt}": dw[d] = sum over chunks of ws[c][0][d], db[d] = sum of ws[c][1][d] (each optional). */
@@ -256,11 +256,18 @@ typedef struct hrt_ln_args {
   uint32_t pad;
 } hrt_ln_args;
 
-/* Row chunking of the layer_norm weight-gradient partial sums: 4 rows per chunk (one workgroup of four
- * wavefronts, one row each). */
-static inline int64_t hrt_ln_rows_per_chunk(int64_t rows) { return rows > 0 ? 4 : 1; }
-static inline int64_t hrt_ln_chunks(int64_t rows) {
-  int64_t r = hrt_ln_rows_per_chunk(rows);
+/* Row chunking of the layer_norm weight-gradient partial sums.  A chunk is one workgroup of the backward
+ * (one wavefront per row) and writes 2 D fp32 sums: a third of the bf16 bytes of its rows' x, g and dx at
+ * 4 rows, a sixth at 8, a twelfth at 16.  The chunk doubles from 4 rows while it holds at least 8192
+ * elements, at least 128 chunks remain and its rows of fp32 (staged in LDS to be added) fit in 128 KiB
+ * (short rows keep more, smaller workgroups: [1024, 1024] is faster with 4-row chunks). */
+static inline int64_t hrt_ln_rows_per_chunk(int64_t rows, int64_t D) {
+  int64_t r = 4;
+  while (r < 16 && r * D >= 8192 && rows >= 256 * r && 2 * r * D * 4 <= 131072) r *= 2;
+  return r;
+}
+static inline int64_t hrt_ln_chunks(int64_t rows, int64_t D) {
+  int64_t r = hrt_ln_rows_per_chunk(rows, D);
   return (rows + r - 1) / r;
 }
 
@@ -270,8 +277,9 @@ static inline int64_t hrt_ln_chunks(int64_t rows) {
  * (code recorded into a HIP graph, tight serving loops, harnesses that forbid hipMalloc).  The caller
  * passes inputs and outputs as for "ln_bwd_{dt}" with ws = 0; the per-chunk partial sums of dw / db go to a
  * file-scope device array of HRT_LN_SCRATCH_BYTES that the library holds on each GPU until the process
- * ends.  Its size bounds the problem: hrt_ln_chunks(rows) * 2 * D * 4 bytes must fit (rows * D up to about
- * 4 Mi elements, e.g. [1024, 2048] or [2048, 2048]) whenever dw or db is requested; larger calls fail with
+ * ends.  Its size bounds the problem: hrt_ln_chunks(rows, D) * 2 * D * 4 bytes must fit (rows * D up to
+ * 4 Mi elements with 4-row chunks, 8 Mi with 8-row chunks, e.g. [1024, 2048], [1024, 4096] or
+ * [2048, 4096]) whenever dw or db is requested; larger calls fail with
  * an error and queue nothing.  dx alone needs no scratch and has no such limit.  Every call writes the
  * partial sums before reading them, so nothing needs clearing; calls on the runtime's one stream run in
  * order, but work that overlaps on one GPU (a recorded graph replayed beside another call) shares the array

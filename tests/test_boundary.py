@@ -162,6 +162,10 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in py._fields_:
             lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    ln_shapes = [(1, 1), (5, 7), (1023, 2048), (1024, 2048), (1024, 4096), (1024, 8192), (2048, 2048), (4096, 2048),
+                 (4096, 4096), (100000, 64), (3, 5000)]
+    for rows, D in ln_shapes:
+        lines.append(f'  printf("ln_chunks {rows}x{D} %lld\\n", (long long)hrt_ln_chunks({rows}, {D}));')
     lines.append("  return 0; }")
     src = tmp_path / "layout.c"
     src.write_text("\n".join(lines))
@@ -173,7 +177,9 @@ def test_python_abi_structs_match_the_c_headers(tmp_path):
         assert got[(cname, "size")] == ctypes.sizeof(py), cname
         for fname, _ in py._fields_:
             assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
-    assert abi.ln_chunks(1024) == 256 and abi.ln_chunks(5) == 2
+    for rows, D in ln_shapes:  # the Python mirror of the chunking rule computes what the header does
+        assert got[("ln_chunks", f"{rows}x{D}")] == abi.ln_chunks(rows, D), (rows, D)
+    assert abi.ln_chunks(1024, 2048) == 128 and abi.ln_chunks(4096, 2048) == 256 and abi.ln_chunks(5, 7) == 2
 
 
 def test_conv3_sizes_and_splits_match_the_c_header(tmp_path):

@@ -135,7 +135,7 @@ def test_layer_norm_stats_are_fp32_with_reference_shape():
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("affine", [False, True])
-@pytest.mark.parametrize("rows,D", [(6, 96), (10, 2048), (5, 5000)])
+@pytest.mark.parametrize("rows,D", [(6, 96), (10, 2048), (5, 5000), (1030, 2048)])
 def test_layer_norm_backward(dt, affine, rows, D):
     x = randn((rows, D), dt, scale=2.0)
     w = randn((D,), dt, 1) if affine else None
@@ -184,16 +184,18 @@ def _ln_bwd_args(x, g, w, mean, rstd, dx, dw, db, ws):
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,D,affine", [(1024, 2048, True), (1021, 2048, True), (37, 512, False), (13, 1000, True),
-                                           (2, 4096, True), (300, 200, True)])
+                                           (2, 4096, True), (300, 200, True), (2100, 2048, True), (4096, 2048, False),
+                                           (1500, 4096, True), (1024, 1024, True)])
 def test_layer_norm_backward_one_call_matches_two(dt, rows, D, affine):
     """"ln_bwd" given dw / db also reduces the partial sums (one call for dx, dw, db, as the shim queues it);
     it must give the bits of "ln_bwd" followed by "ln_wgrad", on ragged row counts, rows off the full-chunk
-    path and without affine parameters, and two calls in a row on different inputs must each see their own
-    partial sums."""
+    path and without affine parameters, with chunks of 4, 8 and 16 rows (8 from 1024 rows, 16 from 2048 when
+    16 rows of D floats fit 128 KiB: (2100, 2048) and (4096, 2048); (1500, 4096) stays at 8, (1024, 1024)
+    at 4), and two calls in a row on different inputs must each see their own partial sums."""
     from torch_vulkan import abi
     rt = abi.Runtime()
     kind = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dt]
-    chunks = abi.ln_chunks(rows)
+    chunks = abi.ln_chunks(rows, D)
     outs = []
     for seed in (5, 6):
         gen = torch.Generator().manual_seed(seed * 1000 + rows)

@@ -46,7 +46,7 @@ def _args(x, gy, w, mean, rstd, dx, dw, db, ws=0):
 def _allocating(rt, dtype, x, gy, w, mean, rstd):
     rows, D = x.shape
     dx, dw, db = torch.empty_like(x), torch.empty(D, dtype=dtype, device=DEV), torch.empty(D, dtype=dtype, device=DEV)
-    ws = torch.empty(abi.ln_chunks(rows) * 2 * D, dtype=torch.float32, device=DEV)
+    ws = torch.empty(abi.ln_chunks(rows, D) * 2 * D, dtype=torch.float32, device=DEV)
     a = _args(x, gy, w, mean, rstd, dx, dw, db, ws.data_ptr())
     rt.dispatch(f"ln_bwd_{KIND[dtype]}", a)
     rt.dispatch(f"ln_wgrad_{KIND[dtype]}", a)
@@ -96,8 +96,8 @@ def test_noalloc_without_affine_and_dx_only():
 
 def test_noalloc_rejects_what_it_cannot_serve():
     rt = abi.Runtime()
-    rows, D = 4096, 2048  # 1024 chunks x 16 KiB = 16 MiB of partial sums > the 8 MiB array
-    assert abi.ln_chunks(rows) * 2 * D * 4 > abi.LN_SCRATCH_BYTES
+    rows, D = 4096, 4096  # 512 chunks of 8 rows x 32 KiB = 16 MiB of partial sums > the 8 MiB array
+    assert abi.ln_chunks(rows, D) * 2 * D * 4 > abi.LN_SCRATCH_BYTES
     x = torch.zeros(rows, D, dtype=torch.bfloat16, device=DEV)
     stats = torch.zeros(rows, dtype=torch.float32, device=DEV)
     dw = torch.empty(D, dtype=torch.bfloat16, device=DEV)

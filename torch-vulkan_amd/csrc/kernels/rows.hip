@@ -17,6 +17,7 @@ namespace hk {
 namespace {
 
 constexpr int kMaxNV = 8;  // 16-byte vectors per lane on the register path
+constexpr size_t kLnLds = 128 * 1024;  // LDS bytes the layer_norm backward may stage its chunk's rows in
 
 // Load / store 16 bytes as float values.
 template <typename T>
@@ -456,12 +457,22 @@ __global__ __launch_bounds__(256) void ln_fwd_row(const typename T::storage* __r
   }
 }
 
-// Backward, register path: one chunk of 4 rows per workgroup, one wavefront per row.  dx per row; with ws,
-// the chunk's column sums of g*xhat and g (its 4 rows added through LDS: every wavefront stores its row,
-// then each thread sums the 4 rows of its columns) as ws row pair `chunk`.  With `both` (8 D floats of
-// LDS) the two quantities are staged together behind one barrier, else one after the other (three
-// barriers).  HW: weight present.
-template <typename T, int NV, bool FULL, bool HW>
+// Partial sums go out as streaming stores: read once, by the column reduction (2-4% faster than cached
+// stores, whose dirty lines the end of the launch must write back).
+__device__ __forceinline__ void ws_store(float* p, f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p)); }
+// Sum of N consecutive rows of D floats (four positions from b) in a fixed tree: ((r0 + r1) + (r2 + r3)) + ...
+template <int N>
+__device__ __forceinline__ f32x4 rows_tree(const float* b, int64_t D) {
+  if constexpr (N == 1) return *reinterpret_cast<const f32x4*>(b);
+  else return rows_tree<N / 2>(b, D) + rows_tree<N / 2>(b + (N / 2) * D, D);
+}
+
+// Backward, register path: one chunk of RPC rows per workgroup, one wavefront per row.  dx per row; with
+// ws, the chunk's column sums of g*xhat and g (its RPC rows added through LDS: every wavefront stores its
+// row, then each thread sums the RPC rows of its columns in a fixed tree) as ws row pair `chunk`.  With
+// `both` (2 RPC D floats of LDS) the two quantities are staged together behind one barrier, else one after
+// the other (three barriers).  HW: weight present.
+template <typename T, int NV, bool FULL, bool HW, int RPC>
 __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restrict__ x, const typename T::storage* __restrict__ g,
                                              const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
                                              const typename T::storage* __restrict__ w, typename T::storage* __restrict__ dx,
@@ -469,7 +480,7 @@ __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restri
                                              bool both) {
   constexpr int V = Vec<T>::N;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row0 = chunk * 4 + wave;
+  const int64_t row0 = chunk * RPC + wave;
   const bool live = row0 < rows;
   const int64_t row = live ? row0 : rows - 1;  // a row past the end loads the last row; its terms are zeroed
   // every load issued before the first use, with no branch between them, and pinned there by the empty asm
@@ -543,7 +554,7 @@ __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restri
   if (!ws) return;  // uniform across the workgroup: no barrier below is skipped by only some waves
   // rows past the end and lanes past the row hold zeros (xh = gv = 0 above)
   float* out = ws + chunk * 2 * D;
-  if (both) {  // part holds [2][4 rows][D]: both quantities staged, one barrier
+  if (both) {  // part holds [2][RPC rows][D]: both quantities staged, one barrier
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
       const int64_t col = (int64_t)(c * 64 + lane) * V;
@@ -553,16 +564,14 @@ __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restri
         for (int e = 0; e < V; ++e) o[e] = gv[c][e] * xh[c][e];
         Vec<F32>::store(part + wave * D + col, o);
         if constexpr (V == 8) Vec<F32>::store(part + wave * D + col + 4, o + 4);
-        Vec<F32>::store(part + (4 + wave) * D + col, gv[c]);
-        if constexpr (V == 8) Vec<F32>::store(part + (4 + wave) * D + col + 4, gv[c] + 4);
+        Vec<F32>::store(part + (RPC + wave) * D + col, gv[c]);
+        if constexpr (V == 8) Vec<F32>::store(part + (RPC + wave) * D + col + 4, gv[c] + 4);
       }
     }
     __syncthreads();
-    for (int64_t i = (int64_t)threadIdx.x * 4; i < 2 * D; i += 256 * 4) {  // i: position in the 2D-wide ws row
-      const float* b = part + (i < D ? i : 3 * D + i);  // quantity 1 starts at 4 D in part, at D in the ws row
-      const f32x4 r0 = *reinterpret_cast<const f32x4*>(b), r1 = *reinterpret_cast<const f32x4*>(b + D);
-      const f32x4 r2 = *reinterpret_cast<const f32x4*>(b + 2 * D), r3 = *reinterpret_cast<const f32x4*>(b + 3 * D);
-      *reinterpret_cast<f32x4*>(out + i) = (r0 + r1) + (r2 + r3);
+    for (int64_t i = (int64_t)threadIdx.x * 4; i < 2 * D; i += 64 * RPC * 4) {  // i: position in the 2D-wide ws row
+      const float* b = part + (i < D ? i : (RPC - 1) * D + i);  // quantity 1 starts at RPC D in part, at D in the ws row
+      ws_store(out + i, rows_tree<RPC>(b, D));
     }
     return;
   }
@@ -581,23 +590,20 @@ __device__ __forceinline__ void ln_bwd_chunk(const typename T::storage* __restri
       }
     }
     __syncthreads();
-    for (int64_t i = (int64_t)threadIdx.x * 4; i < D; i += 256 * 4) {
-      const f32x4 r0 = *reinterpret_cast<const f32x4*>(part + i), r1 = *reinterpret_cast<const f32x4*>(part + D + i);
-      const f32x4 r2 = *reinterpret_cast<const f32x4*>(part + 2 * D + i), r3 = *reinterpret_cast<const f32x4*>(part + 3 * D + i);
-      *reinterpret_cast<f32x4*>(out + qn * D + i) = (r0 + r1) + (r2 + r3);
-    }
+    for (int64_t i = (int64_t)threadIdx.x * 4; i < D; i += 64 * RPC * 4)
+      ws_store(out + qn * D + i, rows_tree<RPC>(part + i, D));
   }
 }
 
-template <typename T, int NV, bool FULL, bool HW>
-__global__ __launch_bounds__(256) void ln_bwd_reg(const typename T::storage* __restrict__ x,
-                                                  const typename T::storage* __restrict__ g,
-                                                  const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
-                                                  const typename T::storage* __restrict__ w,
-                                                  typename T::storage* __restrict__ dx, float* __restrict__ ws, int64_t rows,
-                                                  int64_t D, bool both) {
-  extern __shared__ float part[];  // [4 rows][D] or [2][4 rows][D] (both) when ws != nullptr
-  ln_bwd_chunk<T, NV, FULL, HW>(x, g, mean_in, rstd_in, w, dx, ws, rows, D, blockIdx.x, part, both);
+template <typename T, int NV, bool FULL, bool HW, int RPC>
+__global__ __launch_bounds__(64 * RPC) void ln_bwd_reg(const typename T::storage* __restrict__ x,
+                                                       const typename T::storage* __restrict__ g,
+                                                       const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+                                                       const typename T::storage* __restrict__ w,
+                                                       typename T::storage* __restrict__ dx, float* __restrict__ ws,
+                                                       int64_t rows, int64_t D, bool both) {
+  extern __shared__ float part[];  // [RPC rows][D] or [2][RPC rows][D] (both) when ws != nullptr
+  ln_bwd_chunk<T, NV, FULL, HW, RPC>(x, g, mean_in, rstd_in, w, dx, ws, rows, D, blockIdx.x, part, both);
 }
 
 // Sum over chunks of one column of the per-chunk partial sums (src = the column's value in chunk 0, stride
@@ -633,17 +639,17 @@ __device__ __forceinline__ float combine_groups16(const float* sp) {
   return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
 }
 
-// Backward, generic path: workgroup per chunk of 4 rows; ws accumulated in place (each thread owns its
+// Backward, generic path: workgroup per chunk of RPC rows; ws accumulated in place (each thread owns its
 // columns, so the read-modify-write has no races).
-template <typename T>
+template <typename T, int RPC>
 __global__ __launch_bounds__(256) void ln_bwd_row(const typename T::storage* __restrict__ x, const typename T::storage* __restrict__ g,
                                                   const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
                                                   const typename T::storage* __restrict__ w, typename T::storage* __restrict__ dx,
                                                   float* __restrict__ ws, int64_t rows, int64_t D) {
   __shared__ float red[4];
   float* pw = ws ? ws + (int64_t)blockIdx.x * 2 * D : nullptr;
-  for (int rr = 0; rr < 4; ++rr) {
-    const int64_t row = (int64_t)blockIdx.x * 4 + rr;
+  for (int rr = 0; rr < RPC; ++rr) {
+    const int64_t row = (int64_t)blockIdx.x * RPC + rr;
     if (row >= rows) {
       if (pw && rr == 0)
         for (int64_t i = threadIdx.x; i < 2 * D; i += 256) pw[i] = 0.f;
@@ -799,10 +805,12 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const auto& a = *static_cast<const hrt_ln_args*>(p);
   if (a.rows < 0 || a.D <= 0) return ctx.fail("bad shape");
   if (a.rows == 0) return true;
-  if (hrt_ln_rows_per_chunk(a.rows) != 4) return ctx.fail("ln chunking mismatch");
+  // chunks of the partial-sum rule when ws is given; dx alone runs 4-row workgroups (more of them)
+  const int rpc = a.ws ? (int)hrt_ln_rows_per_chunk(a.rows, a.D) : 4;
+  if (rpc != 4 && rpc != 8 && rpc != 16) return ctx.fail("ln chunking mismatch");
   using S = typename T::storage;
   const uint64_t bytes = (uint64_t)(a.rows * a.D) * sizeof(S);
-  const int64_t chunks = hrt_ln_chunks(a.rows);
+  const int64_t chunks = hrt_ln_chunks(a.rows, a.D);
   const bool wgrad = a.ws && (a.dw || a.db);
   if ((a.dw || a.db) && !a.ws) return ctx.fail("dw / db need the partial-sum workspace ws");
   if (!ctx.check(a.x, bytes, "x") || !ctx.check(a.g, bytes, "g") || !ctx.check(a.mean, a.rows * 4, "mean") ||
@@ -816,17 +824,26 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   const float *mu = (const float*)a.mean, *rs = (const float*)a.rstd;
   int nv = reg_nv<T>(a.D, {a.x, a.g, a.w, a.dx});
   const auto full_row = [&](int v) { return a.D == (int64_t)v * 64 * Vec<T>::N; };  // rows fill every chunk: no column guards
-  const bool both = ws && (size_t)(8 * a.D) * 4 <= 64 * 1024;
-  const size_t lds = ws ? (size_t)((both ? 8 : 4) * a.D) * 4 : 0;
-  if (lds > 64 * 1024 || a.D % 4) nv = 0;
-  const dim3 grid((uint32_t)chunks);
-  auto go = [&](auto nvc, auto fullc, auto hwc) {
-    hipLaunchKernelGGL((ln_bwd_reg<T, decltype(nvc)::value, decltype(fullc)::value, decltype(hwc)::value>), grid, dim3(256),
-                       lds, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D, both);
+  const bool both = ws && (size_t)(2 * rpc * a.D) * 4 <= kLnLds;
+  const size_t lds = ws ? (size_t)((both ? 2 * rpc : rpc) * a.D) * 4 : 0;
+  if (lds > kLnLds || a.D % 4) nv = 0;
+  const dim3 grid((uint32_t)cdiv(a.rows, rpc));  // = chunks when ws is given
+  auto go = [&](auto nvc, auto fullc, auto hwc, auto rpcc) {
+    constexpr int RPC = decltype(rpcc)::value, NV = decltype(nvc)::value;
+    if constexpr (RPC == 16 && NV * Vec<T>::N > 32)  // D > 2048: 16 rows of D floats exceed kLnLds, never chosen
+      hipLaunchKernelGGL((ln_bwd_row<T, 16>), grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
+    else
+      hipLaunchKernelGGL((ln_bwd_reg<T, NV, decltype(fullc)::value, decltype(hwc)::value, RPC>), grid, dim3(64 * RPC), lds,
+                         ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D, both);
+  };
+  auto by_rpc = [&](auto nvc, auto fullc, auto hwc) {
+    if (rpc == 4) go(nvc, fullc, hwc, std::integral_constant<int, 4>());
+    else if (rpc == 8) go(nvc, fullc, hwc, std::integral_constant<int, 8>());
+    else go(nvc, fullc, hwc, std::integral_constant<int, 16>());
   };
   auto by_w = [&](auto nvc, auto fullc) {
-    if (w) go(nvc, fullc, std::true_type());
-    else go(nvc, fullc, std::false_type());
+    if (w) by_rpc(nvc, fullc, std::true_type());
+    else by_rpc(nvc, fullc, std::false_type());
   };
   auto by_full = [&](auto nvc) {
     if (full_row(decltype(nvc)::value)) by_w(nvc, std::true_type());
@@ -837,7 +854,10 @@ bool launch_ln_bwd(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
     case 2: by_full(std::integral_constant<int, 2>()); break;
     case 4: by_full(std::integral_constant<int, 4>()); break;
     case 8: by_full(std::integral_constant<int, 8>()); break;
-    default: hipLaunchKernelGGL(ln_bwd_row<T>, grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
+    default:
+      if (rpc == 4) hipLaunchKernelGGL((ln_bwd_row<T, 4>), grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
+      else if (rpc == 8) hipLaunchKernelGGL((ln_bwd_row<T, 8>), grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
+      else hipLaunchKernelGGL((ln_bwd_row<T, 16>), grid, dim3(256), 0, ctx.stream, x, g, mu, rs, w, dx, ws, a.rows, a.D);
   }
   if (!hrt::launch_ok(hipGetLastError(), ctx, "ln_bwd")) return false;
   // dw / db by the column reduction of the partial sums, queued right behind (ln_wgrad's kernel).  A single
@@ -856,7 +876,7 @@ bool launch_ln_wgrad(const void* p, const uint32_t*, hrt::LaunchCtx& ctx) {
   if (a.rows <= 0 || a.D <= 0) return ctx.fail("bad shape");
   if (!a.dw && !a.db) return true;
   using S = typename T::storage;
-  const int64_t chunks = hrt_ln_chunks(a.rows);
+  const int64_t chunks = hrt_ln_chunks(a.rows, a.D);
   if (!ctx.check(a.ws, (uint64_t)(chunks * 2 * a.D) * 4, "ws") || (a.dw && !ctx.check(a.dw, a.D * sizeof(S), "dw")) ||
       (a.db && !ctx.check(a.db, a.D * sizeof(S), "db")))
     return false;
@@ -900,7 +920,7 @@ bool ln_bwd_into_scratch(hrt_ln_args a, hrt::LaunchCtx& ctx) {
   const bool wgrad = (a.dw || a.db) && a.rows > 0;
   if (wgrad) {
     const uint64_t cap = HRT_LN_SCRATCH_BYTES, per_chunk = 2 * (uint64_t)a.D * sizeof(float);
-    const uint64_t chunks = (uint64_t)hrt_ln_chunks(a.rows);
+    const uint64_t chunks = (uint64_t)hrt_ln_chunks(a.rows, a.D);
     if (per_chunk > cap || chunks > cap / per_chunk)
       return ctx.fail("rows " + std::to_string(a.rows) + " x D " + std::to_string(a.D) + " needs " +
                       std::to_string(chunks) + " x " + std::to_string(per_chunk) +

@@ -151,7 +151,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> k_layer_norm_backward(
     A.dx = dptr(dx);
   }
   if (want_dw || want_db) {  // per-chunk column sums of g * xhat and g, reduced into dw / db by the same call
-    partial = at::empty({hrt_ln_chunks(sh->rows), 2, sh->D}, x.options().dtype(at::kFloat));
+    partial = at::empty({hrt_ln_chunks(sh->rows, sh->D), 2, sh->D}, x.options().dtype(at::kFloat));
     A.ws = dptr(partial);
     if (want_dw) dw = at::empty_like(*weight, at::MemoryFormat::Contiguous);
     if (want_db) db = at::empty_like(*bias, at::MemoryFormat::Contiguous);

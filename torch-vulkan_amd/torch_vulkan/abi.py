@@ -148,9 +148,18 @@ class Dq8Args(ctypes.Structure):
     _fields_ = [("q", u64), ("scale", u64), ("out", u64), ("rows", i64), ("cols", i64), ("nblocks", i64)]
 
 
-def ln_chunks(rows):
+def ln_rows_per_chunk(rows, D):
+    """hrt_ln_rows_per_chunk (include/hrt_ops.h): rows of one layer_norm weight-gradient chunk."""
+    r = 4
+    while r < 16 and r * D >= 8192 and rows >= 256 * r and 2 * r * D * 4 <= 131072:
+        r *= 2
+    return r
+
+
+def ln_chunks(rows, D):
     """hrt_ln_chunks (include/hrt_ops.h): partial-sum rows of the layer_norm weight gradient."""
-    return (rows + 3) // 4
+    r = ln_rows_per_chunk(rows, D)
+    return (rows + r - 1) // r
 
 
 LN_SCRATCH_BYTES = 8 << 20  # HRT_LN_SCRATCH_BYTES (include/hrt_ops.h)
