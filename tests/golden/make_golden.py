@@ -20,7 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def make_dq(rows, cols, seed):
-    # same generator recipe as the reference's tests/test_dequant_int8.py:24-29
+    """The inputs the reference's tests/test_dequant_int8.py:24-29 draws for a shape and seed (the same
+    generator calls in the same order, so the same values)."""
     g = torch.Generator().manual_seed(seed)
     q = torch.randint(-127, 128, (rows, cols), generator=g, dtype=torch.int8)
     nb = (cols + 63) // 64
@@ -29,10 +30,15 @@ def make_dq(rows, cols, seed):
 
 
 def closed_form(q, scale, dt):
-    # torch_vulkan/__init__.py:203-205, executed by torch's CPU kernels
-    cols = q.shape[1]
-    s = scale.float().repeat_interleave(64, dim=1)[:, :cols]
-    return (q.float() * s).to(dt)
+    """The closed form of torch_vulkan/__init__.py:203-205 (one float32 product per element, rounded once to
+    dt), executed by torch's CPU kernels: the row is padded to whole 64-element blocks, each block times its
+    scale."""
+    rows, cols = q.shape
+    nb = scale.shape[1]
+    blocks = torch.zeros(rows, nb * 64)
+    blocks[:, :cols] = q.float()
+    prod = blocks.view(rows, nb, 64) * scale.float().unsqueeze(-1)
+    return prod.view(rows, nb * 64)[:, :cols].to(dt)
 
 
 def bits(t):

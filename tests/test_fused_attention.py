@@ -1,8 +1,11 @@
-"""Fused scaled-dot-product attention (forward + backward) on the GPU vs the float64 oracle
-(reference tests/test_fused_attention.py:1-169).  Tolerances: relative L2 of out / dq / dk / dv below
-{f32 1e-5, bf16 1e-2, f16 4e-3} — the stricter of the reference's {3e-5, 2e-2, 4e-3} and the bounds of this
-build's target (bf16 1e-2, f32 1e-5).  Also: lse against its closed form, the [B,S,H,D]-transposed
-calling convention, large logits, fallback to the math path, the auto policy, unaligned views,
+"""Fused scaled-dot-product attention (forward + backward) on the GPU against the float64 oracle.
+
+The reference's tests/test_fused_attention.py fixes the behaviours: the fused kernels (not the bmm + softmax
+math path) give the output and the q / k / v gradients for head dimensions below, at and off the vector
+widths, ragged and cross-attention sequence lengths, batches and heads; masks and unsupported forms take the
+math path.  Tolerances: relative L2 of out / dq / dk / dv below {f32 1e-5, bf16 1e-2, f16 4e-3} — the
+stricter of the reference's {3e-5, 2e-2, 4e-3} and the bounds of this build's target.  Also: lse against its
+closed form, the [B,S,H,D]-transposed calling convention, large logits, the auto policy, unaligned views,
 special cases (Sk = 1, identical keys, zero dO) and the BASELINE shapes S = 1024 and S = 4096."""
 
 import numpy as np
@@ -18,31 +21,35 @@ pytestmark = pytest.mark.gpu
 import torch_vulkan  # noqa: E402
 
 dev = torch.device("vk")
-DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+FLOATS = [torch.float32, torch.bfloat16, torch.float16]
 REL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 4e-3}
-OVR = "aten::_scaled_dot_product_fused_attention_overrideable"
+FUSED = "aten::_scaled_dot_product_fused_attention_overrideable"  # the PrivateUse1 SDPA operator
 
 
 @pytest.fixture(autouse=True)
-def _fused_on():
+def _always_fused():
+    """The default policy ("auto") picks the path by shape; these tests pin the fused kernels, and restore
+    the default afterwards."""
     torch_vulkan.set_fused_attention("on")
     yield
     torch_vulkan.set_fused_attention("auto")
 
 
-SHAPES = [
-    (1, 1, 32, 32, 64),
-    (1, 2, 40, 50, 64),
-    (2, 3, 33, 33, 40),
-    (1, 4, 100, 77, 64),
-    (1, 2, 64, 64, 128),
-    (1, 2, 17, 5, 20),
-    (1, 2, 130, 130, 96),
-    (1, 2, 35, 37, 30),
-    (1, 1, 48, 48, 36),
-    (1, 2, 200, 300, 128),
-    (2, 2, 129, 257, 112),
-]
+# name -> (B, H, Sq, Sk, D)
+GEOMETRIES = {
+    "one key block": (1, 1, 64, 64, 64),
+    "ragged queries and keys": (1, 2, 45, 52, 64),
+    "head dim 40, batch 2": (2, 3, 39, 39, 40),
+    "77 keys (text cross-attention)": (1, 4, 90, 77, 64),
+    "head dim 128": (1, 2, 128, 128, 128),
+    "head dim 20, 6 keys": (1, 2, 19, 6, 20),
+    "several blocks, head dim 96": (1, 2, 150, 150, 96),
+    "head dim 30 (not a multiple of 4)": (1, 2, 31, 43, 30),
+    "head dim 36": (1, 1, 56, 56, 36),
+    "300 keys, head dim 128": (1, 2, 200, 300, 128),
+    "batch 2, head dim 112": (2, 2, 129, 257, 112),
+    "one query": (1, 3, 1, 70, 64),
+}
 
 
 def oracle_all(q, k, v, g, scale=None):
@@ -53,33 +60,32 @@ def oracle_all(q, k, v, g, scale=None):
     return out, lse, dq, dk, dv
 
 
-def run_vk(q, k, v, g):
-    qv, kv, vv = (t.to(dev).requires_grad_(True) for t in (q, k, v))
-    o = F.scaled_dot_product_attention(qv, kv, vv)
-    o.backward(g.to(dev))
-    return o.detach(), qv.grad, kv.grad, vv.grad
+def sdpa_with_grads(q, k, v, g):
+    """out, dq, dk, dv of F.scaled_dot_product_attention on the device for CPU inputs q, k, v and dout g."""
+    leaves = [t.to(dev).requires_grad_(True) for t in (q, k, v)]
+    out = F.scaled_dot_product_attention(*leaves)
+    grads = torch.autograd.grad(out, leaves, g.to(dev))
+    return (out.detach(), *grads)
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("shape", SHAPES)
-def test_fused_matches_oracle(shape, dtype):
-    B, H, Sq, Sk, D = shape
-    q, k, v, g = uniform((B, H, Sq, D), dtype, 1), uniform((B, H, Sk, D), dtype, 2), uniform((B, H, Sk, D), dtype, 3), \
-        uniform((B, H, Sq, D), dtype, 4)
-    ro, rlse, rq, rk, rv = oracle_all(q, k, v, g)
-    o, dq, dk, dv = run_vk(q, k, v, g)
-    assert o.dtype == dtype and dq.dtype == dtype and dk.dtype == dtype and dv.dtype == dtype
-    for name, got, ref in (("out", o, ro), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
-        assert tuple(got.shape) == ref.shape, name
-        e = oracle.rel_l2(f64(got), ref)
-        assert e < REL[dtype], f"{name} {shape} {dtype}: rel-L2 {e}"
+@pytest.mark.parametrize("name", list(GEOMETRIES))
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_fused_attention_against_the_oracle(dtype, name):
+    B, H, Sq, Sk, D = GEOMETRIES[name]
+    q, g = uniform((B, H, Sq, D), dtype, 1), uniform((B, H, Sq, D), dtype, 4)
+    k, v = uniform((B, H, Sk, D), dtype, 2), uniform((B, H, Sk, D), dtype, 3)
+    want = oracle_all(q, k, v, g)
+    got = sdpa_with_grads(q, k, v, g)
+    for what, t, r in zip(("out", "dq", "dk", "dv"), got, (want[0],) + want[2:]):
+        assert t.dtype == dtype and tuple(t.shape) == r.shape, what
+        e = oracle.rel_l2(f64(t), r)
+        assert e < REL[dtype], f"{what} {name} {dtype}: rel-L2 {e}"
     kc = torch_vulkan.kernel_counts()
-    assert kc.get(OVR, 0) >= 1 and kc.get(OVR + "_backward", 0) >= 2, kc
-    fb = torch_vulkan.fallback_counts()
-    assert not any("softmax" in n or "bmm" in n for n in fb), fb
+    assert kc.get(FUSED, 0) >= 1 and kc.get(FUSED + "_backward", 0) >= 2, kc
+    assert not [n for n in torch_vulkan.fallback_counts() if "softmax" in n or "bmm" in n]
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dtype", FLOATS)
 def test_forward_lse_matches_closed_form(dtype):
     B, H, S, D = 1, 3, 77, 64
     q, k, v = uniform((B, H, S, D), dtype, 5), uniform((B, H, S + 9, D), dtype, 6), uniform((B, H, S + 9, D), dtype, 7)
@@ -89,34 +95,33 @@ def test_forward_lse_matches_closed_form(dtype):
     assert np.allclose(f64(lse), rl, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_strided_inputs_bshd(dtype):
-    """The calling convention of real models: [B,S,H,D] tensors viewed with transpose(1, 2)."""
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_token_major_inputs_are_read_in_place(dtype):
+    """The calling convention of real models: [B,S,H,D] tensors handed over as transpose(1, 2) views."""
     B, H, S, D = 2, 4, 70, 64
-    qb, kb, vb, gb = (uniform((B, S, H, D), dtype, s) for s in (5, 6, 7, 8))
-    q, k, v, g = (t.transpose(1, 2) for t in (qb, kb, vb, gb))
+    tok = [uniform((B, S, H, D), dtype, s) for s in (5, 6, 7, 8)]
+    q, k, v, g = (t.transpose(1, 2) for t in tok)
     ro, _, rq, rk, rv = oracle_all(q, k, v, g)
-    qv, kv, vv = (t.to(dev).transpose(1, 2).detach().requires_grad_(True) for t in (qb, kb, vb))
-    gd = gb.to(dev).transpose(1, 2)
+    leaves = [t.to(dev).transpose(1, 2).detach().requires_grad_(True) for t in tok[:3]]
     torch_vulkan.reset_fallback_counts()
-    o = F.scaled_dot_product_attention(qv, kv, vv)
-    assert torch_vulkan.kernel_counts().get("aten::copy_", 0) == 0  # strided q/k/v read in place
-    o.backward(gd)
-    for name, got, ref in (("out", o, ro), ("dq", qv.grad, rq), ("dk", kv.grad, rk), ("dv", vv.grad, rv)):
-        assert oracle.rel_l2(f64(got), ref) < REL[dtype], name
-    assert o.transpose(1, 2).is_contiguous()
+    out = F.scaled_dot_product_attention(*leaves)
+    assert torch_vulkan.kernel_counts().get("aten::copy_", 0) == 0  # no copy to head-major first
+    grads = torch.autograd.grad(out, leaves, tok[3].to(dev).transpose(1, 2))
+    for what, t, r in zip(("out", "dq", "dk", "dv"), (out, *grads), (ro, rq, rk, rv)):
+        assert oracle.rel_l2(f64(t), r) < REL[dtype], what
+    assert out.transpose(1, 2).is_contiguous()  # the output comes back token-major too
 
 
 def test_large_logits_are_kept_fp32():
     B, H, S, D = 1, 2, 256, 64
-    q, k, v = uniform((B, H, S, D), torch.bfloat16, 11, 6.0), uniform((B, H, S, D), torch.bfloat16, 12, 6.0), \
-        uniform((B, H, S, D), torch.bfloat16, 13)
+    q, k = uniform((B, H, S, D), torch.bfloat16, 11, 6.0), uniform((B, H, S, D), torch.bfloat16, 12, 6.0)
+    v = uniform((B, H, S, D), torch.bfloat16, 13)
     ro, _ = oracle.attention_fwd(f64(q), f64(k), f64(v), 1 / np.sqrt(D))
     got = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev))
     assert oracle.rel_l2(f64(got), ro) < 6e-3
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dtype", FLOATS)
 @pytest.mark.parametrize("D", [64, 128])
 def test_row_max_rising_across_key_stages(dtype, D):
     """Logits that grow along the key axis by ~11 log2 units per 128 keys: every key stage raises the
@@ -140,7 +145,7 @@ def test_unsupported_shapes_use_the_math_path():
     ro, _ = oracle.attention_fwd(f64(q), f64(k), f64(v), 1 / np.sqrt(160))
     got = F.scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev))
     assert oracle.rel_l2(f64(got), ro) < 3e-5
-    assert torch_vulkan.kernel_counts().get(OVR, 0) == 0
+    assert torch_vulkan.kernel_counts().get(FUSED, 0) == 0
     mask = torch.zeros(S, S)
     mask[:, S // 2:] = float("-inf")
     q2, k2, v2 = (t[..., :64].contiguous() for t in (q, k, v))
@@ -168,7 +173,7 @@ def test_explicit_scale(scale):
             continue
         e = oracle.rel_l2(f64(got), ref)
         assert e < tol, f"{name} scale {scale}: rel-L2 {e}"
-    fused = torch_vulkan.kernel_counts().get(OVR, 0)
+    fused = torch_vulkan.kernel_counts().get(FUSED, 0)
     assert (fused >= 1) == (scale > 0), (scale, fused)
 
 
@@ -177,19 +182,19 @@ def test_auto_policy():
     q = uniform((1, 2, 64, 64), torch.float32, 41)
     torch_vulkan.reset_fallback_counts()
     got = F.scaled_dot_product_attention(q.to(dev), q.to(dev), q.to(dev))
-    assert torch_vulkan.kernel_counts().get(OVR, 0) == 0  # small f32: math path
+    assert torch_vulkan.kernel_counts().get(FUSED, 0) == 0  # small f32: math path
     ro, _ = oracle.attention_fwd(f64(q), f64(q), f64(q), 1 / 8.0)
     assert oracle.rel_l2(f64(got), ro) < 3e-5
     qb = q.to(dev, torch.bfloat16)
     F.scaled_dot_product_attention(qb, qb, qb)
-    assert torch_vulkan.kernel_counts().get(OVR, 0) == 1  # bf16: matrix-core kernel
+    assert torch_vulkan.kernel_counts().get(FUSED, 0) == 1  # bf16: matrix-core kernel
     torch_vulkan.set_fused_attention("off")
     torch_vulkan.reset_fallback_counts()
     F.scaled_dot_product_attention(qb, qb, qb)
-    assert torch_vulkan.kernel_counts().get(OVR, 0) == 0
+    assert torch_vulkan.kernel_counts().get(FUSED, 0) == 0
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dtype", FLOATS)
 def test_unaligned_views(dtype):
     B, H, S, D = 1, 2, 45, 64
     n = B * H * S * D
@@ -225,7 +230,7 @@ def test_special_cases(dtype):
 def baseline_check(S, heads_checked):
     B, H, D = 1, 16, 128
     q, k, v, g = (randn((B, H, S, D), torch.bfloat16, s) for s in (1, 2, 3, 4))
-    o, dq, dk, dv = run_vk(q, k, v, g)
+    o, dq, dk, dv = sdpa_with_grads(q, k, v, g)
     hs = slice(0, heads_checked)
     ro, _, rq, rk, rv = oracle_all(q[:, hs], k[:, hs], v[:, hs], g[:, hs])
     for name, got, ref in (("out", o, ro), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
@@ -246,7 +251,7 @@ def test_long_sequences_128_query_blocks(Sq, Sk, D):
     k, v = randn((B, H, Sk, D), dt, 72), randn((B, H, Sk, D), dt, 73)
     g = randn((B, H, Sq, D), dt, 74)
     out, lse, *_ = torch.ops.aten._scaled_dot_product_fused_attention_overrideable(q.to(dev), k.to(dev), v.to(dev), None)
-    o, dq, dk, dv = run_vk(q, k, v, g)
+    o, dq, dk, dv = sdpa_with_grads(q, k, v, g)
     assert torch.equal(o.cpu(), out.cpu())
     for h in (0, H - 1):
         hs = slice(h, h + 1)
@@ -267,7 +272,7 @@ def test_baseline_s4096_h16_d128_bf16():
     the rel-L2 bar 1e-2."""
     S, B, H, D = 4096, 1, 16, 128
     q, k, v, g = (randn((B, H, S, D), torch.bfloat16, s) for s in (1, 2, 3, 4))
-    o, dq, dk, dv = run_vk(q, k, v, g)
+    o, dq, dk, dv = sdpa_with_grads(q, k, v, g)
     hs = slice(0, 2)
     ro, _, rq, rk, rv = oracle_all(q[:, hs], k[:, hs], v[:, hs], g[:, hs])
     for name, got, ref in (("out", o, ro), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):

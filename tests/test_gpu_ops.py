@@ -1,6 +1,8 @@
-"""Transfers, views and device copies of the vk boundary (reference tests/test_gpu_ops.py:27-89): dtype
-round trips, host<->device conversion and broadcast, non-contiguous sources and destinations, storage
-offsets, device-side casts/fills, empty tensors, large transfers with memory release, resize_."""
+"""Transfers, views and device copies across the vk boundary.  The reference's tests/test_gpu_ops.py:27-89
+fix what its device must do here (round trips of every dtype, host <-> device copies with dtype conversion
+and broadcast, non-contiguous sources and destinations, storage offsets, device-side copies and casts, empty
+tensors, a large transfer whose memory is released, resize_); these tests check the same behaviours as a
+matrix of dtypes x layouts x directions, every result bit for bit against the same operation on the CPU."""
 
 import pytest
 import torch
@@ -10,44 +12,84 @@ pytestmark = pytest.mark.gpu
 import torch_vulkan  # noqa: E402
 
 dev = torch.device("vk")
+DTYPES = [torch.float32, torch.float16, torch.bfloat16, torch.int64, torch.int32, torch.int8, torch.uint8, torch.bool]
+
+
+def sample(dtype, shape, seed):
+    """Deterministic values of `dtype` with both signs (where the dtype has them), zeros and, for floats,
+    values that do not fit the narrower float types."""
+    g = torch.Generator().manual_seed(seed)
+    if dtype == torch.bool:
+        return torch.rand(shape, generator=g) < 0.5
+    if dtype.is_floating_point:
+        return ((torch.randn(shape, generator=g) * 3.0).exp() * torch.randn(shape, generator=g).sign()).to(dtype)
+    lo, hi = (0, 256) if dtype == torch.uint8 else (-128, 128) if dtype == torch.int8 else (-1000, 1000)
+    return torch.randint(lo, hi, shape, generator=g, dtype=torch.int64).to(dtype)
+
+
+def same_bits(got, ref):
+    """Equal shape, dtype and bits (so -0.0, NaN payloads and rounding all count)."""
+    assert got.shape == ref.shape and got.dtype == ref.dtype, (got.shape, ref.shape, got.dtype, ref.dtype)
+    got, ref = got.contiguous(), ref.contiguous()
+    if got.dtype.is_floating_point:
+        as_int = {8: torch.int64, 4: torch.int32, 2: torch.int16}[got.element_size()]
+        got, ref = got.view(as_int), ref.view(as_int)
+    assert torch.equal(got, ref)
+
+
+# How a [6, 10] tensor is viewed before it crosses the boundary: contiguous, transposed, a strided window,
+# a flat window at a storage offset, a broadcast row.
+LAYOUTS = {
+    "contiguous": lambda t: t,
+    "transposed": lambda t: t.t(),
+    "strided window": lambda t: t[1::2, 2::3],
+    "storage offset": lambda t: t.reshape(-1)[7:41],
+    "broadcast row": lambda t: t[2:3].expand(4, 10),
+}
 
 
 def test_runs_on_an_mi355x():
     assert "gfx950" in torch_vulkan.device_name()
 
 
-def test_roundtrip_dtypes():
-    for dt in (torch.float32, torch.float16, torch.bfloat16, torch.int64, torch.uint8, torch.bool, torch.int8, torch.int32):
-        x = (torch.rand(7, 5) * 10).to(dt)
-        assert torch.equal(x.to(dev).cpu(), x), dt
+@pytest.mark.parametrize("layout", list(LAYOUTS))
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_views_cross_the_boundary_both_ways(dtype, layout):
+    host = sample(dtype, (6, 10), seed=DTYPES.index(dtype))
+    view = LAYOUTS[layout](host)
+    same_bits(view.to(dev).cpu(), view)                   # host view -> device -> host
+    same_bits(LAYOUTS[layout](host.to(dev)).cpu(), view)  # the same view taken on the device, read back
+    same_bits(LAYOUTS[layout](host.to(dev)).clone().cpu(), view)  # device -> device copy of the view
 
 
-def test_cpu_to_vk_with_dtype_conversion_and_broadcast():
-    x = torch.arange(6, dtype=torch.float32)
-    assert torch.equal(x.to(dev).to(torch.int32).cpu(), x.to(torch.int32))
-    dst = torch.zeros(3, 4, device=dev)
-    dst.copy_(torch.tensor([1.0, 2.0, 3.0, 4.0]))
-    assert torch.equal(dst.cpu(), torch.tensor([1.0, 2.0, 3.0, 4.0]).expand(3, 4))
+@pytest.mark.parametrize("src,dst", [(torch.float32, torch.float32), (torch.float32, torch.bfloat16),
+                                     (torch.float16, torch.float32), (torch.int64, torch.float32),
+                                     (torch.float32, torch.int32), (torch.uint8, torch.int64)])
+def test_copy_into_a_device_tensor_converts_and_broadcasts(src, dst):
+    row = sample(src, (5,), seed=11)
+    ref = torch.zeros(3, 5, dtype=dst).copy_(row)
+    got = torch.zeros(3, 5, dtype=dst, device=dev)
+    got.copy_(row)                   # host row, broadcast over the device rows, converted on the way
+    same_bits(got.cpu(), ref)
+    got2 = torch.zeros(3, 5, dtype=dst, device=dev)
+    got2.copy_(row.to(dev))          # the same from a device row
+    same_bits(got2.cpu(), ref)
+    same_bits(row.to(dev).to(dst).cpu(), row.to(dst))  # a device-side cast
 
 
-def test_noncontiguous_source_and_destination():
-    x = torch.randn(4, 6)
-    assert torch.equal(x.t().to(dev).cpu(), x.t())
-    v = x.to(dev).t()
-    assert torch.equal(v.cpu(), x.t())
-    d = torch.zeros(4, 6, device=dev)
-    d.t().copy_(torch.arange(24, dtype=torch.float32).reshape(6, 4))
-    assert torch.equal(d.cpu(), torch.arange(24, dtype=torch.float32).reshape(6, 4).t())
-
-
-def test_view_with_storage_offset_reads_and_writes():
-    x = torch.arange(100, dtype=torch.float32)
-    d = x.to(dev)
-    assert torch.equal(d[10:20].cpu(), x[10:20])
-    d[10:20] = -1.0
-    ref = x.clone()
-    ref[10:20] = -1.0
-    assert torch.equal(d.cpu(), ref)
+def test_writes_through_device_views_land_where_the_cpu_puts_them():
+    host = sample(torch.float32, (8, 12), seed=3)
+    ref, d = host.clone(), host.to(dev)
+    ops = [
+        lambda t: t[2:5].fill_(-1.5),                                       # rows at a storage offset
+        lambda t: t[:, 3].copy_(torch.arange(8, dtype=torch.float32)),      # a strided column, host source
+        lambda t: t.t()[1:4].copy_(sample(torch.float32, (3, 8), seed=4)),  # transposed destination
+        lambda t: t.reshape(-1)[50:70].copy_(torch.linspace(0, 1, 20)),     # flat window
+    ]
+    for op in ops:
+        op(ref)
+        op(d)
+        same_bits(d.cpu(), ref)
 
 
 def test_device_copies_casts_and_fills_run_on_the_device():
@@ -77,26 +119,35 @@ def test_bf16_cast_rounds_to_nearest_even_like_torch():
     assert torch.equal(got16[5:].view(torch.int16), x.to(torch.float16)[5:].view(torch.int16))
 
 
-def test_empty_tensors_do_not_crash():
-    e = torch.empty(0, 3, device=dev)
-    assert e.cpu().shape == (0, 3)
-    assert (e + e).shape == (0, 3)
+def test_empty_tensors_pass_through_transfers_views_and_ops():
+    for shape in [(0,), (0, 3), (4, 0, 2)]:
+        e = torch.empty(shape, device=dev)
+        assert e.cpu().shape == shape and e.numel() == 0
+        assert (e + e).shape == shape and e.to(torch.bfloat16).shape == shape
+        assert torch.zeros(shape).to(dev).clone().cpu().shape == shape
+    assert torch.empty(5, 0, device=dev).t().contiguous().shape == (0, 5)
 
 
-def test_large_tensor_roundtrip_and_memory_is_released():
-    before = torch_vulkan.live_bytes()
-    x = torch.randn(64 << 20)
-    d = x.to(dev)
-    assert torch_vulkan.live_bytes() - before >= x.numel() * 4
-    assert torch.equal(d.cpu(), x)
+def test_a_256_mib_transfer_round_trips_and_its_memory_is_released():
+    base = torch_vulkan.live_bytes()
+    host = sample(torch.float32, (64 << 20,), seed=9)  # 256 MiB
+    d = host.to(dev)
+    assert torch_vulkan.live_bytes() >= base + host.numel() * 4
+    same_bits(d.cpu(), host)
+    same_bits(d[-1000:].cpu(), host[-1000:])  # the far end of the block, through a view
     del d
-    assert torch_vulkan.live_bytes() == before
+    assert torch_vulkan.live_bytes() == base
 
 
-def test_resize_keeps_existing_data():
-    d = torch.arange(10, dtype=torch.float32).to(dev)
-    d.resize_(20)
-    assert torch.equal(d.cpu()[:10], torch.arange(10, dtype=torch.float32))
+def test_resize_keeps_the_data_it_had():
+    host = sample(torch.float32, (10,), seed=5)
+    d = host.to(dev)
+    d.resize_(25)    # grows: the first ten values stay
+    same_bits(d.cpu()[:10], host)
+    d.resize_(4)     # shrinks to a prefix
+    same_bits(d.cpu(), host[:4])
+    d.resize_(3, 2)  # a new shape over the same storage
+    same_bits(d.cpu().reshape(-1)[:4], host[:4])
 
 
 def test_memory_api():

@@ -1,7 +1,12 @@
-"""mm / bmm / addmm / baddbmm on the GPU vs the float64 oracle (reference tests/test_mm.py:1-221) with the
-reference tolerance max|err| <= tol * max(|ref|max, 1) * (1 + 0.01 sqrt(K)), tol = f32 2e-5, bf16 1.2e-2,
-f16 2e-3: odd shapes, transposed and sliced operands read in place, bias broadcast x alpha/beta, batched,
-nn.Linear autograd, matrix-core vs FMA agreement, and the BASELINE shapes (1024^3 + bias, 1024x2048x8192)."""
+"""mm / bmm / addmm / baddbmm on the GPU against the float64 oracle.
+
+The reference's tests/test_mm.py fixes the behaviours (odd shapes, transposed and sliced operands read in
+place, bias broadcast with alpha / beta, batched products, nn.Linear autograd, the matrix-core and FMA
+kernels agreeing) and the tolerance: the largest error at most tol x max(1, largest |reference|) x
+(1 + sqrt(K) / 100) with tol = 2e-5 (float32), 1.2e-2 (bfloat16), 2e-3 (float16).  These tests build each
+operand through one helper (row-major, or stored transposed and read through its .t() view) and add the
+device's own tile paths (direct-to-LDS tiles of every size, split K, narrow and short-K products) and the
+BASELINE shapes (1024^3 + bias, 1024x2048x8192)."""
 
 import os
 
@@ -17,147 +22,152 @@ pytestmark = pytest.mark.gpu
 import torch_vulkan  # noqa: E402
 
 dev = torch.device("vk")
-DTYPES = [torch.float32, torch.bfloat16, torch.float16]
-TOL = {torch.float32: 2e-5, torch.bfloat16: 1.2e-2, torch.float16: 2e-3}
+FLOATS = [torch.float32, torch.bfloat16, torch.float16]
+GEMM_TOL = {torch.float32: 2e-5, torch.bfloat16: 1.2e-2, torch.float16: 2e-3}
 
 
-def check(out, ref64, dtype, k):
-    o = f64(out)
-    assert o.shape == ref64.shape
-    scale = float(np.abs(ref64).max()) + 1e-9
-    err = float(np.abs(o - ref64).max())
-    assert err <= TOL[dtype] * max(scale, 1.0) * (1 + k ** 0.5 * 0.01), f"max err {err} scale {scale}"
+def assert_gemm_close(out, want64, dt, k):
+    """out (a vk tensor) against the float64 product: largest error within GEMM_TOL[dt] x max(1, largest
+    |want|) x (1 + sqrt(k) / 100)."""
+    got = f64(out)
+    assert got.shape == want64.shape, (got.shape, want64.shape)
+    bound = GEMM_TOL[dt] * max(1.0, float(np.abs(want64).max()) if want64.size else 0.0) * (1.0 + np.sqrt(k) / 100.0)
+    err = float(np.abs(got - want64).max()) if got.size else 0.0
+    assert err <= bound, f"largest error {err} > {bound}"
 
 
-def no_fallback(*names):
+def assert_on_device(*names):
     fb = torch_vulkan.fallback_counts()
-    assert not {n: fb[n] for n in names if n in fb}, fb
+    hit = {n: fb[n] for n in names if n in fb}
+    assert not hit, f"ran on the CPU: {hit}"
 
 
-SHAPES = [(1, 1, 1), (7, 5, 3), (64, 16, 64), (65, 17, 63), (128, 129, 300), (33, 1000, 40), (5, 2048, 7),
-          (256, 256, 256), (300, 72, 520), (1, 4096, 16), (1024, 16, 2048)]
+def stored(rows, cols, dt, seed, transposed=False, scale=1.0):
+    """A logical [rows, cols] operand as (CPU values, device tensor): row-major, or with `transposed` stored
+    as [cols, rows] and handed over as its .t() view, which the kernels read in place."""
+    if transposed:
+        host = randn((cols, rows), dt, seed, scale)
+        return host.t(), host.to(dev).t()
+    host = randn((rows, cols), dt, seed, scale)
+    return host, host.to(dev)
 
 
-@pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("m,k,n", SHAPES)
-def test_mm_shapes(dt, m, k, n):
-    a, b = randn((m, k), dt, 1), randn((k, n), dt, 2)
-    out = torch.mm(a.to(dev), b.to(dev))
-    assert out.dtype == dt and out.shape == (m, n)
-    check(out, oracle.gemm(f64(a), f64(b)), dt, k)
-    assert torch_vulkan.kernel_counts().get("aten::mm") == 1
-    no_fallback("aten::mm")
+# (M, K, N): single elements, primes around the tile sizes, long K with few outputs, one row, tall and thin
+PRODUCT_SHAPES = [(1, 1, 1), (3, 7, 2), (64, 32, 64), (63, 31, 65), (127, 255, 129), (40, 1500, 24),
+                  (9, 3000, 5), (256, 256, 256), (520, 72, 300), (1, 2048, 24), (2048, 16, 1024)]
 
 
-@pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("ta", [False, True])
-@pytest.mark.parametrize("tb", [False, True])
-def test_mm_transposed_operands_without_copy(dt, ta, tb):
+@pytest.mark.parametrize("m,k,n", PRODUCT_SHAPES)
+@pytest.mark.parametrize("dt", FLOATS)
+def test_product_shapes(dt, m, k, n):
+    a, A = stored(m, k, dt, 1)
+    b, B = stored(k, n, dt, 2)
+    out = torch.mm(A, B)
+    assert out.dtype == dt and tuple(out.shape) == (m, n)
+    assert_gemm_close(out, oracle.gemm(f64(a), f64(b)), dt, k)
+    assert torch_vulkan.kernel_counts().get("aten::mm") == 1  # one product, one kernel
+    assert_on_device("aten::mm")
+
+
+@pytest.mark.parametrize("lb", ["row-major", "transposed", "window"])
+@pytest.mark.parametrize("la", ["row-major", "transposed", "window"])
+@pytest.mark.parametrize("dt", FLOATS)
+def test_operand_layouts_are_read_in_place(dt, la, lb):
+    """Row-major, transposed and windowed (a sub-block of a larger tensor, at a storage offset) operands:
+    no copy kernel runs before the product."""
     m, k, n = 70, 45, 90
-    a = randn((k, m) if ta else (m, k), dt, 3)
-    b = randn((n, k) if tb else (k, n), dt, 4)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b))
+
+    def make(rows, cols, seed, layout):
+        if layout == "window":
+            host = randn((rows + 6, cols + 9), dt, seed)
+            return host[4:4 + rows, 5:5 + cols], host.to(dev)[4:4 + rows, 5:5 + cols]
+        return stored(rows, cols, dt, seed, layout == "transposed")
+
+    a, A = make(m, k, 3, la)
+    b, B = make(k, n, 4, lb)
     torch_vulkan.reset_fallback_counts()
-    check(torch.mm(A, B), ref, dt, k)
-    assert "aten::clone" not in torch_vulkan.fallback_counts()
-    assert torch_vulkan.kernel_counts().get("aten::copy_", 0) == 0  # operands read in place
-    no_fallback("aten::mm")
+    assert_gemm_close(torch.mm(A, B), oracle.gemm(f64(a), f64(b)), dt, k)
+    kc = torch_vulkan.kernel_counts()
+    assert kc.get("aten::copy_", 0) == 0 and "aten::clone" not in torch_vulkan.fallback_counts(), kc
+    assert_on_device("aten::mm")
 
 
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
 @pytest.mark.parametrize("m,k,n", [(96, 80, 70), (256, 512, 384), (200, 136, 264)])
-def test_mfma_transposes_and_bias(dt, ta, tb, m, k, n):
-    a = randn((k, m) if ta else (m, k), dt, 3)
-    b = randn((n, k) if tb else (k, n), dt, 4)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b))
-    check(torch.mm(A, B), ref, dt, k)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_matrix_core_layouts_with_scaled_bias(dt, ta, tb, m, k, n):
+    a, A = stored(m, k, dt, 3, ta)
+    b, B = stored(k, n, dt, 4, tb)
+    assert_gemm_close(torch.mm(A, B), oracle.gemm(f64(a), f64(b)), dt, k)
     bias = randn((n,), dt, 5)
     out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=2.0)
-    check(out, oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 2.0), dt, k)
+    assert_gemm_close(out, oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 2.0), dt, k)
 
 
-def test_mm_on_sliced_views_with_offset():
-    for dt in DTYPES:
-        a, b = randn((20, 30), dt, 5), randn((30, 25), dt, 6)
-        ad, bd = a.to(dev), b.to(dev)
-        out = torch.mm(ad[3:15, 4:20], bd[4:20, 2:22])
-        check(out, oracle.gemm(f64(a[3:15, 4:20]), f64(b[4:20, 2:22])), dt, 16)
-
-
-@pytest.mark.parametrize("dt", DTYPES)
-def test_bmm(dt):
+@pytest.mark.parametrize("dt", FLOATS)
+def test_batched_products(dt):
+    """bmm with a plain and a column-major right operand, and baddbmm with a bias broadcast over rows."""
     a, b = randn((5, 37, 29), dt, 1), randn((5, 29, 41), dt, 2)
-    ref = oracle.gemm(f64(a), f64(b))
-    check(torch.bmm(a.to(dev), b.to(dev)), ref, dt, 29)
-    out2 = torch.bmm(a.to(dev), b.to(dev).transpose(1, 2).contiguous().transpose(1, 2))
-    check(out2, ref, dt, 29)
-    no_fallback("aten::bmm")
+    want = oracle.gemm(f64(a), f64(b))
+    bd_colmajor = b.to(dev).mT.contiguous().mT  # same values, strides (29 * 41, 1, 29)
+    for B in (b.to(dev), bd_colmajor):
+        assert_gemm_close(torch.bmm(a.to(dev), B), want, dt, 29)
+    p, q, bias = randn((3, 10, 8), dt, 6), randn((3, 8, 12), dt, 7), randn((3, 1, 12), dt, 8)
+    out = torch.baddbmm(bias.to(dev), p.to(dev), q.to(dev), alpha=0.5, beta=1.5)
+    assert_gemm_close(out, oracle.gemm(f64(p), f64(q), f64(bias), 0.5, 1.5), dt, 8)
+    assert_on_device("aten::bmm", "aten::baddbmm")
 
 
-@pytest.mark.parametrize("bias_shape", [(40,), (1, 40), (30, 1), (30, 40), ()])
-@pytest.mark.parametrize("dt", DTYPES)
-def test_addmm_bias_broadcast_alpha_beta(bias_shape, dt):
-    a, b = randn((30, 20), dt, 1), randn((20, 40), dt, 2)
-    bias = randn(bias_shape, dt, 3)
-    for alpha, beta in [(1.0, 1.0), (0.5, 2.0), (2.0, 0.0)]:
+@pytest.mark.parametrize("bias_shape", [(), (40,), (1, 40), (30, 1), (30, 40)])
+@pytest.mark.parametrize("dt", FLOATS)
+def test_addmm_bias_shapes_and_scales(dt, bias_shape):
+    a, b, bias = randn((30, 20), dt, 1), randn((20, 40), dt, 2), randn(bias_shape, dt, 3)
+    for alpha, beta in [(1.0, 1.0), (0.5, 2.0), (2.0, 0.0), (-1.0, 0.25)]:
         out = torch.addmm(bias.to(dev), a.to(dev), b.to(dev), alpha=alpha, beta=beta)
-        ref = oracle.gemm(f64(a), f64(b), f64(bias), alpha, beta)
-        check(out, np.broadcast_to(ref, (30, 40)), dt, 20)
-    no_fallback("aten::addmm")
+        want = np.broadcast_to(oracle.gemm(f64(a), f64(b), f64(bias), alpha, beta), (30, 40))
+        assert_gemm_close(out, want, dt, 20)
+    assert_on_device("aten::addmm")
 
 
-@pytest.mark.parametrize("dt", DTYPES)
-def test_baddbmm(dt):
-    a, b = randn((3, 10, 8), dt, 1), randn((3, 8, 12), dt, 2)
-    bias = randn((3, 1, 12), dt, 3)
-    out = torch.baddbmm(bias.to(dev), a.to(dev), b.to(dev), alpha=0.5, beta=1.5)
-    check(out, oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 1.5), dt, 8)
-    no_fallback("aten::baddbmm")
-
-
-def test_mixed_dtype_and_empty_k_fall_back_correctly():
-    a, b = randn((4, 5), torch.float32), randn((5, 6), torch.bfloat16)
+def test_mismatched_dtypes_raise_and_empty_reductions_give_zeros():
     with pytest.raises(RuntimeError):
-        torch.mm(a.to(dev), b.to(dev))
-    z = torch.mm(torch.zeros(3, 0, device=dev), torch.zeros(0, 4, device=dev))
-    assert torch.equal(z.cpu(), torch.zeros(3, 4))
+        torch.mm(randn((4, 5), torch.float32).to(dev), randn((5, 6), torch.bfloat16).to(dev))
+    for dt in (torch.float32, torch.bfloat16):
+        z = torch.mm(torch.zeros(3, 0, dtype=dt, device=dev), torch.zeros(0, 4, dtype=dt, device=dev))
+        assert torch.equal(z.cpu(), torch.zeros(3, 4, dtype=dt))
+    assert torch.mm(torch.zeros(0, 5, device=dev), torch.zeros(5, 2, device=dev)).shape == (0, 2)
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_linear_forward_backward(dt):
-    torch.manual_seed(0)
-    lin = torch.nn.Linear(48, 32).to(dt)
-    x = randn((2, 10, 48), dt, 5)
-    W, bvec = f64(lin.weight), f64(lin.bias)
-    xd = x.to(dev).requires_grad_(True)
-    lin_d = torch.nn.Linear(48, 32).to(dt)
-    lin_d.load_state_dict(lin.state_dict())
-    lin_d.to(dev)
-    y = lin_d(xd)
-    ref = oracle.gemm(f64(x).reshape(20, 48), W.T, bvec, 1.0, 1.0).reshape(2, 10, 32)
-    check(y, ref, dt, 48)
-    g = randn((2, 10, 32), dt, 6)
-    y.backward(g.to(dev))
-    g2 = f64(g).reshape(20, 32)
-    check(xd.grad, oracle.gemm(g2, W).reshape(2, 10, 48), dt, 32)
-    check(lin_d.weight.grad, oracle.gemm(g2.T, f64(x).reshape(20, 48)), dt, 20)
-    assert "aten::mm" not in torch_vulkan.fallback_counts()
+def test_linear_layer_gradients(dt):
+    """F.linear on [2, 10, 48] tokens with a [32, 48] weight and bias: output, input, weight and bias
+    gradients against float64."""
+    x, w, bias, gy = randn((2, 10, 48), dt, 5), randn((32, 48), dt, 6, 0.15), randn((32,), dt, 7), randn((2, 10, 32), dt, 8)
+    xd, wd, bd = (t.to(dev).requires_grad_(True) for t in (x, w, bias))
+    y = torch.nn.functional.linear(xd, wd, bd)
+    gx, gw, gb = torch.autograd.grad(y, (xd, wd, bd), gy.to(dev))
+    x2, g2 = f64(x).reshape(20, 48), f64(gy).reshape(20, 32)
+    assert_gemm_close(y, oracle.gemm(x2, f64(w).T, f64(bias), 1.0, 1.0).reshape(2, 10, 32), dt, 48)
+    assert_gemm_close(gx, oracle.gemm(g2, f64(w)).reshape(2, 10, 48), dt, 32)
+    assert_gemm_close(gw, oracle.gemm(g2.T, x2), dt, 20)
+    assert np.allclose(f64(gb), g2.sum(0), rtol=GEMM_TOL[dt], atol=GEMM_TOL[dt] * 5)
+    assert_on_device("aten::mm", "aten::addmm")
 
 
-def test_mfma_agrees_with_fma_kernel():
+def test_matrix_core_and_fma_kernels_agree():
+    """The same batched bf16 product with the matrix-core kernels on and off (the FMA path)."""
     a, b = randn((4, 70, 90), torch.bfloat16, 1), randn((4, 90, 50), torch.bfloat16, 2)
-    out_mfma = torch.bmm(a.to(dev), b.to(dev)).cpu().float()
-    torch_vulkan.set_coop_enabled(False)
-    try:
-        out_fma = torch.bmm(a.to(dev), b.to(dev)).cpu().float()
-    finally:
-        torch_vulkan.set_coop_enabled(True)
-    assert torch.allclose(out_mfma, out_fma, rtol=1.5e-2, atol=3e-2), (out_mfma - out_fma).abs().max()
+    results = {}
+    for mfma in (True, False):
+        torch_vulkan.set_coop_enabled(mfma)
+        try:
+            results[mfma] = torch.bmm(a.to(dev), b.to(dev)).cpu().float()
+        finally:
+            torch_vulkan.set_coop_enabled(True)
+    want = oracle.gemm(f64(a), f64(b))
+    for r in results.values():
+        assert_gemm_close(r, want, torch.bfloat16, 90)
+    assert torch.allclose(results[True], results[False], rtol=1.5e-2, atol=3e-2)
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
@@ -166,14 +176,12 @@ def test_mfma_agrees_with_fma_kernel():
 def test_tile_aligned_fast_path_layouts_and_bias(dt, ta, tb, m, k, n):
     """Problems that fill the GPU with 128x256 (first shape) or 256x128 (second) tiles take the
     direct-to-LDS kernel; every operand layout, bias broadcast over rows, alpha and beta."""
-    a = randn((k, m) if ta else (m, k), dt, 13)
-    b = randn((n, k) if tb else (k, n), dt, 14)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, dt, 13, ta)
+    b, B = stored(k, n, dt, 14, tb)
     bias = randn((n,), dt, 15)
     out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=2.0)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 2.0)
-    check(out, ref, dt, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 2.0)
+    assert_gemm_close(out, ref, dt, k)
     assert oracle.rel_l2(f64(out), ref) <= (1e-2 if dt == torch.bfloat16 else 2e-3)
 
 
@@ -183,14 +191,12 @@ def test_small_tile_fast_path_layouts_and_bias(ta, tb, m, k, n):
     """Tile-aligned problems too small for 128 x 256 tiles take the 64 x 64-tile direct-to-LDS kernel (the
     second shape has a K step count that is not a multiple of the three-buffer ring)."""
     dt = torch.bfloat16
-    a = randn((k, m) if ta else (m, k), dt, 23)
-    b = randn((n, k) if tb else (k, n), dt, 24)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, dt, 23, ta)
+    b, B = stored(k, n, dt, 24, tb)
     bias = randn((n,), dt, 25)
     out = torch.addmm(bias.to(dev), A, B, alpha=1.5, beta=0.5)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 1.5, 0.5)
-    check(out, ref, dt, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 1.5, 0.5)
+    assert_gemm_close(out, ref, dt, k)
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
 
 
@@ -200,14 +206,12 @@ def test_large_tile_fast_path_layouts_and_bias(ta, tb, m, k, n):
     """Problems with at least 256 tiles of 256 x 256 take the 256 x 256-tile kernel with a two-buffer ring (odd
     K step counts: the loop's last step runs alone)."""
     dt = torch.bfloat16
-    a = randn((k, m) if ta else (m, k), dt, 33)
-    b = randn((n, k) if tb else (k, n), dt, 34)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, dt, 33, ta)
+    b, B = stored(k, n, dt, 34, tb)
     bias = randn((n,), dt, 35)
     out = torch.addmm(bias.to(dev), A, B, alpha=1.5, beta=0.5)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 1.5, 0.5)
-    check(out, ref, dt, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 1.5, 0.5)
+    assert_gemm_close(out, ref, dt, k)
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
 
 
@@ -229,19 +233,17 @@ SKINNY = [
 def test_skinny_products_split_k(m, k, n, ta, tb, dt):
     """Products one 64-wide tile across split K over fp32 partials and a second, in-order reduction kernel;
     checked against the oracle (with addmm's bias, alpha and beta) and for run-to-run identity."""
-    a = randn((k, m) if ta else (m, k), dt, 41)
-    b = randn((n, k) if tb else (k, n), dt, 42)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, dt, 41, ta)
+    b, B = stored(k, n, dt, 42, tb)
     bias = randn((n,), dt, 43)
     out = torch.addmm(bias.to(dev), A, B, alpha=0.75, beta=1.25)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.75, 1.25)
-    check(out, ref, dt, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 0.75, 1.25)
+    assert_gemm_close(out, ref, dt, k)
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
     out2 = torch.addmm(bias.to(dev), A, B, alpha=0.75, beta=1.25)
     assert torch.equal(out.cpu(), out2.cpu())
     plain = torch.mm(A, B)
-    assert oracle.rel_l2(f64(plain), oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), None, 1.0, 0.0)) <= 1e-2
+    assert oracle.rel_l2(f64(plain), oracle.gemm(f64(a), f64(b), None, 1.0, 0.0)) <= 1e-2
 
 
 def test_tile_aligned_fast_path_batched_and_full_bias():
@@ -250,14 +252,14 @@ def test_tile_aligned_fast_path_batched_and_full_bias():
     bias = randn((bt, m, n), torch.bfloat16, 18)
     out = torch.baddbmm(bias.to(dev), a.to(dev), b.to(dev), alpha=1.5, beta=-1.0)
     ref = np.stack([oracle.gemm(f64(a[i]), f64(b[i]), f64(bias[i]), 1.5, -1.0) for i in range(bt)])
-    check(out, ref, torch.bfloat16, k)
+    assert_gemm_close(out, ref, torch.bfloat16, k)
 
 
 def test_baseline_addmm_1024_cubed_with_bias():
     a, b, bias = randn((1024, 1024), torch.bfloat16, 1), randn((1024, 1024), torch.bfloat16, 2), randn((1024,), torch.bfloat16, 3)
     out = torch.addmm(bias.to(dev), a.to(dev), b.to(dev))
     ref = oracle.gemm(f64(a), f64(b), f64(bias), 1.0, 1.0)
-    check(out, ref, torch.bfloat16, 1024)
+    assert_gemm_close(out, ref, torch.bfloat16, 1024)
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
 
 
@@ -274,7 +276,7 @@ def test_baseline_gemm_1024x2048x8192(layout):
         out = torch.mm(a.to(dev), w.to(dev).t())
         ref = oracle.gemm(f64(a), f64(w).T)
     assert oracle.rel_l2(f64(out), ref) <= 1e-2
-    check(out, ref, torch.bfloat16, K)
+    assert_gemm_close(out, ref, torch.bfloat16, K)
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
@@ -284,18 +286,16 @@ def test_wide_split_k_on_large_tiles(m, k, n, ta, tb, dt):
     """Products whose 128 x 256 tiles alone give fewer than 192 workgroups (the DiT stack's 1024 x 2048
     outputs) split K over the fast kernel's large tiles with fp32 partials (HRT_MM_F32_OUT) and the ordered
     mm_reduce: against the oracle with bias, alpha and beta, and bit-identical run to run."""
-    a = randn((k, m) if ta else (m, k), dt, 51)
-    b = randn((n, k) if tb else (k, n), dt, 52)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, dt, 51, ta)
+    b, B = stored(k, n, dt, 52, tb)
     bias = randn((n,), dt, 53)
     out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.5)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.5)
-    check(out, ref, dt, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 1.5)
+    assert_gemm_close(out, ref, dt, k)
     assert oracle.rel_l2(f64(out), ref) <= (1e-2 if dt == torch.bfloat16 else 4e-3)
     again = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.5)
     assert torch.equal(out.cpu(), again.cpu())
-    no_fallback("aten::addmm")
+    assert_on_device("aten::addmm")
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
@@ -318,10 +318,10 @@ def test_short_k_products(dt, k, m, n, wlayout):
     hd, wd = h.to(dev), w_store.to(dev)
     wd = wd.t() if wlayout == "nk" else wd
     ref = f64(h) @ f64(w)
-    check(hd @ wd, ref, dt, k)
-    check(torch.addmm(bias.to(dev), hd, wd, beta=0.5, alpha=2.0), 0.5 * f64(bias)[None, :] + 2.0 * ref, dt, k)
-    check(torch.addmm(acc0.to(dev), hd, wd), f64(acc0) + ref, dt, k)  # a full [M, N] bias
-    no_fallback("aten::mm", "aten::addmm")
+    assert_gemm_close(hd @ wd, ref, dt, k)
+    assert_gemm_close(torch.addmm(bias.to(dev), hd, wd, beta=0.5, alpha=2.0), 0.5 * f64(bias)[None, :] + 2.0 * ref, dt, k)
+    assert_gemm_close(torch.addmm(acc0.to(dev), hd, wd), f64(acc0) + ref, dt, k)  # a full [M, N] bias
+    assert_on_device("aten::mm", "aten::addmm")
     # accumulating in place (the bias is the output itself), through the C ABI
     from torch_vulkan import abi
     y = acc0.to(dev)
@@ -331,7 +331,7 @@ def test_short_k_products(dt, k, m, n, wlayout):
     a.a_sm, a.a_sk, a.b_sk, a.b_sn, a.c_sm, a.c_sn = hd.stride(0), hd.stride(1), wd.stride(0), wd.stride(1), n, 1
     a.bias_sm, a.bias_sn, a.has_bias, a.alpha, a.beta = n, 1, 1, 1.0, 1.0
     abi.Runtime().dispatch("mm_mfma_" + ("bf16" if dt == torch.bfloat16 else "f16"), a)
-    check(y, f64(acc0) + ref, dt, k)
+    assert_gemm_close(y, f64(acc0) + ref, dt, k)
     if m == 1024 and k == 16:
         assert torch.equal((hd @ wd).cpu(), (hd @ wd).cpu())  # deterministic
 
@@ -370,10 +370,10 @@ def test_narrow_output_products(dt, p, r, q, form):
     m, n = ref.shape
     torch_vulkan.reset_fallback_counts()
     out = A @ B
-    check(out, ref, dt, q)
+    assert_gemm_close(out, ref, dt, q)
     bias = randn((n,), dt, 61)
-    check(torch.addmm(bias.to(dev), A, B, alpha=0.75, beta=1.25), 1.25 * f64(bias)[None, :] + 0.75 * ref, dt, q)
-    no_fallback("aten::mm", "aten::addmm")
+    assert_gemm_close(torch.addmm(bias.to(dev), A, B, alpha=0.75, beta=1.25), 1.25 * f64(bias)[None, :] + 0.75 * ref, dt, q)
+    assert_on_device("aten::mm", "aten::addmm")
     assert torch.equal(out.cpu(), (A @ B).cpu())
     from torch_vulkan import abi
     acc0 = randn((m, n), dt, 62)
@@ -384,7 +384,7 @@ def test_narrow_output_products(dt, p, r, q, form):
     a.a_sm, a.a_sk, a.b_sk, a.b_sn, a.c_sm, a.c_sn = A.stride(0), A.stride(1), B.stride(0), B.stride(1), n, 1
     a.bias_sm, a.bias_sn, a.has_bias, a.alpha, a.beta = n, 1, 1, 1.0, 1.0
     abi.Runtime().dispatch("mm_mfma_" + ("bf16" if dt == torch.bfloat16 else "f16"), a)
-    check(y, f64(acc0) + ref, dt, q)
+    assert_gemm_close(y, f64(acc0) + ref, dt, q)
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 4, 7])
@@ -413,7 +413,7 @@ def test_split_k_reduction_paths_agree(splits, bias_kind):
     ref = 0.5 * ws.double().cpu().sum(0).numpy()
     if bias is not None:
         ref = ref + 1.5 * f64(bias)
-    check(c_vec, ref, torch.bfloat16, splits)
+    assert_gemm_close(c_vec, ref, torch.bfloat16, splits)
 
 
 @pytest.mark.parametrize("ta", [False, True])
@@ -424,14 +424,12 @@ def test_tiles_128x192(m, k, n, ta, tb):
     128 x 256 ones (a DiT block's QKV projection x W^T, N = 6144) take the 128 x 192 tile kernel when B is laid
     out along K (tb: B given as the transposed view of an [N, K] weight), either A layout; B laid out along N
     keeps the 128 x 256 tiles.  Against the oracle, with addmm's bias."""
-    a = randn((k, m) if ta else (m, k), torch.bfloat16, 81)
-    b = randn((n, k) if tb else (k, n), torch.bfloat16, 82, 0.1)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, torch.bfloat16, 81, ta)
+    b, B = stored(k, n, torch.bfloat16, 82, tb, 0.1)
     bias = randn((n,), torch.bfloat16, 83)
     out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.0)
-    check(out, ref, torch.bfloat16, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 1.0)
+    assert_gemm_close(out, ref, torch.bfloat16, k)
     assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
 
 
@@ -443,14 +441,12 @@ def test_tiles_64x128(m, k, n, ta, tb, dt):
     """Products with too few 128 x 256 / 256 x 128 tiles to fill the GPU but several hundred 64 x 128 ones
     (2048^2 outputs) take the 64 x 128 tile kernel (four wavefronts of 32 x 64), every A and B layout, both
     16-bit types; against the oracle, with addmm's bias, and run to run bit-identical."""
-    a = randn((k, m) if ta else (m, k), dt, 91)
-    b = randn((n, k) if tb else (k, n), dt, 92, 0.1)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, dt, 91, ta)
+    b, B = stored(k, n, dt, 92, tb, 0.1)
     bias = randn((n,), dt, 93)
     out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.0)
-    check(out, ref, dt, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 1.0)
+    assert_gemm_close(out, ref, dt, k)
     assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
 
 
@@ -462,14 +458,12 @@ def test_tiles_64x64_long_k_four_buffer_ring(m, k, n, ta, tb, dt):
     """Long reductions on 64 x 64 tiles (K >= 4096, at most 512 workgroups) copy three steps ahead through
     four LDS buffers; 64, 65 and 67 K steps, so the ring's last block is whole, or leaves 1 or 3 steps.
     Every layout, both 16-bit types, against the oracle, run to run bit-identical."""
-    a = randn((k, m) if ta else (m, k), dt, 94)
-    b = randn((n, k) if tb else (k, n), dt, 95, 0.1)
-    A = a.to(dev).t() if ta else a.to(dev)
-    B = b.to(dev).t() if tb else b.to(dev)
+    a, A = stored(m, k, dt, 94, ta)
+    b, B = stored(k, n, dt, 95, tb, 0.1)
     bias = randn((n,), dt, 96)
     out = torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0)
-    ref = oracle.gemm(f64(a.t() if ta else a), f64(b.t() if tb else b), f64(bias), 0.5, 1.0)
-    check(out, ref, dt, k)
+    ref = oracle.gemm(f64(a), f64(b), f64(bias), 0.5, 1.0)
+    assert_gemm_close(out, ref, dt, k)
     assert torch.equal(out.cpu(), torch.addmm(bias.to(dev), A, B, alpha=0.5, beta=1.0).cpu())
 
 

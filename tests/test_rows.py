@@ -1,6 +1,12 @@
-"""softmax / layer_norm on the GPU vs the float64 oracle (reference tests/test_rows.py:1-230, softmax and
-layer_norm parts), with the reference tolerance rule max|err| <= TOL * max(|ref|, 1) * mult, plus the
-BASELINE shapes: softmax fp32 [16384, 1024] and layer_norm bf16 [1024, 2048], forward and backward."""
+"""softmax / layer_norm on the GPU against the float64 oracle.
+
+The reference's tests/test_rows.py (its softmax and layer_norm parts) fixes the behaviours (softmax over any
+dimension, masked and large inputs, views, half inputs with a float32 result, its backward; layer_norm with
+and without affine parameters, over trailing dimensions, float32 statistics, its backward) and the
+tolerance: the largest error at most 3e-5 / 1.2e-2 / 2.5e-3 (float32 / bfloat16 / float16) times
+max(1, largest |reference|), widened per case.  Here the cases are tables run forward and backward
+together, plus _safe_softmax, the BASELINE shapes (softmax fp32 [16384, 1024], layer_norm bf16
+[1024, 2048]) and the layer_norm backward's chunked weight-gradient sums."""
 
 import numpy as np
 import pytest
@@ -15,78 +21,60 @@ pytestmark = pytest.mark.gpu
 import torch_vulkan  # noqa: E402
 
 dev = torch.device("vk")
-DTYPES = [torch.float32, torch.bfloat16, torch.float16]
-TOL = {torch.float32: 3e-5, torch.bfloat16: 1.2e-2, torch.float16: 2.5e-3}
+FLOATS = [torch.float32, torch.bfloat16, torch.float16]
+ROW_TOL = {torch.float32: 3e-5, torch.bfloat16: 1.2e-2, torch.float16: 2.5e-3}
 
 
-def no_fallback(*names):
+def assert_on_device(*names):
     fb = torch_vulkan.fallback_counts()
-    assert not {n: fb[n] for n in names if n in fb}, fb
+    hit = {n: fb[n] for n in names if n in fb}
+    assert not hit, f"ran on the CPU: {hit}"
 
 
 # ---- softmax ----------------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("shape,dim", [((7, 33), -1), ((3, 5, 4), 1), ((3, 5, 4), 0), ((2, 1000), 1), ((4, 5000), -1),
-                                       ((5, 1), -1), ((2, 3, 4, 5), 2), ((3, 4096), -1), ((2, 2048), -1), ((6, 8), -1)])
-def test_softmax_forward(dt, shape, dim):
-    x = randn(shape, dt, scale=3.0)
-    out = torch.softmax(x.to(dev), dim)
-    assert out.dtype == dt
-    max_abs_close(out, oracle.softmax_fwd(f64(x), dim), TOL[dt])
-    no_fallback("aten::_softmax")
+# (shape, dim): last and inner dimensions, a length-1 axis, rows of 1000 / 2048 / 4096 / 5000 elements
+SOFTMAX = [((7, 33), -1), ((3, 5, 4), 1), ((3, 5, 4), 0), ((2, 1000), 1), ((4, 5000), -1), ((5, 1), -1),
+           ((2, 3, 4, 5), 2), ((3, 4096), -1), ((2, 2048), -1), ((6, 8), -1), ((3, 7, 5), 1), ((5, 4, 37), -1)]
+
+
+@pytest.mark.parametrize("shape,dim", SOFTMAX, ids=str)
+@pytest.mark.parametrize("dt", FLOATS)
+def test_softmax_and_its_gradient(dt, shape, dim):
+    x, gy = randn(shape, dt, 0, 3.0), randn(shape, dt, 3)
+    xd = x.to(dev).requires_grad_(True)
+    y = torch.softmax(xd, dim)
+    assert y.dtype == dt
+    max_abs_close(y, oracle.softmax_fwd(f64(x), dim), ROW_TOL[dt])
     assert torch_vulkan.kernel_counts().get("aten::_softmax", 0) == 1
+    (gx,) = torch.autograd.grad(y, xd, gy.to(dev))
+    # the backward from the device's own (rounded) forward output, as the kernel computes it
+    max_abs_close(gx, oracle.softmax_bwd(f64(y), f64(gy), dim), ROW_TOL[dt], mult=2.0)
+    assert_on_device("aten::_softmax", "aten::_softmax_backward_data")
 
 
-def test_softmax_masked_entries_and_large_values():
-    x = randn((4, 40), torch.float32, scale=50.0)
+def test_softmax_of_masked_large_and_strided_inputs():
+    x = randn((4, 40), torch.float32, 0, 50.0)  # large logits: the row maximum is subtracted first
     x[:, 5:12] = float("-inf")
-    out = torch.softmax(x.to(dev), -1)
-    max_abs_close(out, oracle.softmax_fwd(f64(x), -1), TOL[torch.float32])
-    assert torch.all(out.cpu()[:, 5:12] == 0)
-
-
-def test_softmax_non_contiguous_input():
-    x = randn((6, 8, 9), torch.float32)
-    xd = x.to(dev).transpose(0, 2)
-    max_abs_close(torch.softmax(xd, -1), oracle.softmax_fwd(f64(x.transpose(0, 2)), -1), TOL[torch.float32])
-
-
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(5, 4, 37), (3, 1024), (2, 6000)])
-def test_softmax_backward(dt, shape):
-    x = randn(shape, dt, scale=2.0)
-    g = randn(shape, dt, seed=3)
-    xd = x.to(dev).requires_grad_(True)
-    y = torch.softmax(xd, -1)
-    y.backward(g.to(dev))
-    # oracle backward from the device's own (rounded) forward output, as the reference kernel computes it
-    ref = oracle.softmax_bwd(f64(y), f64(g), -1)
-    max_abs_close(xd.grad, ref, TOL[dt], mult=2.0)
-    no_fallback("aten::_softmax_backward_data")
-
-
-def test_softmax_backward_over_inner_dim():
-    x = randn((3, 7, 5), torch.float32)
-    g = randn((3, 7, 5), torch.float32, seed=4)
-    xd = x.to(dev).requires_grad_(True)
-    y = torch.softmax(xd, 1)
-    y.backward(g.to(dev))
-    max_abs_close(xd.grad, oracle.softmax_bwd(f64(y), f64(g), 1), TOL[torch.float32], mult=2.0)
+    y = torch.softmax(x.to(dev), -1)
+    max_abs_close(y, oracle.softmax_fwd(f64(x), -1), ROW_TOL[torch.float32])
+    assert torch.all(y.cpu()[:, 5:12] == 0)
+    z = randn((6, 8, 9), torch.float32, 1)
+    max_abs_close(torch.softmax(z.to(dev).permute(2, 1, 0), -1), oracle.softmax_fwd(f64(z.permute(2, 1, 0)), -1),
+                  ROW_TOL[torch.float32])
 
 
 def test_softmax_half_to_float_and_safe_softmax():
-    x = randn((4, 33), torch.bfloat16, scale=3.0)
-    out = torch.softmax(x.to(dev), -1, dtype=torch.float32)
-    assert out.dtype == torch.float32
-    max_abs_close(out, oracle.softmax_fwd(f64(x), -1), 1e-6)
-    y = randn((4, 33), torch.float32)
-    y[1, :] = float("-inf")
-    y[2, :5] = float("-inf")
-    o = torch._safe_softmax(y.to(dev), -1)
-    ref = oracle.softmax_fwd(f64(y), -1, safe=True)
-    max_abs_close(o, ref, 1e-6)
-    assert torch.equal(o.cpu()[1], torch.zeros(33))
-    no_fallback("aten::_safe_softmax")
+    x = randn((4, 33), torch.bfloat16, 2, 3.0)
+    y = torch.softmax(x.to(dev), -1, dtype=torch.float32)
+    assert y.dtype == torch.float32
+    max_abs_close(y, oracle.softmax_fwd(f64(x), -1), 1e-6)
+    z = randn((4, 33), torch.float32, 3)
+    z[1, :] = float("-inf")  # a fully masked row: zeros instead of NaN
+    z[2, :5] = float("-inf")
+    s = torch._safe_softmax(z.to(dev), -1)
+    max_abs_close(s, oracle.softmax_fwd(f64(z), -1, safe=True), 1e-6)
+    assert torch.equal(s.cpu()[1], torch.zeros(33))
+    assert_on_device("aten::_safe_softmax")
 
 
 def test_softmax_baseline_shape_fp32_16384x1024():
@@ -102,56 +90,65 @@ def test_softmax_baseline_shape_fp32_16384x1024():
 
 
 # ---- layer_norm -------------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("rows,D", [(3, 7), (5, 256), (4, 1000), (2, 2048), (1, 1), (3, 5000), (9, 4096)])
+def ln_operands(rows, D, dt, affine, seed=0):
+    x = randn((rows, D), dt, seed, 2.0)
+    w = randn((D,), dt, seed + 1) if affine else None
+    b = randn((D,), dt, seed + 2) if affine else None
+    return x, w, b
+
+
+def dev_or_none(t, grad=False):
+    return None if t is None else t.to(dev).requires_grad_(grad)
+
+
+def f64_or_none(t):
+    return None if t is None else f64(t)
+
+
 @pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("rows,D", [(3, 7), (5, 256), (4, 1000), (2, 2048), (1, 1), (3, 5000), (9, 4096)])
+@pytest.mark.parametrize("dt", FLOATS)
 def test_layer_norm_forward(dt, rows, D, affine):
-    x = randn((rows, D), dt, scale=2.0)
-    w = randn((D,), dt, 1) if affine else None
-    b = randn((D,), dt, 2) if affine else None
-    out = F.layer_norm(x.to(dev), (D,), None if w is None else w.to(dev), None if b is None else b.to(dev), 1e-5)
-    ref, _, _ = oracle.layer_norm_fwd(f64(x), 1, None if w is None else f64(w), None if b is None else f64(b), 1e-5)
-    max_abs_close(out, ref, TOL[dt], mult=2.0)
-    no_fallback("aten::native_layer_norm")
+    x, w, b = ln_operands(rows, D, dt, affine)
+    y = F.layer_norm(x.to(dev), (D,), dev_or_none(w), dev_or_none(b), 1e-5)
+    want, _, _ = oracle.layer_norm_fwd(f64(x), 1, f64_or_none(w), f64_or_none(b), 1e-5)
+    max_abs_close(y, want, ROW_TOL[dt], mult=2.0)
+    assert_on_device("aten::native_layer_norm")
 
 
-def test_layer_norm_multi_dim_and_5d():
-    x = randn((1, 1, 8, 8, 128), torch.bfloat16, scale=2.0)
-    out = F.layer_norm(x.to(dev), (128,), eps=1e-6)
-    max_abs_close(out, oracle.layer_norm_fwd(f64(x), 1, None, None, 1e-6)[0], TOL[torch.bfloat16], mult=2.0)
-    y = randn((4, 3, 5), torch.float32)
-    max_abs_close(F.layer_norm(y.to(dev), (3, 5)), oracle.layer_norm_fwd(f64(y), 2)[0], TOL[torch.float32])
-    no_fallback("aten::native_layer_norm")
+def test_layer_norm_over_trailing_dimensions_of_higher_rank_inputs():
+    x = randn((1, 1, 8, 8, 128), torch.bfloat16, 4, 2.0)  # the DiT's [B, T, H, W, D] tokens, no affine
+    max_abs_close(F.layer_norm(x.to(dev), (128,), eps=1e-6), oracle.layer_norm_fwd(f64(x), 1, None, None, 1e-6)[0],
+                  ROW_TOL[torch.bfloat16], mult=2.0)
+    z = randn((4, 3, 5), torch.float32, 5)  # normalized over the last two dimensions
+    max_abs_close(F.layer_norm(z.to(dev), (3, 5)), oracle.layer_norm_fwd(f64(z), 2)[0], ROW_TOL[torch.float32])
+    assert_on_device("aten::native_layer_norm")
 
 
-def test_layer_norm_stats_are_fp32_with_reference_shape():
-    x = randn((4, 64), torch.bfloat16).to(dev)
-    out, mean, rstd = torch.native_layer_norm(x, (64,), None, None, 1e-5)
-    assert mean.dtype == torch.float32 and rstd.dtype == torch.float32 and out.dtype == torch.bfloat16
-    assert mean.shape == (4, 1)
+def test_layer_norm_statistics_are_float32_rows():
+    x = randn((4, 64), torch.bfloat16, 6)
+    y, mean, rstd = torch.native_layer_norm(x.to(dev), (64,), None, None, 1e-5)
+    assert (y.dtype, mean.dtype, rstd.dtype) == (torch.bfloat16, torch.float32, torch.float32)
+    assert mean.shape == rstd.shape == (4, 1)
     _, rm, rr = oracle.layer_norm_fwd(f64(x), 1, None, None, 1e-5)
     assert np.allclose(f64(mean), rm, rtol=1e-6, atol=1e-6) and np.allclose(f64(rstd), rr, rtol=1e-5)
 
 
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("affine", [False, True])
 @pytest.mark.parametrize("rows,D", [(6, 96), (10, 2048), (5, 5000), (1030, 2048)])
-def test_layer_norm_backward(dt, affine, rows, D):
-    x = randn((rows, D), dt, scale=2.0)
-    w = randn((D,), dt, 1) if affine else None
-    b = randn((D,), dt, 2) if affine else None
-    g = randn((rows, D), dt, 3)
-    xd = x.to(dev).requires_grad_(True)
-    wd = w.to(dev).requires_grad_(True) if affine else None
-    bd = b.to(dev).requires_grad_(True) if affine else None
-    F.layer_norm(xd, (D,), wd, bd, 1e-5).backward(g.to(dev))
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_layer_norm_gradients(dt, affine, rows, D):
+    x, w, b = ln_operands(rows, D, dt, affine, seed=7)
+    gy = randn((rows, D), dt, 10)
+    xd, wd, bd = x.to(dev).requires_grad_(True), dev_or_none(w, True), dev_or_none(b, True)
+    y = F.layer_norm(xd, (D,), wd, bd, 1e-5)
+    inputs = [xd] + ([wd, bd] if affine else [])
+    got = torch.autograd.grad(y, inputs, gy.to(dev))
     _, mean, rstd = oracle.layer_norm_fwd(f64(x), 1, None, None, 1e-5)
-    dx, dw, db = oracle.layer_norm_bwd(f64(g), f64(x), mean, rstd, 1, None if w is None else f64(w))
-    max_abs_close(xd.grad, dx, TOL[dt], mult=4.0)
-    if affine:
-        max_abs_close(wd.grad, dw, TOL[dt], mult=4.0)
-        max_abs_close(bd.grad, db, TOL[dt], mult=4.0)
-    no_fallback("aten::native_layer_norm_backward")
+    want = oracle.layer_norm_bwd(f64(gy), f64(x), mean, rstd, 1, f64_or_none(w))
+    for g, r in zip(got, want):
+        max_abs_close(g, r, ROW_TOL[dt], mult=4.0)
+    assert_on_device("aten::native_layer_norm_backward")
 
 
 def test_layer_norm_baseline_shape_bf16_1024x2048():

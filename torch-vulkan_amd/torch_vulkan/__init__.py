@@ -245,12 +245,14 @@ def dequant_int8(q, scale, out_dtype=torch.bfloat16):
     function does (torch_vulkan/__init__.py:193-205).
     """
     if q.device.type == "vk":
-        q = q if q.is_contiguous() else q.contiguous()
-        scale = scale if scale.is_contiguous() else scale.contiguous()
-        return _C.dequant_int8(q, scale, out_dtype)
-    cols = q.shape[1]
-    s = scale.float().repeat_interleave(64, dim=1)[:, :cols]
-    return (q.float() * s).to(out_dtype)
+        return _C.dequant_int8(q.contiguous(), scale.contiguous(), out_dtype)
+    # each row padded to whole 64-element blocks, every block times its scale in float32, rounded once
+    rows, cols = q.shape
+    nb = scale.shape[1]
+    blocks = torch.zeros((rows, nb * 64), dtype=torch.float32)
+    blocks[:, :cols] = q.float()
+    prod = blocks.view(rows, nb, 64) * scale.float().unsqueeze(-1)
+    return prod.view(rows, nb * 64)[:, :cols].to(out_dtype)
 
 
 def dequant_int8_linear(x, q, scale, bias=None):
@@ -259,9 +261,7 @@ def dequant_int8_linear(x, q, scale, bias=None):
     The dequantized weight never reaches memory; its values are bit-identical to dequant_int8's."""
     if x.device.type != "vk":
         raise RuntimeError("dequant_int8_linear: x must be a vk tensor")
-    q = q if q.is_contiguous() else q.contiguous()
-    scale = scale if scale.is_contiguous() else scale.contiguous()
-    return _C.dequant_int8_linear(x, q, scale, bias)
+    return _C.dequant_int8_linear(x, q.contiguous(), scale.contiguous(), bias)
 
 
 def event_record(slot: int) -> None:
