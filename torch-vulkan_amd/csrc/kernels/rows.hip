@@ -731,7 +731,16 @@ __global__ __launch_bounds__(512) void ln_wgrad_cols32(const float* __restrict__
       acc += v2;
       acc += v3;
     }
-    for (; c < chunks; c += 64) acc += *reinterpret_cast<const f32x4*>(src + c * stride);
+    if (c < chunks) {  // the last 1-3 chunks of this group: loaded together (indices clamped), added in order
+      const int64_t last = chunks - 1;
+      f32x4 t0 = *reinterpret_cast<const f32x4*>(src + c * stride);
+      f32x4 t1 = *reinterpret_cast<const f32x4*>(src + (c + 64 < last ? c + 64 : last) * stride);
+      f32x4 t2 = *reinterpret_cast<const f32x4*>(src + (c + 128 < last ? c + 128 : last) * stride);
+      asm volatile("" : "+v"(t0), "+v"(t1), "+v"(t2));  // keeps the loads together, ahead of the branches
+      acc += t0;
+      if (c + 64 < chunks) acc += t1;
+      if (c + 128 < chunks) acc += t2;
+    }
   }
   *reinterpret_cast<f32x4*>(sp + grp * 32 + quad * 4) = acc;
   __syncthreads();
