@@ -300,16 +300,31 @@ __global__ __launch_bounds__(256) void red_finish(RedKArgs p) {
   const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (o >= p.n_out) return;
   // split k goes to accumulator k % 8 (8 loads in flight); the accumulators are added in a fixed order
+  // (16 loads issued together per round, and the last round's loads too, with clamped indices: a loop of
+  // 8 loads per iteration waited for each iteration's loads before issuing the next)
   const HK_G float* ws = gcptr<float>(p.ws);
   float a[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   int64_t k = 0;
-  for (; k + 8 <= p.splits; k += 8) {
+  for (; k + 16 <= p.splits; k += 16) {
+    float v[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] += ws[(k + u) * p.n_out + o];
+    for (int u = 0; u < 16; ++u) v[u] = ws[(k + u) * p.n_out + o];
+#pragma unroll
+    for (int u = 0; u < 16; u += 4) asm volatile("" : "+v"(v[u]), "+v"(v[u + 1]), "+v"(v[u + 2]), "+v"(v[u + 3]));
+#pragma unroll
+    for (int u = 0; u < 16; ++u) a[u & 7] += v[u];
   }
+  if (k < p.splits) {
+    const int64_t last = p.splits - 1;
+    float v[16];
 #pragma unroll
-  for (int u = 0; u < 8; ++u)
-    if (k + u < p.splits) a[u] += ws[(k + u) * p.n_out + o];
+    for (int u = 0; u < 16; ++u) v[u] = ws[(k + u < last ? k + u : last) * p.n_out + o];
+#pragma unroll
+    for (int u = 0; u < 16; u += 4) asm volatile("" : "+v"(v[u]), "+v"(v[u + 1]), "+v"(v[u + 2]), "+v"(v[u + 3]));
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (k + u < p.splits) a[u & 7] += v[u];
+  }
   const float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
   store_out(p.out, p.odt, o, s / p.div);
 }
