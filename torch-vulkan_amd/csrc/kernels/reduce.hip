@@ -335,8 +335,28 @@ __global__ __launch_bounds__(256) void red_finish_wide(RedKArgs p) {
   __shared__ float red[4];
   const int64_t o = blockIdx.x;
   const HK_G float* ws = gcptr<float>(p.ws);
+  // thread t adds splits t, t + 256, ... in order, four loads issued together per round (a loop of one
+  // load per iteration made a round trip per split it added)
   float a = 0.0f;
-  for (int64_t k = threadIdx.x; k < p.splits; k += 256) a += ws[k * p.n_out + o];
+  int64_t k = threadIdx.x;
+  for (; k + 768 < p.splits; k += 1024) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = ws[(k + 256 * u) * p.n_out + o];
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a += v[u];
+  }
+  if (k < p.splits) {
+    const int64_t last = p.splits - 1;
+    float v[3];
+#pragma unroll
+    for (int u = 0; u < 3; ++u) v[u] = ws[(k + 256 * u < last ? k + 256 * u : last) * p.n_out + o];
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]));
+    a += v[0];
+    if (k + 256 < p.splits) a += v[1];
+    if (k + 512 < p.splits) a += v[2];
+  }
   a = block_sum<4>(a, red);
   if (threadIdx.x == 0) store_out(p.out, p.odt, o, a / p.div);
 }
